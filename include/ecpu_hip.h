@@ -1,0 +1,187 @@
+/*
+ * libecpu for MI355X (gfx950): the C ABI of piLM's native library, served by
+ * HIP kernels that run on the GPU.
+ *
+ * Every declaration keeps the name, argument order, struct layout and return
+ * codes of the piLM interface it replaces (cited as path:line in the piLM
+ * repository), so src/abi/bindings.py can load this library unchanged through
+ * PILM_ECPU_LIB.  What changes is where the data lives:
+ *
+ *   - Matrix/vector pointers passed to ekernel_* are device (HBM) pointers.
+ *     A pointer that is not device memory, or a buffer that is smaller than
+ *     the shape in the descriptor implies, is rejected with ECPU_ERR_PARAM and
+ *     a message in ecpu_last_error(); nothing is launched.
+ *   - Kernels are enqueued on the library's current stream (the null stream
+ *     unless ecpu_hip_set_stream() chose another) and the call returns without
+ *     waiting.  Work queued on that stream afterwards is ordered after it;
+ *     the device vtable's synchronize() makes results visible to the host.
+ *   - The `isa` argument is accepted and ignored, as in the reference.
+ *
+ * Numerics: the linear kernels reproduce the reference CPU kernels' summation
+ * order exactly (8 fp32 FMA lanes for int8 weights, 2x8 lanes per 16-element
+ * chunk for int4, fresh per-group dots folded with one FMA per group), so
+ * their outputs are bit-identical to the reference for every shape.
+ */
+#ifndef PILM_ECPU_HIP_H
+#define PILM_ECPU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- ecpu_base.h:11-16, 18-26 ------------------------------------------ */
+#define ECPU_OK              0
+#define ECPU_ERR_PARAM     (-1)
+#define ECPU_ERR_MEM       (-2)
+#define ECPU_ERR_DEVICE    (-3)  /* a HIP runtime call failed */
+#define ECPU_ERR_KERNEL    (-4)
+#define ECPU_ERR_UNSUPPORTED (-5)
+
+typedef enum {
+    ECPU_PRECISION_F32 = 0,
+    ECPU_PRECISION_F16 = 1,
+    ECPU_PRECISION_BF16 = 2,
+    ECPU_PRECISION_F8_E4M3 = 3,
+    ECPU_PRECISION_F8_E5M2 = 4,
+    ECPU_PRECISION_I8 = 5,
+    ECPU_PRECISION_I4 = 6,
+} ecpu_precision_t;
+
+/* ---- device/api.h:11-46: device vtable, gains EDEV_HIP ----------------- */
+typedef enum {
+    EDEV_ECPU = 0,   /* host memory (posix_memalign), as in the reference   */
+    EDEV_CUDA = 1,   /* reserved slot kept for enum compatibility; init -1  */
+    EDEV_HIP = 2,    /* MI355X HBM: hipMalloc / hipMemcpy / hipDeviceSynchronize */
+    EDEV_COUNT
+} edevice_t;
+
+typedef enum {
+    EDEV_CAP_NONE = 0,
+    EDEV_CAP_F16 = 1 << 0,
+    EDEV_CAP_BF16 = 1 << 1,
+    EDEV_CAP_FP8 = 1 << 2,
+    EDEV_CAP_INT8_AMX = 1 << 3,
+    EDEV_CAP_AVX512 = 1 << 4,
+    EDEV_CAP_AVX2 = 1 << 5,
+    EDEV_CAP_NEON = 1 << 6,
+    EDEV_CAP_SVE = 1 << 7,
+    EDEV_CAP_NUMA = 1 << 8,
+    EDEV_CAP_UNIFIED_MEM = 1 << 9,
+    EDEV_CAP_MFMA = 1 << 10,     /* new: CDNA matrix cores */
+} edevice_caps_t;
+
+typedef struct edevice_vtable {
+    const char *name;
+    edevice_t id;
+    uint64_t caps;
+    void *(*alloc)(size_t bytes, size_t alignment);
+    void (*free)(void *ptr);
+    void (*memcpy_h2d)(void *dst, const void *src, size_t n);
+    void (*memcpy_d2h)(void *dst, const void *src, size_t n);
+    void (*memcpy_d2d)(void *dst, const void *src, size_t n);
+    int (*synchronize)(void);
+    size_t (*mem_total)(void);
+    size_t (*mem_free)(void);
+    int (*init)(void);
+    int (*shutdown)(void);
+} edevice_vtable_t;
+
+const edevice_vtable_t *edevice_get(edevice_t dev);                       /* device/api.h:41 */
+int edevice_register(edevice_t dev, const edevice_vtable_t *vtable);      /* device/api.h:42 */
+int edevice_set_active(edevice_t dev);                                    /* device/api.h:43 */
+const edevice_vtable_t *edevice_active(void);                             /* device/api.h:44 */
+int edevice_init_all(void);                                               /* device/api.h:45 */
+void edevice_shutdown_all(void);                                          /* device/api.h:46 */
+
+/* ---- ecpu.h:23-39: library lifecycle ----------------------------------- */
+typedef struct {
+    int n_threads;
+    int numa_policy;
+    int disable_amx;
+    int disable_avx512;
+    size_t eram_budget_bytes;
+    size_t kv_cache_budget_bytes;
+    edevice_t device_type;        /* default EDEV_HIP in this library */
+} ecpu_config_t;
+
+ecpu_config_t ecpu_config_default(void);                                  /* ecpu.h:33 */
+int ecpu_init(const ecpu_config_t *config);                               /* ecpu.h:35 */
+void ecpu_shutdown(void);                                                 /* ecpu.h:36 */
+int ecpu_is_initialized(void);                                            /* ecpu.h:37 */
+const char *ecpu_version(void);                                           /* ecpu.h:38 */
+const char *ecpu_last_error(void);                                        /* ecpu.h:39 */
+
+/* ---- kernel/api.h:14-24: ISA enum, gains the GPU target ---------------- */
+typedef enum {
+    EKERNEL_ISA_SCALAR = 0,
+    EKERNEL_ISA_AVX2 = 1,
+    EKERNEL_ISA_AVX512 = 2,
+    EKERNEL_ISA_AMX = 3,
+    EKERNEL_ISA_NEON = 4,
+    EKERNEL_ISA_SVE = 5,
+    EKERNEL_ISA_GFX950 = 6,
+} ekernel_isa_t;
+
+ekernel_isa_t ekernel_detect_isa(void);                                   /* kernel/api.h:23 */
+const char *ekernel_isa_name(ekernel_isa_t isa);                          /* kernel/api.h:24 */
+
+/* ---- kernel/api.h:26-38: f32 GEMM (required by bindings.py:_configure) -- */
+typedef struct {
+    size_t M, N, K;
+    ecpu_precision_t a_prec;
+    ecpu_precision_t b_prec;
+    ecpu_precision_t out_prec;
+    int transpose_a;
+    int transpose_b;
+} ekernel_gemm_desc_t;
+
+int ekernel_gemm(const ekernel_gemm_desc_t *desc, const void *A, const void *B, void *C,
+                 ekernel_isa_t isa);                                      /* kernel/api.h:35-38 */
+
+/* ---- kernel/api.h:40-119: the quantized matrix-product path ------------ */
+typedef struct {
+    size_t M, N, K;
+} ekernel_linear_w8a32_desc_t;
+
+/* C[m,n] = scales[n] * sum_k A[m,k] * W[n,k]; A fp32 [M,K], W int8 [N,K],
+ * scales fp32 [N], C fp32 [M,N].                          kernel/api.h:52-57 */
+int ekernel_linear_w8a32(const ekernel_linear_w8a32_desc_t *desc, const float *A, const int8_t *W,
+                         const float *scales, float *C, ekernel_isa_t isa);
+
+/* As above with bf16 A and bf16 (round-to-nearest-even) C.   kernel/api.h:59-64 */
+int ekernel_linear_w8a16_bf16(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                              const int8_t *W, const float *scales, uint16_t *C, ekernel_isa_t isa);
+
+/* Packed int4 W [N, ceil(K/2)] (low nibble = even k, two's complement),
+ * per-row fp32 scales [N].                                 kernel/api.h:100-105 */
+int ekernel_linear_w4a16_bf16(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                              const uint8_t *W, const float *scales, uint16_t *C, ekernel_isa_t isa);
+
+/* Packed int4 W with fp32 scales [N, ceil(K/32)] / [N, ceil(K/128)].
+ *                                                          kernel/api.h:107-119 */
+int ekernel_linear_w4a16g32_bf16(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                                 const uint8_t *W, const float *scales, uint16_t *C,
+                                 ekernel_isa_t isa);
+int ekernel_linear_w4a16g128_bf16(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                                  const uint8_t *W, const float *scales, uint16_t *C,
+                                  ekernel_isa_t isa);
+
+/* ---- kernel/api.h:195-198: bf16 SwiGLU (required by _configure) -------- */
+int ekernel_swiglu_bf16(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n);
+
+/* ---- additions (no counterpart in the reference) ----------------------- */
+
+/* Choose the HIP stream the ekernel_* entry points enqueue on (NULL = the
+ * null stream).  Callers that run on another stream (e.g. PyTorch's current
+ * stream) set it before calling.  Per process, not per thread. */
+int ecpu_hip_set_stream(void *hip_stream);
+void *ecpu_hip_get_stream(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PILM_ECPU_HIP_H */

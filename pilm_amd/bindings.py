@@ -1,0 +1,293 @@
+"""ctypes bindings to the HIP libecpu (pilm_amd/lib/libecpu.so).
+
+Mirrors src/abi/bindings.py of piLM: the same loader search
+(`PILM_ECPU_LIB` first, bindings.py:28-57), the same required symbols and
+argtypes (`_configure`, bindings.py:59-233), the same ctypes structures
+(bindings.py:235-289) and the same `*_ptr` helpers returning the C rc
+(bindings.py:352-505).  Pointers handed to the linear kernels are device
+(HBM) pointers; the library rejects anything else with ECPU_ERR_PARAM.
+
+There is no CPU fallback: if the library cannot be found or lacks a symbol,
+loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+_lib = None
+_lib_path = None
+
+_REQUIRED_SYMBOLS = [
+    "ecpu_version", "ecpu_last_error", "ecpu_config_default", "ecpu_init", "ecpu_is_initialized",
+    "ecpu_shutdown", "ekernel_detect_isa", "ekernel_isa_name", "edevice_active", "ekernel_gemm",
+    "ekernel_linear_w8a32", "ekernel_linear_w8a16_bf16", "ekernel_swiglu_bf16",
+]
+
+_OPTIONAL_KERNEL_SYMBOLS = [
+    "ekernel_gemm",
+    "ekernel_linear_w8a32",
+    "ekernel_linear_w8a16_bf16",
+    "ekernel_linear_w8a16_bf16_argmax",
+    "ekernel_linear_w8a16_bf16_i8b8",
+    "ekernel_linear_w8a16_bf16_q8",
+    "ekernel_linear_w4a16_bf16",
+    "ekernel_linear_w4a16g32_bf16",
+    "ekernel_linear_w4a16g128_bf16",
+    "ekernel_linear_w4a16_bf16_q8",
+    "ekernel_linear_w4a16_bf16_i4b8",
+    "ekernel_linear_w4a16_bf16_b8",
+    "ekernel_swiglu_bf16",
+    "ekernel_swiglu_w4a16_bf16",
+    "ekernel_rmsnorm_bf16",
+    "ekernel_gated_delta_recurrent_f32",
+]
+
+DEFAULT_LIB = Path(__file__).resolve().parent / "lib" / "libecpu.so"
+
+ECPU_OK = 0
+ECPU_ERR_PARAM = -1
+ECPU_ERR_MEM = -2
+ECPU_ERR_DEVICE = -3
+ECPU_ERR_KERNEL = -4
+ECPU_ERR_UNSUPPORTED = -5
+
+
+def _load_lib():
+    global _lib, _lib_path
+    if _lib is not None:
+        return _lib
+    candidates = []
+    env_lib = os.environ.get("PILM_ECPU_LIB")
+    if env_lib:
+        candidates.append(Path(env_lib))
+    candidates.append(DEFAULT_LIB)
+    for c in candidates:
+        if c.exists():
+            lib = ctypes.CDLL(str(c))
+            _configure(lib)
+            _lib = lib
+            _lib_path = str(c)
+            return _lib
+    raise RuntimeError(
+        f"HIP libecpu not found (looked in {[str(c) for c in candidates]}); "
+        "build it with `python -m pilm_amd.build`")
+
+
+class EcpuConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_threads", ctypes.c_int),
+        ("numa_policy", ctypes.c_int),
+        ("disable_amx", ctypes.c_int),
+        ("disable_avx512", ctypes.c_int),
+        ("eram_budget_bytes", ctypes.c_size_t),
+        ("kv_cache_budget_bytes", ctypes.c_size_t),
+        ("device_type", ctypes.c_int),
+    ]
+
+
+class EdeviceVtable(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("id", ctypes.c_int),
+        ("caps", ctypes.c_uint64),
+        ("alloc", ctypes.c_void_p),
+        ("free", ctypes.c_void_p),
+        ("memcpy_h2d", ctypes.c_void_p),
+        ("memcpy_d2h", ctypes.c_void_p),
+        ("memcpy_d2d", ctypes.c_void_p),
+        ("synchronize", ctypes.c_void_p),
+        ("mem_total", ctypes.c_void_p),
+        ("mem_free", ctypes.c_void_p),
+        ("init", ctypes.c_void_p),
+        ("shutdown", ctypes.c_void_p),
+    ]
+
+
+class EkernelGemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("M", ctypes.c_size_t),
+        ("N", ctypes.c_size_t),
+        ("K", ctypes.c_size_t),
+        ("a_prec", ctypes.c_int),
+        ("b_prec", ctypes.c_int),
+        ("out_prec", ctypes.c_int),
+        ("transpose_a", ctypes.c_int),
+        ("transpose_b", ctypes.c_int),
+    ]
+
+
+class EkernelLinearW8A32Desc(ctypes.Structure):
+    _fields_ = [
+        ("M", ctypes.c_size_t),
+        ("N", ctypes.c_size_t),
+        ("K", ctypes.c_size_t),
+    ]
+
+
+_LINEAR_ARGTYPES = [ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p,
+                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+
+
+def _configure(lib):
+    missing = [s for s in _REQUIRED_SYMBOLS if not hasattr(lib, s)]
+    if missing:
+        raise AttributeError(f"libecpu is missing required symbols: {missing}")
+    lib.ecpu_version.restype = ctypes.c_char_p
+    lib.ecpu_last_error.restype = ctypes.c_char_p
+    lib.ecpu_config_default.restype = EcpuConfig
+    lib.ecpu_init.argtypes = [ctypes.POINTER(EcpuConfig)]
+    lib.ecpu_init.restype = ctypes.c_int
+    lib.ecpu_is_initialized.restype = ctypes.c_int
+    lib.ekernel_detect_isa.restype = ctypes.c_int
+    lib.ekernel_isa_name.argtypes = [ctypes.c_int]
+    lib.ekernel_isa_name.restype = ctypes.c_char_p
+    lib.edevice_active.restype = ctypes.POINTER(EdeviceVtable)
+    lib.ecpu_shutdown.argtypes = []
+    lib.ecpu_shutdown.restype = None
+    lib.ekernel_gemm.argtypes = [ctypes.POINTER(EkernelGemmDesc), ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_int]
+    lib.ekernel_gemm.restype = ctypes.c_int
+    for name in ("ekernel_linear_w8a32", "ekernel_linear_w8a16_bf16", "ekernel_linear_w4a16_bf16",
+                 "ekernel_linear_w4a16g32_bf16", "ekernel_linear_w4a16g128_bf16"):
+        if hasattr(lib, name):
+            fn = getattr(lib, name)
+            fn.argtypes = _LINEAR_ARGTYPES
+            fn.restype = ctypes.c_int
+    lib.ekernel_swiglu_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.ekernel_swiglu_bf16.restype = ctypes.c_int
+    if hasattr(lib, "ecpu_hip_set_stream"):
+        lib.ecpu_hip_set_stream.argtypes = [ctypes.c_void_p]
+        lib.ecpu_hip_set_stream.restype = ctypes.c_int
+        lib.ecpu_hip_get_stream.argtypes = []
+        lib.ecpu_hip_get_stream.restype = ctypes.c_void_p
+
+
+EDEV_ECPU = 0
+EDEV_CUDA = 1
+EDEV_HIP = 2
+
+ECPU_PRECISION_F32 = 0
+ECPU_PRECISION_F16 = 1
+ECPU_PRECISION_BF16 = 2
+ECPU_PRECISION_F8_E4M3 = 3
+ECPU_PRECISION_F8_E5M2 = 4
+ECPU_PRECISION_I8 = 5
+ECPU_PRECISION_I4 = 6
+
+ISA_NAMES = {0: "scalar", 1: "avx2", 2: "avx512", 3: "amx", 4: "neon", 5: "sve", 6: "gfx950"}
+
+
+def init(device_type=EDEV_HIP, n_threads=0, kv_cache_budget=4 * 1024**3):
+    lib = _load_lib()
+    cfg = lib.ecpu_config_default()
+    cfg.device_type = device_type
+    cfg.n_threads = n_threads
+    cfg.kv_cache_budget_bytes = kv_cache_budget
+    rc = lib.ecpu_init(ctypes.byref(cfg))
+    if rc != 0:
+        err = lib.ecpu_last_error()
+        raise RuntimeError(f"ecpu_init failed ({rc}): {err.decode() if err else 'unknown'}")
+    return lib
+
+
+def version():
+    return _load_lib().ecpu_version().decode()
+
+
+def detect_isa():
+    lib = _load_lib()
+    return ISA_NAMES.get(lib.ekernel_detect_isa(), "unknown")
+
+
+def library_path():
+    _load_lib()
+    return _lib_path
+
+
+def last_error() -> str | None:
+    err = _load_lib().ecpu_last_error()
+    return err.decode() if err else None
+
+
+def available_kernel_symbols():
+    lib = _load_lib()
+    return {name: hasattr(lib, name) for name in _OPTIONAL_KERNEL_SYMBOLS}
+
+
+def runtime_info():
+    return {
+        "library_path": library_path(),
+        "version": version(),
+        "isa": detect_isa(),
+        "symbols": available_kernel_symbols(),
+        "env_library_path": os.environ.get("PILM_ECPU_LIB"),
+    }
+
+
+def active_device_info():
+    lib = _load_lib()
+    vt = lib.edevice_active()
+    if not vt:
+        return None
+    name = vt.contents.name.decode() if vt.contents.name else "unknown"
+    return {"name": name, "id": vt.contents.id, "caps": vt.contents.caps}
+
+
+def shutdown():
+    _load_lib().ecpu_shutdown()
+
+
+def set_stream(stream_handle: int) -> None:
+    """Make the library enqueue on this hipStream_t (0 = null stream)."""
+    _load_lib().ecpu_hip_set_stream(ctypes.c_void_p(stream_handle or None))
+
+
+def gemm_f32_ptr(a_ptr: int, b_ptr: int, c_ptr: int, m: int, n: int, k: int,
+                 transpose_a: bool = False, transpose_b: bool = False, isa: int | None = None) -> int:
+    lib = _load_lib()
+    if isa is None:
+        isa = lib.ekernel_detect_isa()
+    desc = EkernelGemmDesc(m, n, k, ECPU_PRECISION_F32, ECPU_PRECISION_F32, ECPU_PRECISION_F32,
+                           int(transpose_a), int(transpose_b))
+    return lib.ekernel_gemm(ctypes.byref(desc), ctypes.c_void_p(a_ptr), ctypes.c_void_p(b_ptr),
+                            ctypes.c_void_p(c_ptr), int(isa))
+
+
+def _linear_ptr(name: str, a_ptr: int, w_ptr: int, scales_ptr: int, c_ptr: int, m: int, n: int, k: int,
+                isa: int | None) -> int:
+    lib = _load_lib()
+    if not hasattr(lib, name):
+        raise RuntimeError(f"loaded eCPU library does not expose {name}")
+    if isa is None:
+        isa = lib.ekernel_detect_isa()
+    desc = EkernelLinearW8A32Desc(m, n, k)
+    return getattr(lib, name)(ctypes.byref(desc), ctypes.c_void_p(a_ptr), ctypes.c_void_p(w_ptr),
+                              ctypes.c_void_p(scales_ptr), ctypes.c_void_p(c_ptr), int(isa))
+
+
+def linear_w8a32_ptr(a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa=None) -> int:
+    return _linear_ptr("ekernel_linear_w8a32", a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa)
+
+
+def linear_w8a16_bf16_ptr(a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa=None) -> int:
+    return _linear_ptr("ekernel_linear_w8a16_bf16", a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa)
+
+
+def linear_w4a16_bf16_ptr(a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa=None) -> int:
+    return _linear_ptr("ekernel_linear_w4a16_bf16", a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa)
+
+
+def linear_w4a16g32_bf16_ptr(a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa=None) -> int:
+    return _linear_ptr("ekernel_linear_w4a16g32_bf16", a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa)
+
+
+def linear_w4a16g128_bf16_ptr(a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa=None) -> int:
+    return _linear_ptr("ekernel_linear_w4a16g128_bf16", a_ptr, w_ptr, scales_ptr, c_ptr, m, n, k, isa)
+
+
+def swiglu_bf16_ptr(gate_ptr: int, up_ptr: int, out_ptr: int, n: int) -> int:
+    lib = _load_lib()
+    return lib.ekernel_swiglu_bf16(ctypes.c_void_p(gate_ptr), ctypes.c_void_p(up_ptr),
+                                   ctypes.c_void_p(out_ptr), ctypes.c_size_t(n))

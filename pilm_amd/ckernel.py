@@ -1,0 +1,314 @@
+"""torch-tensor wrappers around the HIP libecpu, plus the weight quantizers.
+
+Mirrors src/runtime/ckernel.py of piLM: the same function names, argument
+meaning, dtype/ndim/shape rules and error behaviour (ValueError for a bad
+argument, RuntimeError("ekernel_... failed: rc=...") for a nonzero C return
+code).  The difference is residency: kernel inputs must be GPU tensors
+(PyTorch-ROCm reports them as device type "cuda"), outputs are allocated on
+the same device, and work is enqueued on PyTorch's current stream.
+
+The quantizers (ckernel.py:70-161) and the int4 unpack helper (:279-296)
+produce/consume the reference's packed layout and run on whatever device the
+weight lives on.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from . import bindings as abi
+
+_GPU = "cuda"   # PyTorch-ROCm names HIP devices "cuda"
+
+
+def _bind_stream(t: torch.Tensor) -> None:
+    abi.set_stream(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _rc_error(name: str, rc: int) -> RuntimeError:
+    err = abi.last_error()
+    return RuntimeError(f"{name} failed: rc={rc}" + (f" ({err})" if err else ""))
+
+
+def _require_f32_gpu_2d(name: str, tensor: torch.Tensor) -> torch.Tensor:
+    if tensor.device.type != _GPU:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if tensor.dtype != torch.float32:
+        raise ValueError(f"{name} must be torch.float32, got {tensor.dtype}")
+    if tensor.ndim != 2:
+        raise ValueError(f"{name} must be 2D, got shape={tuple(tensor.shape)}")
+    return tensor.contiguous()
+
+
+def _same_device(*ts: torch.Tensor) -> None:
+    devs = {t.device for t in ts}
+    if len(devs) != 1:
+        raise ValueError(f"all tensors must be on one device, got {sorted(map(str, devs))}")
+
+
+# ------------------------------------------------------------------ GEMM
+
+def gemm_f32(a: torch.Tensor, b: torch.Tensor, transpose_b: bool = False) -> torch.Tensor:
+    """ckernel.py:23-46: a[M,K] @ b[K,N] (or b[N,K].T when transpose_b)."""
+    a = _require_f32_gpu_2d("a", a)
+    b = _require_f32_gpu_2d("b", b)
+    _same_device(a, b)
+    m, k = a.shape
+    if transpose_b:
+        n, kb = b.shape
+    else:
+        kb, n = b.shape
+    if kb != k:
+        raise ValueError(f"incompatible GEMM shapes: a={tuple(a.shape)} b={tuple(b.shape)} transpose_b={transpose_b}")
+    out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    _bind_stream(a)
+    rc = abi.gemm_f32_ptr(a.data_ptr(), b.data_ptr(), out.data_ptr(), m, n, k, False, transpose_b)
+    if rc != 0:
+        raise _rc_error("ekernel_gemm", rc)
+    return out
+
+
+def _as_2d(x: torch.Tensor):
+    original_shape: Tuple[int, ...] = tuple(x.shape)
+    if x.ndim == 1:
+        return x.reshape(1, -1), True, original_shape
+    if x.ndim == 2:
+        return x, False, original_shape
+    return x.reshape(-1, x.shape[-1]), False, original_shape
+
+
+def _restore(out: torch.Tensor, squeeze: bool, original_shape) -> torch.Tensor:
+    if squeeze:
+        return out.reshape(-1)
+    if len(original_shape) > 2:
+        return out.reshape(*original_shape[:-1], out.shape[-1])
+    return out
+
+
+def linear_f32(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """ckernel.py:49-67: F32 linear without bias, x @ weight.T."""
+    x2d, squeeze, shape = _as_2d(x)
+    return _restore(gemm_f32(x2d, weight, transpose_b=True), squeeze, shape)
+
+
+# ------------------------------------------------------------ quantizers
+
+def _require_2d(name: str, weight: torch.Tensor) -> None:
+    if weight.ndim != 2:
+        raise ValueError(f"{name} must be 2D, got shape={tuple(weight.shape)}")
+
+
+def quantize_weight_i8_per_row(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """ckernel.py:70-75: scale = max|w|/127 (>= 1e-8), round half-even, clamp +-127."""
+    if weight.dtype != torch.float32:
+        raise ValueError(f"weight must be torch.float32, got {weight.dtype}")
+    _require_2d("weight", weight)
+    weight = weight.contiguous()
+    max_abs = weight.abs().amax(dim=1)
+    scales = torch.clamp(max_abs / 127.0, min=1e-8).to(torch.float32)
+    qweight = torch.round(weight / scales.unsqueeze(1)).clamp(-127, 127).to(torch.int8).contiguous()
+    return qweight, scales.contiguous()
+
+
+def quantize_weight_i8_per_row_chunked(weight: torch.Tensor, rows_per_chunk: int = 1024):
+    """ckernel.py:78-95, chunked over rows (outputs identical to the one-shot form)."""
+    _require_2d("weight", weight)
+    rows, cols = weight.shape
+    rows_per_chunk = max(1, int(rows_per_chunk))
+    qweight = torch.empty((rows, cols), dtype=torch.int8, device=weight.device)
+    scales = torch.empty((rows,), dtype=torch.float32, device=weight.device)
+    for start in range(0, rows, rows_per_chunk):
+        end = min(start + rows_per_chunk, rows)
+        q, s = quantize_weight_i8_per_row(weight[start:end].to(torch.float32))
+        qweight[start:end].copy_(q)
+        scales[start:end].copy_(s)
+    return qweight.contiguous(), scales.contiguous()
+
+
+def _pack_nibbles(q: torch.Tensor) -> torch.Tensor:
+    if q.shape[1] % 2:
+        q = torch.nn.functional.pad(q, (0, 1))
+    low = torch.bitwise_and(q[:, 0::2], 0x0F).to(torch.uint8)
+    high = torch.bitwise_left_shift(torch.bitwise_and(q[:, 1::2], 0x0F), 4).to(torch.uint8)
+    return torch.bitwise_or(low, high)
+
+
+def quantize_weight_i4_per_row_chunked(weight: torch.Tensor, rows_per_chunk: int = 1024):
+    """ckernel.py:98-121: packed int4 [N, ceil(K/2)] (low nibble = even k), fp32 scales [N]."""
+    _require_2d("weight", weight)
+    rows, cols = weight.shape
+    packed_cols = (cols + 1) // 2
+    rows_per_chunk = max(1, int(rows_per_chunk))
+    qweight = torch.empty((rows, packed_cols), dtype=torch.uint8, device=weight.device)
+    scales = torch.empty((rows,), dtype=torch.float32, device=weight.device)
+    for start in range(0, rows, rows_per_chunk):
+        end = min(start + rows_per_chunk, rows)
+        chunk = weight[start:end].to(torch.float32).contiguous()
+        max_abs = chunk.abs().amax(dim=1)
+        chunk_scales = torch.clamp(max_abs / 7.0, min=1e-8).to(torch.float32)
+        q = torch.round(chunk / chunk_scales.unsqueeze(1)).clamp(-7, 7).to(torch.int16)
+        qweight[start:end].copy_(_pack_nibbles(q))
+        scales[start:end].copy_(chunk_scales)
+    return qweight.contiguous(), scales.contiguous()
+
+
+def quantize_weight_i4_grouped_chunked(weight: torch.Tensor, group_size: int = 32, rows_per_chunk: int = 1024):
+    """ckernel.py:124-161: packed int4 with fp32 scales [N, ceil(K/G)]; the last
+    partial group is zero-padded before its max is taken."""
+    if group_size not in {32, 128}:
+        raise ValueError("only group_size=32 or 128 is currently supported by the C kernel")
+    _require_2d("weight", weight)
+    rows, cols = weight.shape
+    packed_cols = (cols + 1) // 2
+    groups = (cols + group_size - 1) // group_size
+    rows_per_chunk = max(1, int(rows_per_chunk))
+    qweight = torch.empty((rows, packed_cols), dtype=torch.uint8, device=weight.device)
+    scales = torch.empty((rows, groups), dtype=torch.float32, device=weight.device)
+    for start in range(0, rows, rows_per_chunk):
+        end = min(start + rows_per_chunk, rows)
+        chunk = weight[start:end].to(torch.float32).contiguous()
+        if cols % group_size:
+            chunk = torch.nn.functional.pad(chunk, (0, groups * group_size - cols))
+        grouped = chunk.reshape(end - start, groups, group_size)
+        max_abs = grouped.abs().amax(dim=2)
+        chunk_scales = torch.clamp(max_abs / 7.0, min=1e-8).to(torch.float32)
+        q = torch.round(grouped / chunk_scales.unsqueeze(2)).clamp(-7, 7).to(torch.int16)
+        q = q.reshape(end - start, groups * group_size)[:, :cols]
+        qweight[start:end].copy_(_pack_nibbles(q))
+        scales[start:end].copy_(chunk_scales)
+    return qweight.contiguous(), scales.contiguous()
+
+
+def unpack_i4_rows_to_i8(qweight: torch.Tensor, in_features: int | None = None) -> torch.Tensor:
+    """ckernel.py:279-296: sign-extend each nibble (v >= 8 -> v - 16)."""
+    if qweight.dtype != torch.uint8 or qweight.ndim != 2:
+        raise ValueError("qweight must be a 2D torch.uint8 tensor")
+    qweight = qweight.contiguous()
+    n, packed_k = qweight.shape
+    k = packed_k * 2 if in_features is None else int(in_features)
+    if k <= 0 or packed_k != (k + 1) // 2:
+        raise ValueError(f"incompatible W4 packed shape: qweight={tuple(qweight.shape)} in_features={in_features}")
+    low = torch.bitwise_and(qweight, 0x0F).to(torch.int16)
+    high = torch.bitwise_and(torch.bitwise_right_shift(qweight, 4), 0x0F).to(torch.int16)
+    low = torch.where(low >= 8, low - 16, low)
+    high = torch.where(high >= 8, high - 16, high)
+    unpacked = torch.empty((n, packed_k * 2), dtype=torch.int8, device=qweight.device)
+    unpacked[:, 0::2].copy_(low.to(torch.int8))
+    unpacked[:, 1::2].copy_(high.to(torch.int8))
+    return unpacked[:, :k].contiguous()
+
+
+# --------------------------------------------------------------- linears
+
+def _check_w8(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, xdtype: torch.dtype, tag: str):
+    if x.device.type != _GPU or x.dtype != xdtype or x.ndim != 2:
+        raise ValueError(f"x must be a 2D GPU {xdtype} tensor")
+    if qweight.device.type != _GPU or qweight.dtype != torch.int8 or qweight.ndim != 2:
+        raise ValueError("qweight must be a 2D GPU torch.int8 tensor")
+    if scales.device.type != _GPU or scales.dtype != torch.float32 or scales.ndim != 1:
+        raise ValueError("scales must be a 1D GPU torch.float32 tensor")
+    _same_device(x, qweight, scales)
+    x, qweight, scales = x.contiguous(), qweight.contiguous(), scales.contiguous()
+    m, k = x.shape
+    n, wk = qweight.shape
+    if wk != k or scales.shape[0] != n:
+        raise ValueError(f"incompatible {tag} shapes: x={tuple(x.shape)} qweight={tuple(qweight.shape)} "
+                         f"scales={tuple(scales.shape)}")
+    return x, qweight, scales, m, n, k
+
+
+def linear_w8a32(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """ckernel.py:164-180: fp32 x [M,K], int8 qweight [N,K], fp32 scales [N] -> fp32 [M,N]."""
+    x, qweight, scales, m, n, k = _check_w8(x, qweight, scales, torch.float32, "W8A32")
+    out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _bind_stream(x)
+    rc = abi.linear_w8a32_ptr(x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), out.data_ptr(), m, n, k)
+    if rc != 0:
+        raise _rc_error("ekernel_linear_w8a32", rc)
+    return out
+
+
+def linear_w8a16_bf16(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """ckernel.py:183-201: bf16 x, int8 qweight, fp32 scales -> bf16 [M,N]."""
+    x, qweight, scales, m, n, k = _check_w8(x, qweight, scales, torch.bfloat16, "W8A16")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _bind_stream(x)
+    rc = abi.linear_w8a16_bf16_ptr(x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), out.data_ptr(), m, n, k)
+    if rc != 0:
+        raise _rc_error("ekernel_linear_w8a16_bf16", rc)
+    return out
+
+
+def _check_w4(x, qweight, scales, in_features, scale_ndim: int):
+    if x.device.type != _GPU or x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise ValueError("x must be a 2D GPU torch.bfloat16 tensor")
+    if qweight.device.type != _GPU or qweight.dtype != torch.uint8 or qweight.ndim != 2:
+        raise ValueError("qweight must be a 2D GPU torch.uint8 tensor")
+    if scales.device.type != _GPU or scales.dtype != torch.float32 or scales.ndim != scale_ndim:
+        raise ValueError(f"scales must be a {scale_ndim}D GPU torch.float32 tensor")
+    _same_device(x, qweight, scales)
+    x, qweight, scales = x.contiguous(), qweight.contiguous(), scales.contiguous()
+    m, k = x.shape
+    n, packed_k = qweight.shape
+    if in_features is not None and int(in_features) != k:
+        raise ValueError(f"in_features={in_features} does not match x K={k}")
+    return x, qweight, scales, m, n, k, packed_k
+
+
+def linear_w4a16_bf16(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+                      in_features: int | None = None) -> torch.Tensor:
+    """ckernel.py:465-486: packed int4 with per-row fp32 scales [N]."""
+    x, qweight, scales, m, n, k, packed_k = _check_w4(x, qweight, scales, in_features, 1)
+    if packed_k != (k + 1) // 2 or scales.shape[0] != n:
+        raise ValueError(f"incompatible W4A16 shapes: x={tuple(x.shape)} qweight={tuple(qweight.shape)} "
+                         f"scales={tuple(scales.shape)}")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _bind_stream(x)
+    rc = abi.linear_w4a16_bf16_ptr(x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), out.data_ptr(), m, n, k)
+    if rc != 0:
+        raise _rc_error("ekernel_linear_w4a16_bf16", rc)
+    return out
+
+
+def _linear_w4g(x, qweight, scales, in_features, group: int):
+    x, qweight, scales, m, n, k, packed_k = _check_w4(x, qweight, scales, in_features, 2)
+    groups = (k + group - 1) // group
+    if packed_k != (k + 1) // 2 or tuple(scales.shape) != (n, groups):
+        raise ValueError(f"incompatible W4A16G{group} shapes: x={tuple(x.shape)} qweight={tuple(qweight.shape)} "
+                         f"scales={tuple(scales.shape)}")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _bind_stream(x)
+    fn = abi.linear_w4a16g128_bf16_ptr if group == 128 else abi.linear_w4a16g32_bf16_ptr
+    rc = fn(x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), out.data_ptr(), m, n, k)
+    if rc != 0:
+        raise _rc_error(f"ekernel_linear_w4a16g{group}_bf16", rc)
+    return out
+
+
+def linear_w4a16g32_bf16(x, qweight, scales, in_features=None) -> torch.Tensor:
+    """ckernel.py:521-542: packed int4 with fp32 scales [N, ceil(K/32)]."""
+    return _linear_w4g(x, qweight, scales, in_features, 32)
+
+
+def linear_w4a16g128_bf16(x, qweight, scales, in_features=None) -> torch.Tensor:
+    """ckernel.py:545-566: packed int4 with fp32 scales [N, ceil(K/128)]."""
+    return _linear_w4g(x, qweight, scales, in_features, 128)
+
+
+def swiglu_bf16(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """ckernel.py:569-583: bf16(silu(gate) * up)."""
+    if gate.device.type != _GPU or up.device.type != _GPU:
+        raise ValueError("gate and up must be GPU tensors")
+    if gate.dtype != torch.bfloat16 or up.dtype != torch.bfloat16:
+        raise ValueError("gate and up must be torch.bfloat16")
+    if tuple(gate.shape) != tuple(up.shape):
+        raise ValueError(f"gate/up shapes differ: gate={tuple(gate.shape)} up={tuple(up.shape)}")
+    _same_device(gate, up)
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    _bind_stream(gate)
+    rc = abi.swiglu_bf16_ptr(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel())
+    if rc != 0:
+        raise _rc_error("ekernel_swiglu_bf16", rc)
+    return out

@@ -1,0 +1,474 @@
+// Exact quantized GEMV / small-M GEMM for gfx950.
+//
+// "Exact" means bit-identical to the reference CPU kernels: every output is
+// produced by the same sequence of fp32 roundings as in
+//   src/ecpu/src/kernel/kernels.c:78-109, 330-393   (int8: 8 FMA lanes, lane l
+//        owns k = l mod 8, hsum ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)), FMA tail)
+//   src/ecpu/src/kernel/kernels.c:111-225           (int4: lanes lo[l] take
+//        k = 16c+l, hi[l] take 16c+8+l, hsum(lo+hi), FMA tail in pairs)
+//   src/ecpu/src/kernel/kernels.c:1089-1139         (groups: fresh int4 dot per
+//        group, acc = fma(block, scale[g], acc) in group order)
+// followed by the reference's final multiply / bf16 rounding.  An FMA chain
+// cannot be split without changing its roundings, so the parallelism is laid
+// out around the chains rather than across them:
+//
+//   * one lane owns one output row (all of that row's chains live in its
+//     registers); a wave covers 64 consecutive rows;
+//   * the wave streams its 64 rows in 64-byte "stripes": four coalesced
+//     16-byte loads per lane fetch 64 rows x 64 B, an XOR-swizzled LDS round
+//     trip hands every lane its own row's 64 B (conflict-free on 64 banks);
+//   * activations are the same for all lanes of a wave (same k), so they
+//     arrive through scalar loads and feed v_fma_mix_f32 / v_fma_f32 as SGPR
+//     operands;
+//   * int4 nibbles become exact fp16 values with one and-or against the 1024
+//     exponent pattern plus one packed fp16 add (or fma) per nibble pair;
+//     v_fma_mix_f32 then performs fma(a, w, acc) with w widened exactly;
+//   * group-scaled formats may split K across waves: each wave then stores
+//     its per-group block sums and a small second kernel folds them with the
+//     scales in group order (the only serial part of the group formula).
+//
+// Shapes the stripe loop cannot take (K not a multiple of the stripe,
+// unaligned pointers) run a one-thread-per-output kernel that follows the
+// reference loops literally, tails included.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "internal.h"
+
+namespace pilm {
+
+enum Fmt : int { F_W8A32 = 0, F_W8A16 = 1, F_W4ROW = 2, F_W4G128 = 3, F_W4G32 = 4 };
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Shape and launch geometry; the buffers travel as separate __restrict__
+// kernel arguments so the compiler can prove the activations are never
+// written and fetch them with scalar loads.
+struct GemvArgs {
+    const void *A;
+    const uint8_t *W;
+    const float *S;
+    void *C;
+    float *P;                // per-group partial sums when K is split
+    int M, N, K;
+    int row_bytes;           // bytes per weight row
+    int nstripes;            // 64-byte stripes per row (fast path)
+    int sps;                 // stripes per split
+    int nsplit;
+    int ntiles;              // ceil(N / 64)
+    int G;                   // scale groups per row (group formats)
+};
+
+// Activations are read through the constant address space: the address is the
+// same for every lane of a wave, so each load becomes one s_load and the
+// bf16 -> fp32 shifts run on the scalar unit.  The buffer is never written by
+// these kernels (the scalar cache is not coherent with vector stores).
+typedef __attribute__((address_space(4))) const uint32_t cu32;
+typedef __attribute__((address_space(4))) const float cf32;
+__device__ __forceinline__ const cu32 *as_const(const void *p) { return (const cu32 *)(uintptr_t)p; }
+
+__device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xFFFF0000u); }
+
+// kernels.c:19-25 (no NaN special case, like the reference).
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    uint32_t b = __float_as_uint(x);
+    b += 0x7FFFu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+// kernels.c:56-63
+__device__ __forceinline__ float hsum8(const float l[8]) {
+    return ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
+}
+
+// Eight nibbles (k = 0..7 of this dword, low nibble first) as exact fp16:
+//   q[0] = (w0, w4)  q[1] = (w1, w5)  q[2] = (w2, w6)  q[3] = (w3, w7)
+// XOR 0x8 turns the two's-complement nibble v into u = v + 8; 0x6400|u is the
+// fp16 value 1024 + u, and 0x6400|(u << 4) is 1024 + 16u.  Subtracting 1032,
+// or scaling by 1/16 and subtracting 72, yields v exactly.
+// `magic` must hold 0x64006400; callers pass it through an opaque register so
+// the compiler emits one v_and_or_b32 per nibble pair (mask in an SGPR,
+// magic in a VGPR) instead of an and followed by an or with a literal.
+__device__ __forceinline__ void dequant_w4(uint32_t x, uint32_t magic, h2 q[4]) {
+    const uint32_t u = x ^ 0x88888888u;
+    const uint32_t v = u >> 8;
+    const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const h2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2 bias16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    q[0] = __builtin_bit_cast(h2, (u & 0x000F000Fu) | magic) + bias;
+    q[1] = __builtin_bit_cast(h2, (u & 0x00F000F0u) | magic) * sixteenth + bias16;
+    q[2] = __builtin_bit_cast(h2, (v & 0x000F000Fu) | magic) + bias;
+    q[3] = __builtin_bit_cast(h2, (v & 0x00F000F0u) | magic) * sixteenth + bias16;
+}
+
+__device__ __forceinline__ uint32_t opaque_magic() {
+    uint32_t m = 0x64006400u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
+__device__ __forceinline__ uint32_t word_of(const u32x4 (&r)[4], int d) { return r[d >> 2][d & 3]; }
+
+// One 16-element chunk of the int4 dot for MT activation rows: lo lanes get
+// k0..k0+7 (dword xl), hi lanes get k0+8..k0+15 (dword xh).
+template <int MT>
+__device__ __forceinline__ void w4_chunk(uint32_t xl, uint32_t xh, const cu32 *a32,
+                                         int K, int k0, float (&lo)[MT][8], float (&hi)[MT][8]) {
+    h2 ql[4], qh[4];
+    const uint32_t magic = opaque_magic();
+    dequant_w4(xl, magic, ql);
+    dequant_w4(xh, magic, qh);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const cu32 *a = a32 + ((size_t)m * K + k0) / 2;
+        const uint32_t a0 = a[0], a1 = a[1], a2 = a[2], a3 = a[3];
+        const uint32_t a4 = a[4], a5 = a[5], a6 = a[6], a7 = a[7];
+        lo[m][0] = __builtin_fmaf(bf16_lo(a0), (float)ql[0].x, lo[m][0]);
+        lo[m][1] = __builtin_fmaf(bf16_hi(a0), (float)ql[1].x, lo[m][1]);
+        lo[m][2] = __builtin_fmaf(bf16_lo(a1), (float)ql[2].x, lo[m][2]);
+        lo[m][3] = __builtin_fmaf(bf16_hi(a1), (float)ql[3].x, lo[m][3]);
+        lo[m][4] = __builtin_fmaf(bf16_lo(a2), (float)ql[0].y, lo[m][4]);
+        lo[m][5] = __builtin_fmaf(bf16_hi(a2), (float)ql[1].y, lo[m][5]);
+        lo[m][6] = __builtin_fmaf(bf16_lo(a3), (float)ql[2].y, lo[m][6]);
+        lo[m][7] = __builtin_fmaf(bf16_hi(a3), (float)ql[3].y, lo[m][7]);
+        hi[m][0] = __builtin_fmaf(bf16_lo(a4), (float)qh[0].x, hi[m][0]);
+        hi[m][1] = __builtin_fmaf(bf16_hi(a4), (float)qh[1].x, hi[m][1]);
+        hi[m][2] = __builtin_fmaf(bf16_lo(a5), (float)qh[2].x, hi[m][2]);
+        hi[m][3] = __builtin_fmaf(bf16_hi(a5), (float)qh[3].x, hi[m][3]);
+        hi[m][4] = __builtin_fmaf(bf16_lo(a6), (float)qh[0].y, hi[m][4]);
+        hi[m][5] = __builtin_fmaf(bf16_hi(a6), (float)qh[1].y, hi[m][5]);
+        hi[m][6] = __builtin_fmaf(bf16_lo(a7), (float)qh[2].y, hi[m][6]);
+        hi[m][7] = __builtin_fmaf(bf16_hi(a7), (float)qh[3].y, hi[m][7]);
+    }
+}
+
+__device__ __forceinline__ float w4_block_and_reset(float (&lo)[8], float (&hi)[8]) {
+    float s[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        s[l] = lo[l] + hi[l];
+        lo[l] = 0.0f;
+        hi[l] = 0.0f;
+    }
+    return hsum8(s);
+}
+
+// Stripe-streaming exact kernel.  Block = 4 independent waves; wave task =
+// (64-row tile, K split).  MT activation rows starting at m0 per launch.
+template <int FMT, int MT>
+__global__ __launch_bounds__(256) void gemv_exact_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W_,
+                                                         const float *__restrict__ S_, void *__restrict__ C_,
+                                                         float *__restrict__ P_, GemvArgs p, int m0) {
+    p.A = A_;
+    p.W = W_;
+    p.S = S_;
+    p.C = C_;
+    p.P = P_;
+    __shared__ u32x4 lds[4][64 * 4];
+    // threadIdx.x >> 6 is the same for all lanes of a wave; readfirstlane
+    // tells the compiler so, which keeps the task indices in SGPRs.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int task = blockIdx.x * 4 + wave;
+    if (task >= p.ntiles * p.nsplit) return;   // uniform per wave
+    const int tile = task / p.nsplit;
+    const int split = task - tile * p.nsplit;
+    const int row0 = tile * 64;
+    const int n = row0 + lane;
+    const int nc = n < p.N ? n : p.N - 1;
+    const int s0 = split * p.sps;
+    const int s1 = min(s0 + p.sps, p.nstripes);
+
+    // Loader: instruction i fetches rows row0+16i .. +15, four lanes per row.
+    const int lq = lane & 3, lr = lane >> 2;
+    const uint8_t *src[4];
+    int wslot[4], rslot[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 16 * i + lr;
+        const int rc = min(row0 + r, p.N - 1);
+        src[i] = p.W + (size_t)rc * p.row_bytes + lq * 16;
+        wslot[i] = r * 4 + (lq ^ ((r >> 2) & 3));
+        rslot[i] = lane * 4 + (i ^ ((lane >> 2) & 3));
+    }
+    u32x4 *L = lds[wave];
+
+    u32x4 pre[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pre[i] = *(const u32x4 *)(src[i] + (size_t)s0 * 64);
+
+    constexpr bool kW8 = (FMT == F_W8A32 || FMT == F_W8A16);
+    // int8: lo[m][l] are the 8 lanes.  int4: lo/hi are the two 8-lane halves.
+    float lo[MT][8], hi[MT][8], gacc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        gacc[m] = 0.0f;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) lo[m][l] = hi[m][l] = 0.0f;
+    }
+    const size_t K = (size_t)p.K;
+
+    for (int s = s0; s < s1; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) L[wslot[i]] = pre[i];
+        if (s + 1 < s1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pre[i] = *(const u32x4 *)(src[i] + (size_t)(s + 1) * 64);
+        }
+        u32x4 mine[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[i] = L[rslot[i]];
+
+        if constexpr (kW8) {
+            // 64 int8 weights: k = 64s + 4d + j belongs to lane 4(d&1) + j.
+            const size_t kb = (size_t)s * 64;
+#pragma unroll
+            for (int d = 0; d < 16; ++d) {
+                const uint32_t x = word_of(mine, d);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float w = (float)(int)(int8_t)(uint8_t)(x >> (8 * j));
+                    const int l = 4 * (d & 1) + j;
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const size_t k = (size_t)(m0 + m) * K + kb + 4 * d + j;
+                        float a;
+                        if constexpr (FMT == F_W8A32) {
+                            a = ((const cf32 *)as_const(p.A))[k];
+                        } else {
+                            const uint32_t pr = as_const(p.A)[k >> 1];
+                            a = (j & 1) ? bf16_hi(pr) : bf16_lo(pr);
+                        }
+                        lo[m][l] = __builtin_fmaf(a, w, lo[m][l]);
+                    }
+                }
+            }
+        } else {
+            const cu32 *a32 = as_const(p.A) + ((size_t)m0 * K) / 2;
+            const int kb = s * 128;
+            constexpr int kChunksPerGroup = (FMT == F_W4G32) ? 2 : 8;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                w4_chunk<MT>(word_of(mine, 2 * c), word_of(mine, 2 * c + 1), a32, p.K, kb + 16 * c, lo, hi);
+                if constexpr (FMT == F_W4G128 || FMT == F_W4G32) {
+                    if ((c + 1) % kChunksPerGroup == 0) {
+                        const int g = (FMT == F_W4G128) ? s : 4 * s + c / 2;
+                        const float sc = p.S[(size_t)nc * p.G + g];
+#pragma unroll
+                        for (int m = 0; m < MT; ++m) {
+                            const float block = w4_block_and_reset(lo[m], hi[m]);
+                            if (p.nsplit == 1) {
+                                gacc[m] = __builtin_fmaf(block, sc, gacc[m]);
+                            } else if (n < p.N) {
+                                p.P[((size_t)g * p.M + m0 + m) * p.N + n] = block;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if (n >= p.N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const size_t o = (size_t)(m0 + m) * p.N + n;
+        if constexpr (FMT == F_W8A32) {
+            ((float *)p.C)[o] = hsum8(lo[m]) * p.S[n];
+        } else if constexpr (FMT == F_W8A16) {
+            ((uint16_t *)p.C)[o] = f32_to_bf16(hsum8(lo[m]) * p.S[n]);
+        } else if constexpr (FMT == F_W4ROW) {
+            ((uint16_t *)p.C)[o] = f32_to_bf16(w4_block_and_reset(lo[m], hi[m]) * p.S[n]);
+        } else {
+            if (p.nsplit == 1) ((uint16_t *)p.C)[o] = f32_to_bf16(gacc[m]);
+        }
+    }
+}
+
+// Folds per-group block sums with the scales in group order (kernels.c:1135).
+__global__ __launch_bounds__(256) void group_fold_kernel(const float *__restrict__ P, const float *__restrict__ S,
+                                                         uint16_t *__restrict__ C, int M, int N, int G) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)M * N) return;
+    const int m = (int)(idx / N), n = (int)(idx % N);
+    float acc = 0.0f;
+    for (int g = 0; g < G; ++g) acc = __builtin_fmaf(P[((size_t)g * M + m) * N + n], S[(size_t)n * G + g], acc);
+    C[idx] = f32_to_bf16(acc);
+}
+
+// ----------------------------------------------------- literal fallback
+__device__ __forceinline__ float nib(const uint8_t *w, size_t k) {
+    const uint8_t b = w[k >> 1];
+    const int v = (k & 1) ? (b >> 4) : (b & 0x0F);
+    return (float)(v >= 8 ? v - 16 : v);
+}
+
+__device__ __forceinline__ float bf16_at(const uint16_t *a, size_t k) { return __uint_as_float((uint32_t)a[k] << 16); }
+
+__device__ float dot_i4_literal(const uint16_t *a, const uint8_t *w, size_t K) {
+    float lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t k = 0;
+    for (; k + 16 <= K; k += 16) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            lo[l] = __builtin_fmaf(bf16_at(a, k + l), nib(w, k + l), lo[l]);
+            hi[l] = __builtin_fmaf(bf16_at(a, k + 8 + l), nib(w, k + 8 + l), hi[l]);
+        }
+    }
+    float s[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s[l] = lo[l] + hi[l];
+    float out = hsum8(s);
+    for (; k + 1 < K; k += 2) {
+        out = __builtin_fmaf(bf16_at(a, k), nib(w, k), out);
+        out = __builtin_fmaf(bf16_at(a, k + 1), nib(w, k + 1), out);
+    }
+    if (k < K) out = __builtin_fmaf(bf16_at(a, k), nib(w, k), out);
+    return out;
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void gemv_literal_kernel(GemvArgs p, int group_size) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)p.M * p.N) return;
+    const size_t m = idx / p.N, n = idx % p.N;
+    const size_t K = (size_t)p.K;
+    if constexpr (FMT == F_W8A32 || FMT == F_W8A16) {
+        const int8_t *w = (const int8_t *)p.W + n * K;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        size_t k = 0;
+        for (; k + 8 <= K; k += 8) {
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const float a = (FMT == F_W8A32) ? ((const float *)p.A)[m * K + k + l]
+                                                 : bf16_at((const uint16_t *)p.A, m * K + k + l);
+                acc[l] = __builtin_fmaf(a, (float)w[k + l], acc[l]);
+            }
+        }
+        float out = hsum8(acc);
+        for (; k < K; ++k) {
+            const float a = (FMT == F_W8A32) ? ((const float *)p.A)[m * K + k]
+                                             : bf16_at((const uint16_t *)p.A, m * K + k);
+            out = __builtin_fmaf(a, (float)w[k], out);
+        }
+        if constexpr (FMT == F_W8A32)
+            ((float *)p.C)[idx] = out * p.S[n];
+        else
+            ((uint16_t *)p.C)[idx] = f32_to_bf16(out * p.S[n]);
+    } else {
+        const uint16_t *a = (const uint16_t *)p.A + m * K;
+        const uint8_t *w = p.W + n * (size_t)p.row_bytes;
+        if constexpr (FMT == F_W4ROW) {
+            ((uint16_t *)p.C)[idx] = f32_to_bf16(dot_i4_literal(a, w, K) * p.S[n]);
+        } else {
+            const size_t G = (K + group_size - 1) / group_size;
+            float acc = 0.0f;
+            for (size_t g = 0; g < G; ++g) {
+                const size_t k0 = g * group_size;
+                const size_t gk = K - k0 < (size_t)group_size ? K - k0 : (size_t)group_size;
+                acc = __builtin_fmaf(dot_i4_literal(a + k0, w + k0 / 2, gk), p.S[n * G + g], acc);
+            }
+            ((uint16_t *)p.C)[idx] = f32_to_bf16(acc);
+        }
+    }
+}
+
+// --------------------------------------------------------------- launch
+
+template <int FMT>
+static void launch_exact_mt(int mt, dim3 grid, hipStream_t st, const GemvArgs &a, int m0) {
+    switch (mt) {
+        case 1: gemv_exact_kernel<FMT, 1><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
+        case 2: gemv_exact_kernel<FMT, 2><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
+        case 3: gemv_exact_kernel<FMT, 3><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
+        default: gemv_exact_kernel<FMT, 4><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
+    }
+}
+
+static void launch_exact(int fmt, int mt, dim3 grid, hipStream_t st, const GemvArgs &a, int m0) {
+    switch (fmt) {
+        case F_W8A32: launch_exact_mt<F_W8A32>(mt, grid, st, a, m0); break;
+        case F_W8A16: launch_exact_mt<F_W8A16>(mt, grid, st, a, m0); break;
+        case F_W4ROW: launch_exact_mt<F_W4ROW>(mt, grid, st, a, m0); break;
+        case F_W4G128: launch_exact_mt<F_W4G128>(mt, grid, st, a, m0); break;
+        default: launch_exact_mt<F_W4G32>(mt, grid, st, a, m0); break;
+    }
+}
+
+static int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+// Entry point shared by the five linear formats; arguments are validated by
+// the caller (shapes, device residency, buffer extents).
+int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S,
+               void *C, const char *fn) {
+    if (M == 0 || N == 0) return ECPU_OK;
+    hipStream_t st = current_stream();
+    const bool w8 = (fmt == F_W8A32 || fmt == F_W8A16);
+    const int group = (fmt == F_W4G128) ? 128 : (fmt == F_W4G32 ? 32 : 0);
+    GemvArgs a;
+    a.A = A;
+    a.W = W;
+    a.S = S;
+    a.C = C;
+    a.P = nullptr;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.row_bytes = (int)(w8 ? K : (K + 1) / 2);
+    a.G = group ? (int)((K + group - 1) / group) : 0;
+    a.ntiles = (int)((N + 63) / 64);
+    a.nsplit = 1;
+
+    const size_t stripe_k = w8 ? 64 : 128;
+    const bool aligned = (((uintptr_t)W | (uintptr_t)A) & 15) == 0;
+    const bool fast = K > 0 && K % stripe_k == 0 && aligned && env_int("PILM_HIP_LITERAL", 0) == 0;
+    if (!fast) {
+        const size_t total = M * N;
+        switch (fmt) {
+            case F_W8A32: gemv_literal_kernel<F_W8A32><<<(total + 255) / 256, 256, 0, st>>>(a, 0); break;
+            case F_W8A16: gemv_literal_kernel<F_W8A16><<<(total + 255) / 256, 256, 0, st>>>(a, 0); break;
+            case F_W4ROW: gemv_literal_kernel<F_W4ROW><<<(total + 255) / 256, 256, 0, st>>>(a, 0); break;
+            case F_W4G128: gemv_literal_kernel<F_W4G128><<<(total + 255) / 256, 256, 0, st>>>(a, 128); break;
+            default: gemv_literal_kernel<F_W4G32><<<(total + 255) / 256, 256, 0, st>>>(a, 32); break;
+        }
+        return check_launch(fn);
+    }
+
+    a.nstripes = (int)(K / stripe_k);
+    if (group) {
+        // Split K across waves when the row tiles alone cannot fill the GPU.
+        const int target = env_int("PILM_HIP_SPLIT_TARGET", 2048);
+        int nsplit = env_int("PILM_HIP_NSPLIT", 0);
+        if (nsplit <= 0) nsplit = std::max(1, std::min(a.nstripes, (target + a.ntiles - 1) / a.ntiles));
+        nsplit = std::min(nsplit, a.nstripes);
+        a.sps = (a.nstripes + nsplit - 1) / nsplit;
+        a.nsplit = (a.nstripes + a.sps - 1) / a.sps;
+    } else {
+        a.sps = a.nstripes;
+    }
+    if (a.nsplit > 1) {
+        int rc = ECPU_OK;
+        a.P = scratch_floats((size_t)a.G * M * N, &rc, fn);
+        if (!a.P) return rc;
+    }
+    const int tasks = a.ntiles * a.nsplit;
+    const dim3 grid((tasks + 3) / 4);
+    for (size_t m0 = 0; m0 < M; m0 += 4) {
+        const int mt = (int)std::min<size_t>(4, M - m0);
+        launch_exact(fmt, mt, grid, st, a, (int)m0);
+    }
+    if (a.nsplit > 1) {
+        const size_t total = M * N;
+        group_fold_kernel<<<(total + 255) / 256, 256, 0, st>>>(a.P, S, (uint16_t *)C, (int)M, (int)N, a.G);
+    }
+    return check_launch(fn);
+}
+
+}  // namespace pilm

@@ -1,0 +1,185 @@
+"""GPU parity of the HIP quantized linears against the golden vectors and the oracle.
+
+Every comparison is bit-exact: the HIP kernels follow the reference's
+summation order, so int8/int4 results must match the reference CPU kernels
+byte for byte (fp32 outputs and bf16 outputs alike).  Calls go through the
+C ABI (pilm_amd.ckernel -> ctypes -> libecpu.so), as piLM's Python does.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from pilm_amd import bindings as abi
+from pilm_amd import synth as S
+from tests import _golden as GV
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from pilm_amd import ckernel as ck  # noqa: E402
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(a: np.ndarray, dev, bf16: bool = False):
+    if bf16:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev).view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def from_dev(t) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def run_gpu(fmt: str, x, w, s, dev, in_features=None):
+    if fmt == "w8a32":
+        return from_dev(ck.linear_w8a32(to_dev(x, dev), to_dev(w, dev), to_dev(s, dev)))
+    xb = to_dev(x, dev, bf16=True)
+    if fmt == "w8a16":
+        return from_dev(ck.linear_w8a16_bf16(xb, to_dev(w, dev), to_dev(s, dev)))
+    if fmt == "w4":
+        return from_dev(ck.linear_w4a16_bf16(xb, to_dev(w, dev), to_dev(s, dev), in_features))
+    fn = ck.linear_w4a16g32_bf16 if fmt == "w4g32" else ck.linear_w4a16g128_bf16
+    return from_dev(fn(xb, to_dev(w, dev), to_dev(s, dev), in_features))
+
+
+@pytest.mark.parametrize("case", GV.linear_cases(), ids=lambda c: c["name"])
+def test_golden(case, dev):
+    _say(f"[gpu] golden {case['name']}")
+    y = run_gpu(case["fmt"], *GV.inputs(case), dev)
+    GV.check_output(case, y)
+
+
+@pytest.mark.parametrize("nsplit", ["1", "2", "3", "16"])
+def test_group_split_variants_identical(nsplit, dev, monkeypatch):
+    """Splitting K across waves must not change a single bit."""
+    monkeypatch.setenv("PILM_HIP_NSPLIT", nsplit)
+    for case in GV.linear_cases(prefix="config2_w4g128_M1"):
+        if case["N"] > 20000:
+            continue
+        _say(f"[gpu] nsplit={nsplit} {case['name']}")
+        GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
+    for case in GV.linear_cases(prefix="w4g32_cancel"):
+        GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
+
+
+def test_literal_path_identical(dev, monkeypatch):
+    """The one-thread-per-output kernel gives the same bits on stripe-aligned shapes."""
+    monkeypatch.setenv("PILM_HIP_LITERAL", "1")
+    for case in GV.linear_cases(max_elems=1 << 22):
+        if case["K"] % 128:
+            continue
+        _say(f"[gpu] literal {case['name']}")
+        GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
+
+
+@pytest.mark.parametrize("fmt", ["w8a32", "w8a16", "w4", "w4g32", "w4g128"])
+def test_fresh_shapes_against_oracle(fmt, dev):
+    from oracle import oracle as O
+    gen = GV._gen()
+    rng = np.random.default_rng(2024)
+    for trial in range(12):
+        m = int(rng.choice([1, 2, 4, 5, 7, 16, 33]))
+        n = int(rng.integers(1, 700))
+        k = int(rng.choice([128, 256, 640, 1024, 2048, 4096, 96, 130, 1001]))
+        _say(f"[gpu] oracle {fmt} M={m} N={n} K={k}")
+        x, w, s = gen.make_inputs(fmt, m, n, k, 777 + trial)
+        y = run_gpu(fmt, x, w, s, dev)
+        ref = gen.run(fmt, x, w, s, "oracle")
+        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n, k)
+
+
+def test_power_of_two_scale_full_size(dev):
+    """Size-independent property at the lm_head shape: doubling the scales doubles every output."""
+    n, k = 151936, 2048
+    _say("[gpu] lm_head scale-doubling")
+    x = to_dev(S.activations_bf16(11, 1, k), dev, bf16=True)
+    w = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev)
+    s = torch.rand((n, k // 128), device=dev) * 0.019 + 0.001
+    y1 = ck.linear_w4a16g128_bf16(x, w, s).float()
+    y2 = ck.linear_w4a16g128_bf16(x, w, s * 2).float()
+    assert torch.equal(y2, y1 * 2)
+
+
+def test_side_stream(dev):
+    case = GV.linear_cases(prefix="config2_w4g128_M4_N4096")[0]
+    x, w, s = GV.inputs(case)
+    st = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(st):
+        xd, wd, sd = to_dev(x, dev, bf16=True), to_dev(w, dev), to_dev(s, dev)
+        y = ck.linear_w4a16g128_bf16(xd, wd, sd)
+        out = from_dev(y)
+    GV.check_output(case, out)
+
+
+# ------------------------------------------------------------------ errors
+
+def test_host_pointer_rejected(dev):
+    x = np.zeros((1, 256), np.float32)
+    w = np.zeros((8, 256), np.int8)
+    s = np.ones(8, np.float32)
+    c = np.zeros((1, 8), np.float32)
+    rc = abi.linear_w8a32_ptr(x.ctypes.data, w.ctypes.data, s.ctypes.data, c.ctypes.data, 1, 8, 256)
+    assert rc == abi.ECPU_ERR_PARAM
+    assert "not device memory" in abi.last_error()
+
+
+def test_null_rejected(dev):
+    w = torch.zeros((8, 256), dtype=torch.int8, device=dev)
+    rc = abi.linear_w8a32_ptr(0, w.data_ptr(), w.data_ptr(), w.data_ptr(), 1, 8, 256)
+    assert rc == abi.ECPU_ERR_PARAM
+
+
+def test_undersized_buffer_rejected(dev):
+    lib = abi._load_lib()
+    vt = lib.edevice_active()
+    assert vt.contents.id == abi.EDEV_HIP
+    alloc = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t)(vt.contents.alloc)
+    free = ctypes.CFUNCTYPE(None, ctypes.c_void_p)(vt.contents.free)
+    small = alloc(1 << 20, 256)
+    big = alloc(64 << 20, 256)
+    try:
+        # W needs N*K = 2048*1024 bytes but only 1 MiB is allocated
+        rc = abi.linear_w8a16_bf16_ptr(big, small, big, big, 1, 2048, 1024)
+        assert rc == abi.ECPU_ERR_PARAM
+        assert "allocation ends" in abi.last_error()
+        rc = abi.linear_w8a16_bf16_ptr(big, big + (1 << 20), big + (4 << 20), big + (8 << 20), 1, 2048, 1024)
+        assert rc == abi.ECPU_OK
+        torch.cuda.synchronize()
+    finally:
+        free(small)
+        free(big)
+
+
+def test_wrapper_rejects_cpu_tensors(dev):
+    x = torch.zeros((1, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ck.linear_w4a16g128_bf16(x, torch.zeros((4, 64), dtype=torch.uint8, device=dev),
+                                 torch.ones((4, 1), device=dev))
+
+
+def test_gemm_and_swiglu(dev):
+    rng = np.random.default_rng(5)
+    a = rng.integers(-4, 5, size=(7, 33)).astype(np.float32)
+    b = rng.integers(-4, 5, size=(9, 33)).astype(np.float32)
+    out = ck.gemm_f32(to_dev(a, dev), to_dev(b, dev), transpose_b=True).cpu().numpy()
+    assert np.array_equal(out, a @ b.T)
+    out2 = ck.gemm_f32(to_dev(a, dev), to_dev(b.T.copy(), dev)).cpu().numpy()
+    assert np.array_equal(out2, a @ b.T)
+    g = rng.standard_normal(4096).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    gb, ub = S.f32_to_bf16_bits(g), S.f32_to_bf16_bits(u)
+    y = S.bf16_bits_to_f32(from_dev(ck.swiglu_bf16(to_dev(gb, dev, True), to_dev(ub, dev, True))))
+    gf, uf = S.bf16_bits_to_f32(gb).astype(np.float64), S.bf16_bits_to_f32(ub).astype(np.float64)
+    ref = gf / (1 + np.exp(-gf)) * uf
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-30)
