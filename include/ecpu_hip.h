@@ -180,6 +180,16 @@ int ekernel_swiglu_bf16(const uint16_t *gate, const uint16_t *up, uint16_t *out,
 int ecpu_hip_set_stream(void *hip_stream);
 void *ecpu_hip_get_stream(void);
 
+/* Per-call GPU timing of the linear entry points, the native counterpart of
+ * the per-linear stage profiler in src/models/base/linear.py:148-169.
+ * Between begin and end every linear call records a HIP event pair on its
+ * stream around its kernels.  read() waits for those events and writes one
+ * line per kernel family: "<family> <calls> <total_ms> <alg_bytes> <flops>",
+ * where alg_bytes counts weights + scales + activations + outputs once. */
+int ecpu_hip_profile_begin(void);
+int ecpu_hip_profile_end(void);
+int ecpu_hip_profile_read(char *buf, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

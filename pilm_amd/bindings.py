@@ -157,6 +157,11 @@ def _configure(lib):
             fn.restype = ctypes.c_int
     lib.ekernel_swiglu_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
     lib.ekernel_swiglu_bf16.restype = ctypes.c_int
+    if hasattr(lib, "ecpu_hip_profile_read"):
+        lib.ecpu_hip_profile_begin.restype = ctypes.c_int
+        lib.ecpu_hip_profile_end.restype = ctypes.c_int
+        lib.ecpu_hip_profile_read.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+        lib.ecpu_hip_profile_read.restype = ctypes.c_int
     if hasattr(lib, "ecpu_hip_set_stream"):
         lib.ecpu_hip_set_stream.argtypes = [ctypes.c_void_p]
         lib.ecpu_hip_set_stream.restype = ctypes.c_int
@@ -242,6 +247,29 @@ def shutdown():
 def set_stream(stream_handle: int) -> None:
     """Make the library enqueue on this hipStream_t (0 = null stream)."""
     _load_lib().ecpu_hip_set_stream(ctypes.c_void_p(stream_handle or None))
+
+
+def profile_begin() -> None:
+    """Start recording a HIP event pair around every linear call."""
+    _load_lib().ecpu_hip_profile_begin()
+
+
+def profile_end() -> None:
+    _load_lib().ecpu_hip_profile_end()
+
+
+def profile_read() -> dict:
+    """{family: {"calls", "ms", "bytes", "flops"}} for the calls recorded so far."""
+    lib = _load_lib()
+    buf = ctypes.create_string_buffer(1 << 16)
+    rc = lib.ecpu_hip_profile_read(buf, len(buf))
+    if rc != 0:
+        raise RuntimeError(f"ecpu_hip_profile_read failed: rc={rc} ({last_error()})")
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, calls, ms, nbytes, flops = line.split()
+        out[name] = {"calls": int(calls), "ms": float(ms), "bytes": float(nbytes), "flops": float(flops)}
+    return out
 
 
 def gemm_f32_ptr(a_ptr: int, b_ptr: int, c_ptr: int, m: int, n: int, k: int,

@@ -24,8 +24,12 @@ int check_device_buffer(const void *ptr, size_t bytes, const char *what, const c
 // ECPU_OK after a launch, ECPU_ERR_DEVICE with the HIP error text otherwise.
 int check_launch(const char *fn);
 
-// Per-device scratch the GEMV split path uses for partial sums (grown on
-// demand, kept until ecpu_shutdown / process exit).
-float *scratch_floats(size_t n, int *rc, const char *fn);
+// Scratch for the K-split GEMV path, one set per device: `nfloat`
+// floats of per-group block sums and `nticket` ints of per-tile tickets that
+// are zero whenever no kernel is running.  Grown on demand with hipMalloc;
+// an outgrown set is retired, not freed, until ecpu_shutdown(), so a HIP
+// graph that captured it stays valid.  Calls that overlap in time on one
+// device (different streams) must not both take the split path.
+int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, int **T, const char *fn);
 
 }  // namespace pilm

@@ -34,6 +34,11 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
 
 #include "internal.h"
 
@@ -52,7 +57,8 @@ struct GemvArgs {
     const uint8_t *W;
     const float *S;
     void *C;
-    float *P;                // per-group partial sums when K is split
+    float *P;                // per-group block sums when K is split
+    int *T;                  // per-tile tickets (zero between launches)
     int M, N, K;
     int row_bytes;           // bytes per weight row
     int nstripes;            // 64-byte stripes per row (fast path)
@@ -115,34 +121,34 @@ __device__ __forceinline__ uint32_t word_of(const u32x4 (&r)[4], int d) { return
 
 // One 16-element chunk of the int4 dot for MT activation rows: lo lanes get
 // k0..k0+7 (dword xl), hi lanes get k0+8..k0+15 (dword xh).
-template <int MT>
-__device__ __forceinline__ void w4_chunk(uint32_t xl, uint32_t xh, const cu32 *a32,
-                                         int K, int k0, float (&lo)[MT][8], float (&hi)[MT][8]) {
+// One 16-element chunk of the int4 dot for MT activation rows: lo lanes get
+// k0..k0+7 (dword xl), hi lanes get k0+8..k0+15 (dword xh).  act[m][0..7]
+// hold the chunk's 16 bf16 activations of row m as 8 dwords.
+template <int MT, int STRIDE>
+__device__ __forceinline__ void w4_chunk(uint32_t xl, uint32_t xh, const uint32_t *act, uint32_t magic,
+                                         float (&lo)[MT][8], float (&hi)[MT][8]) {
     h2 ql[4], qh[4];
-    const uint32_t magic = opaque_magic();
     dequant_w4(xl, magic, ql);
     dequant_w4(xh, magic, qh);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        const cu32 *a = a32 + ((size_t)m * K + k0) / 2;
-        const uint32_t a0 = a[0], a1 = a[1], a2 = a[2], a3 = a[3];
-        const uint32_t a4 = a[4], a5 = a[5], a6 = a[6], a7 = a[7];
-        lo[m][0] = __builtin_fmaf(bf16_lo(a0), (float)ql[0].x, lo[m][0]);
-        lo[m][1] = __builtin_fmaf(bf16_hi(a0), (float)ql[1].x, lo[m][1]);
-        lo[m][2] = __builtin_fmaf(bf16_lo(a1), (float)ql[2].x, lo[m][2]);
-        lo[m][3] = __builtin_fmaf(bf16_hi(a1), (float)ql[3].x, lo[m][3]);
-        lo[m][4] = __builtin_fmaf(bf16_lo(a2), (float)ql[0].y, lo[m][4]);
-        lo[m][5] = __builtin_fmaf(bf16_hi(a2), (float)ql[1].y, lo[m][5]);
-        lo[m][6] = __builtin_fmaf(bf16_lo(a3), (float)ql[2].y, lo[m][6]);
-        lo[m][7] = __builtin_fmaf(bf16_hi(a3), (float)ql[3].y, lo[m][7]);
-        hi[m][0] = __builtin_fmaf(bf16_lo(a4), (float)qh[0].x, hi[m][0]);
-        hi[m][1] = __builtin_fmaf(bf16_hi(a4), (float)qh[1].x, hi[m][1]);
-        hi[m][2] = __builtin_fmaf(bf16_lo(a5), (float)qh[2].x, hi[m][2]);
-        hi[m][3] = __builtin_fmaf(bf16_hi(a5), (float)qh[3].x, hi[m][3]);
-        hi[m][4] = __builtin_fmaf(bf16_lo(a6), (float)qh[0].y, hi[m][4]);
-        hi[m][5] = __builtin_fmaf(bf16_hi(a6), (float)qh[1].y, hi[m][5]);
-        hi[m][6] = __builtin_fmaf(bf16_lo(a7), (float)qh[2].y, hi[m][6]);
-        hi[m][7] = __builtin_fmaf(bf16_hi(a7), (float)qh[3].y, hi[m][7]);
+        const uint32_t *a = act + m * STRIDE;
+        lo[m][0] = __builtin_fmaf(bf16_lo(a[0]), (float)ql[0].x, lo[m][0]);
+        lo[m][1] = __builtin_fmaf(bf16_hi(a[0]), (float)ql[1].x, lo[m][1]);
+        lo[m][2] = __builtin_fmaf(bf16_lo(a[1]), (float)ql[2].x, lo[m][2]);
+        lo[m][3] = __builtin_fmaf(bf16_hi(a[1]), (float)ql[3].x, lo[m][3]);
+        lo[m][4] = __builtin_fmaf(bf16_lo(a[2]), (float)ql[0].y, lo[m][4]);
+        lo[m][5] = __builtin_fmaf(bf16_hi(a[2]), (float)ql[1].y, lo[m][5]);
+        lo[m][6] = __builtin_fmaf(bf16_lo(a[3]), (float)ql[2].y, lo[m][6]);
+        lo[m][7] = __builtin_fmaf(bf16_hi(a[3]), (float)ql[3].y, lo[m][7]);
+        hi[m][0] = __builtin_fmaf(bf16_lo(a[4]), (float)qh[0].x, hi[m][0]);
+        hi[m][1] = __builtin_fmaf(bf16_hi(a[4]), (float)qh[1].x, hi[m][1]);
+        hi[m][2] = __builtin_fmaf(bf16_lo(a[5]), (float)qh[2].x, hi[m][2]);
+        hi[m][3] = __builtin_fmaf(bf16_hi(a[5]), (float)qh[3].x, hi[m][3]);
+        hi[m][4] = __builtin_fmaf(bf16_lo(a[6]), (float)qh[0].y, hi[m][4]);
+        hi[m][5] = __builtin_fmaf(bf16_hi(a[6]), (float)qh[1].y, hi[m][5]);
+        hi[m][6] = __builtin_fmaf(bf16_lo(a[7]), (float)qh[2].y, hi[m][6]);
+        hi[m][7] = __builtin_fmaf(bf16_hi(a[7]), (float)qh[3].y, hi[m][7]);
     }
 }
 
@@ -159,21 +165,92 @@ __device__ __forceinline__ float w4_block_and_reset(float (&lo)[8], float (&hi)[
 
 // Stripe-streaming exact kernel.  Block = 4 independent waves; wave task =
 // (64-row tile, K split).  MT activation rows starting at m0 per launch.
+// Wait until at most VM vector-memory operations of this wave are in flight.
+// A wave's vector memory operations complete in issue order, so this
+// guarantees that everything issued before the last VM operations is done.
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((VM & 0xF) | (0x7 << 4) | (0xF << 8) | ((VM >> 4) << 14));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kStripe = 128;        // bytes of each row per stripe: one full cache line
+constexpr int kLoads = 8;           // 16-byte DMA loads per lane per stripe (64 rows x 128 B)
+constexpr int kWaves = 4;           // independent waves per block
+constexpr int kNT = 2;              // cache policy of the weight stream: non-temporal
+
+template <int FMT>
+struct StripeFmt {
+    static constexpr bool w8 = (FMT == F_W8A32 || FMT == F_W8A16);
+    static constexpr bool group = (FMT == F_W4G128 || FMT == F_W4G32);
+    static constexpr int k_per_stripe = w8 ? kStripe : 2 * kStripe;               // 128 or 256
+    static constexpr int groups_per_stripe = FMT == F_W4G128 ? 2 : (FMT == F_W4G32 ? 8 : 0);
+    static constexpr int scale_words = FMT == F_W4G32 ? 8 : (FMT == F_W4G128 ? 2 : 1);
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Issues the DMA loads of stripe `st` into the wave's LDS slot: kLoads
+// 16-byte weight loads per lane (non-temporal), plus the lane's group scales
+// for the stripe when the wave folds the groups itself (two 4-byte loads for
+// g128, two 16-byte loads for g32; each lands lane-linear in scale_slot).
+template <int FMT>
+__device__ __forceinline__ void issue_stripe(const uint8_t *const (&src)[kLoads], const float *ssrc, int st,
+                                             bool scale_dma, u32x4 *slot, float *scale_slot) {
+    using F = StripeFmt<FMT>;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
+        __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)st * kStripe), (lds_void *)(slot + 64 * i), 16,
+                                         0, kNT);
+    if constexpr (F::group) {
+        if (scale_dma) {
+            // (the DMA size is a literal in each branch: the host compilation
+            // pass rejects target-dependent sizes of this builtin)
+            const float *sp = ssrc + (size_t)st * F::groups_per_stripe;
+            if constexpr (FMT == F_W4G32) {
+                __builtin_amdgcn_global_load_lds((const void *)sp, (lds_void *)scale_slot, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)(sp + 4), (lds_void *)(scale_slot + 256), 16, 0, 0);
+            } else {
+                __builtin_amdgcn_global_load_lds((const void *)sp, (lds_void *)scale_slot, 4, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)(sp + 1), (lds_void *)(scale_slot + 64), 4, 0, 0);
+            }
+        }
+    }
+}
+
+// Stripe-streaming exact kernel.  Block = kWaves independent waves; a wave
+// task = (64-row tile, K split).  MT activation rows starting at m0.
+//
+// Each wave streams its 64 rows in stripes of 64 rows x 128 B through one
+// 8 KB LDS slot filled by global_load_lds_dwordx4 (global -> LDS without
+// VGPRs, non-temporal): the wave waits for stripe s, copies it to registers,
+// refills the slot with stripe s + 1 and computes stripe s meanwhile.
+// Lane t of DMA instruction i fetches row 8i + t/8, 16-byte chunk
+// (t & 7) ^ ((row >> 1) & 7): the eight lanes of a row cover its full line,
+// and the data lands XOR-swizzled so that lane r reading its own row is
+// free of LDS bank conflicts.
 template <int FMT, int MT>
-__global__ __launch_bounds__(256) void gemv_exact_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W_,
-                                                         const float *__restrict__ S_, void *__restrict__ C_,
-                                                         float *__restrict__ P_, GemvArgs p, int m0) {
+__global__ __launch_bounds__(64 * kWaves) void gemv_exact_kernel(const void *__restrict__ A_,
+                                                               const uint8_t *__restrict__ W_,
+                                                               const float *__restrict__ S_, void *__restrict__ C_,
+                                                               float *__restrict__ P_, int *__restrict__ T_,
+                                                               GemvArgs p, int m0) {
     p.A = A_;
     p.W = W_;
     p.S = S_;
     p.C = C_;
     p.P = P_;
-    __shared__ u32x4 lds[4][64 * 4];
+    p.T = T_;
+    using F = StripeFmt<FMT>;
+    __shared__ u32x4 slot[kWaves][64 * kLoads];
+    __shared__ float scale_slot[F::group ? kWaves : 1][64 * F::scale_words];
     // threadIdx.x >> 6 is the same for all lanes of a wave; readfirstlane
     // tells the compiler so, which keeps the task indices in SGPRs.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int task = blockIdx.x * 4 + wave;
+    const int task = blockIdx.x * kWaves + wave;
     if (task >= p.ntiles * p.nsplit) return;   // uniform per wave
     const int tile = task / p.nsplit;
     const int split = task - tile * p.nsplit;
@@ -183,25 +260,22 @@ __global__ __launch_bounds__(256) void gemv_exact_kernel(const void *__restrict_
     const int s0 = split * p.sps;
     const int s1 = min(s0 + p.sps, p.nstripes);
 
-    // Loader: instruction i fetches rows row0+16i .. +15, four lanes per row.
-    const int lq = lane & 3, lr = lane >> 2;
-    const uint8_t *src[4];
-    int wslot[4], rslot[4];
+    const uint8_t *src[kLoads];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 16 * i + lr;
-        const int rc = min(row0 + r, p.N - 1);
-        src[i] = p.W + (size_t)rc * p.row_bytes + lq * 16;
-        wslot[i] = r * 4 + (lq ^ ((r >> 2) & 3));
-        rslot[i] = lane * 4 + (i ^ ((lane >> 2) & 3));
+    for (int i = 0; i < kLoads; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        const int q = (lane & 7) ^ ((r >> 1) & 7);
+        src[i] = p.W + (size_t)min(row0 + r, p.N - 1) * p.row_bytes + q * 16;
     }
-    u32x4 *L = lds[wave];
+    const int swz = (lane >> 1) & 7;
+    // When this wave folds the groups itself, the lane's group scales ride
+    // along with each stripe.
+    const bool scale_dma = F::group && p.nsplit == 1;
+    const float *ssrc = p.S + (size_t)nc * p.G;
+    u32x4 *my_slot = &slot[wave][0];
+    float *my_scales = &scale_slot[F::group ? wave : 0][0];
+    issue_stripe<FMT>(src, ssrc, s0, scale_dma, my_slot, my_scales);
 
-    u32x4 pre[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pre[i] = *(const u32x4 *)(src[i] + (size_t)s0 * 64);
-
-    constexpr bool kW8 = (FMT == F_W8A32 || FMT == F_W8A16);
     // int8: lo[m][l] are the 8 lanes.  int4: lo/hi are the two 8-lane halves.
     float lo[MT][8], hi[MT][8], gacc[MT];
 #pragma unroll
@@ -211,24 +285,40 @@ __global__ __launch_bounds__(256) void gemv_exact_kernel(const void *__restrict_
         for (int l = 0; l < 8; ++l) lo[m][l] = hi[m][l] = 0.0f;
     }
     const size_t K = (size_t)p.K;
+    const uint32_t magic = opaque_magic();
 
     for (int s = s0; s < s1; ++s) {
+        wait_vmcnt<0>();   // stripe s (and its scales) landed in the slot
+        u32x4 mine[kLoads];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) L[wslot[i]] = pre[i];
-        if (s + 1 < s1) {
+        for (int j = 0; j < kLoads; ++j) mine[j] = my_slot[8 * lane + (j ^ swz)];
+        float gscale[F::scale_words];
+        if constexpr (F::group) {
+            if (scale_dma) {
+                if constexpr (FMT == F_W4G128) {
+                    gscale[0] = my_scales[lane];
+                    gscale[1] = my_scales[64 + lane];
+                } else {
+                    const f32x4 v0 = ((const f32x4 *)my_scales)[lane];
+                    const f32x4 v1 = ((const f32x4 *)(my_scales + 256))[lane];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pre[i] = *(const u32x4 *)(src[i] + (size_t)(s + 1) * 64);
+                    for (int e = 0; e < 4; ++e) {
+                        gscale[e] = v0[e];
+                        gscale[4 + e] = v1[e];
+                    }
+                }
+            }
         }
-        u32x4 mine[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mine[i] = L[rslot[i]];
+        // The slot is refilled only once every lane's reads have returned.
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        if (s + 1 < s1) issue_stripe<FMT>(src, ssrc, s + 1, scale_dma, my_slot, my_scales);
 
-        if constexpr (kW8) {
-            // 64 int8 weights: k = 64s + 4d + j belongs to lane 4(d&1) + j.
-            const size_t kb = (size_t)s * 64;
+        if constexpr (F::w8) {
+            // 128 int8 weights: k = 128s + 4d + j belongs to lane 4(d&1) + j.
+            const size_t kb = (size_t)s * kStripe;
 #pragma unroll
-            for (int d = 0; d < 16; ++d) {
-                const uint32_t x = word_of(mine, d);
+            for (int d = 0; d < 32; ++d) {
+                const uint32_t x = mine[d >> 2][d & 3];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float w = (float)(int)(int8_t)(uint8_t)(x >> (8 * j));
@@ -248,28 +338,78 @@ __global__ __launch_bounds__(256) void gemv_exact_kernel(const void *__restrict_
                 }
             }
         } else {
-            const cu32 *a32 = as_const(p.A) + ((size_t)m0 * K) / 2;
-            const int kb = s * 128;
+            // Activations arrive in batches of kBatch chunks per row (one
+            // round of scalar loads per batch, immediate offsets from a
+            // per-stripe base).
+            constexpr int kBatch = (MT == 1) ? 8 : (MT == 2 ? 4 : 2);
             constexpr int kChunksPerGroup = (FMT == F_W4G32) ? 2 : 8;
+            const size_t row_dw = K / 2;                                     // dwords per activation row
+            const cu32 *ab = as_const(p.A) + (size_t)m0 * row_dw + (size_t)s * kStripe;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                w4_chunk<MT>(word_of(mine, 2 * c), word_of(mine, 2 * c + 1), a32, p.K, kb + 16 * c, lo, hi);
-                if constexpr (FMT == F_W4G128 || FMT == F_W4G32) {
-                    if ((c + 1) % kChunksPerGroup == 0) {
-                        const int g = (FMT == F_W4G128) ? s : 4 * s + c / 2;
-                        const float sc = p.S[(size_t)nc * p.G + g];
+            for (int cb = 0; cb < 16; cb += kBatch) {
+                uint32_t act[MT][8 * kBatch];
 #pragma unroll
-                        for (int m = 0; m < MT; ++m) {
-                            const float block = w4_block_and_reset(lo[m], hi[m]);
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int j = 0; j < 8 * kBatch; ++j) act[m][j] = ab[m * row_dw + 8 * cb + j];
+#pragma unroll
+                for (int c = cb; c < cb + kBatch; ++c) {
+                    w4_chunk<MT, 8 * kBatch>(mine[c >> 1][2 * (c & 1)], mine[c >> 1][2 * (c & 1) + 1],
+                                             &act[0][8 * (c - cb)], magic, lo, hi);
+                    if constexpr (F::group) {
+                        if ((c + 1) % kChunksPerGroup == 0) {
+                            const int gl = c / kChunksPerGroup;                 // group within the stripe
+                            const int g = F::groups_per_stripe * s + gl;
                             if (p.nsplit == 1) {
-                                gacc[m] = __builtin_fmaf(block, sc, gacc[m]);
-                            } else if (n < p.N) {
-                                p.P[((size_t)g * p.M + m0 + m) * p.N + n] = block;
+#pragma unroll
+                                for (int m = 0; m < MT; ++m)
+                                    gacc[m] = __builtin_fmaf(w4_block_and_reset(lo[m], hi[m]), gscale[gl], gacc[m]);
+                            } else {
+#pragma unroll
+                                for (int m = 0; m < MT; ++m) {
+                                    const float block = w4_block_and_reset(lo[m], hi[m]);
+                                    if (n < p.N)
+                                        __hip_atomic_store(p.P + ((size_t)g * p.M + m0 + m) * p.N + n, block,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                }
                             }
                         }
                     }
                 }
             }
+        }
+    }
+
+    if constexpr (F::group) {
+        if (p.nsplit > 1) {
+            // The block sums went out as agent-scope stores (written through
+            // to the device-coherent level, no L2 write-back needed); once
+            // they have completed (vmcnt 0) the wave takes a ticket.  The last
+            // of the tile's nsplit waves reads every block back with
+            // agent-scope loads and folds the groups in order.
+            wait_vmcnt<0>();
+            int ticket = 0;
+            if (lane == 0)
+                ticket = __hip_atomic_fetch_add(p.T + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ticket = __builtin_amdgcn_readfirstlane(ticket);
+            if (ticket != p.nsplit - 1) return;
+            if (n < p.N) {
+                const size_t gstride = (size_t)p.M * p.N;
+                const float *srow = p.S + (size_t)n * p.G;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float *pp = p.P + (size_t)(m0 + m) * p.N + n;
+                    float acc = 0.0f;
+#pragma unroll 8
+                    for (int g = 0; g < p.G; ++g)
+                        acc = __builtin_fmaf(
+                            __hip_atomic_load(pp + g * gstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), srow[g],
+                            acc);
+                    ((uint16_t *)p.C)[(size_t)(m0 + m) * p.N + n] = f32_to_bf16(acc);
+                }
+            }
+            if (lane == 0) __hip_atomic_store(p.T + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
         }
     }
 
@@ -284,20 +424,9 @@ __global__ __launch_bounds__(256) void gemv_exact_kernel(const void *__restrict_
         } else if constexpr (FMT == F_W4ROW) {
             ((uint16_t *)p.C)[o] = f32_to_bf16(w4_block_and_reset(lo[m], hi[m]) * p.S[n]);
         } else {
-            if (p.nsplit == 1) ((uint16_t *)p.C)[o] = f32_to_bf16(gacc[m]);
+            ((uint16_t *)p.C)[o] = f32_to_bf16(gacc[m]);
         }
     }
-}
-
-// Folds per-group block sums with the scales in group order (kernels.c:1135).
-__global__ __launch_bounds__(256) void group_fold_kernel(const float *__restrict__ P, const float *__restrict__ S,
-                                                         uint16_t *__restrict__ C, int M, int N, int G) {
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)M * N) return;
-    const int m = (int)(idx / N), n = (int)(idx % N);
-    float acc = 0.0f;
-    for (int g = 0; g < G; ++g) acc = __builtin_fmaf(P[((size_t)g * M + m) * N + n], S[(size_t)n * G + g], acc);
-    C[idx] = f32_to_bf16(acc);
 }
 
 // ----------------------------------------------------- literal fallback
@@ -382,10 +511,10 @@ __global__ __launch_bounds__(256) void gemv_literal_kernel(GemvArgs p, int group
 template <int FMT>
 static void launch_exact_mt(int mt, dim3 grid, hipStream_t st, const GemvArgs &a, int m0) {
     switch (mt) {
-        case 1: gemv_exact_kernel<FMT, 1><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
-        case 2: gemv_exact_kernel<FMT, 2><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
-        case 3: gemv_exact_kernel<FMT, 3><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
-        default: gemv_exact_kernel<FMT, 4><<<grid, 256, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a, m0); break;
+        case 1: gemv_exact_kernel<FMT, 1><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
+        case 2: gemv_exact_kernel<FMT, 2><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
+        case 3: gemv_exact_kernel<FMT, 3><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
+        default: gemv_exact_kernel<FMT, 4><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
     }
 }
 
@@ -397,6 +526,41 @@ static void launch_exact(int fmt, int mt, dim3 grid, hipStream_t st, const GemvA
         case F_W4G128: launch_exact_mt<F_W4G128>(mt, grid, st, a, m0); break;
         default: launch_exact_mt<F_W4G32>(mt, grid, st, a, m0); break;
     }
+}
+
+// ---- per-call timing (HIP events on the launch stream) -------------------
+// Enabled by ecpu_hip_profile_begin(); each linear call records one event
+// pair around its kernels, tagged with a family name and the call's
+// algorithmic bytes and flops.  Read back with ecpu_hip_profile_read().
+struct ProfRec {
+    hipEvent_t a, b;
+    const char *family;
+    double bytes, flops;
+};
+static std::mutex g_prof_mu;
+static std::vector<ProfRec> g_prof;
+static std::vector<hipEvent_t> g_event_pool;
+static bool g_prof_on = false;
+
+static hipEvent_t pooled_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    (void)hipEventCreate(&e);
+    return e;
+}
+
+static const char *family_name(int fmt, size_t M) {
+    static const char *names[5][3] = {
+        {"w8a32_gemv", "w8a32_m2to4", "w8a32_m5plus"},
+        {"w8a16_gemv", "w8a16_m2to4", "w8a16_m5plus"},
+        {"w4a16_gemv", "w4a16_m2to4", "w4a16_m5plus"},
+        {"w4a16g128_gemv", "w4a16g128_m2to4", "w4a16g128_m5plus"},
+        {"w4a16g32_gemv", "w4a16g32_m2to4", "w4a16g32_m5plus"}};
+    return names[fmt][M == 1 ? 0 : (M <= 4 ? 1 : 2)];
 }
 
 static int env_int(const char *name, int dflt) {
@@ -418,6 +582,7 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     a.S = S;
     a.C = C;
     a.P = nullptr;
+    a.T = nullptr;
     a.M = (int)M;
     a.N = (int)N;
     a.K = (int)K;
@@ -426,8 +591,9 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     a.ntiles = (int)((N + 63) / 64);
     a.nsplit = 1;
 
-    const size_t stripe_k = w8 ? 64 : 128;
-    const bool aligned = (((uintptr_t)W | (uintptr_t)A) & 15) == 0;
+    const size_t stripe_k = w8 ? kStripe : 2 * kStripe;   // weights per 128-byte stripe
+    const bool aligned = (((uintptr_t)W | (uintptr_t)A) & 15) == 0 &&
+                         (fmt != F_W4G32 || ((uintptr_t)S & 15) == 0) && ((uintptr_t)S & 3) == 0;
     const bool fast = K > 0 && K % stripe_k == 0 && aligned && env_int("PILM_HIP_LITERAL", 0) == 0;
     if (!fast) {
         const size_t total = M * N;
@@ -454,21 +620,91 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         a.sps = a.nstripes;
     }
     if (a.nsplit > 1) {
-        int rc = ECPU_OK;
-        a.P = scratch_floats((size_t)a.G * M * N, &rc, fn);
-        if (!a.P) return rc;
+        const int rc = split_scratch(st, (size_t)a.G * M * N, (size_t)a.ntiles, &a.P, &a.T, fn);
+        if (rc != ECPU_OK) return rc;
     }
     const int tasks = a.ntiles * a.nsplit;
-    const dim3 grid((tasks + 3) / 4);
+    const dim3 grid((tasks + kWaves - 1) / kWaves);
+    hipEvent_t ev0 = nullptr;
+    if (g_prof_on) {
+        std::lock_guard<std::mutex> lk(g_prof_mu);
+        ev0 = pooled_event();
+        (void)hipEventRecord(ev0, st);
+    }
     for (size_t m0 = 0; m0 < M; m0 += 4) {
         const int mt = (int)std::min<size_t>(4, M - m0);
         launch_exact(fmt, mt, grid, st, a, (int)m0);
     }
-    if (a.nsplit > 1) {
-        const size_t total = M * N;
-        group_fold_kernel<<<(total + 255) / 256, 256, 0, st>>>(a.P, S, (uint16_t *)C, (int)M, (int)N, a.G);
+    if (ev0) {
+        std::lock_guard<std::mutex> lk(g_prof_mu);
+        hipEvent_t ev1 = pooled_event();
+        (void)hipEventRecord(ev1, st);
+        const double a_elt = (fmt == F_W8A32) ? 4.0 : 2.0;
+        const double scale_bytes = 4.0 * (double)N * (group ? (double)a.G : 1.0);
+        const double bytes = (double)N * a.row_bytes + scale_bytes + a_elt * (double)(M * K) + a_elt * (double)(M * N);
+        g_prof.push_back({ev0, ev1, family_name(fmt, M), bytes, 2.0 * (double)M * (double)N * (double)K});
     }
     return check_launch(fn);
 }
 
 }  // namespace pilm
+
+using namespace pilm;
+
+extern "C" {
+
+int ecpu_hip_profile_begin(void) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    for (auto &r : g_prof) {
+        g_event_pool.push_back(r.a);
+        g_event_pool.push_back(r.b);
+    }
+    g_prof.clear();
+    g_prof_on = true;
+    return ECPU_OK;
+}
+
+int ecpu_hip_profile_end(void) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof_on = false;
+    return ECPU_OK;
+}
+
+// One line per family: "<family> <calls> <total_ms> <alg_bytes> <flops>".
+int ecpu_hip_profile_read(char *buf, size_t len) {
+    if (!buf || len == 0) return fail(ECPU_ERR_PARAM, "ecpu_hip_profile_read: empty buffer");
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    struct Agg {
+        std::string name;
+        long calls = 0;
+        double ms = 0, bytes = 0, flops = 0;
+    };
+    std::vector<Agg> aggs;
+    for (auto &r : g_prof) {
+        if (hipEventSynchronize(r.b) != hipSuccess) return fail(ECPU_ERR_DEVICE, "profile: event sync failed");
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return fail(ECPU_ERR_DEVICE, "profile: elapsed failed");
+        Agg *g = nullptr;
+        for (auto &x : aggs)
+            if (x.name == r.family) g = &x;
+        if (!g) {
+            aggs.push_back(Agg{r.family});
+            g = &aggs.back();
+        }
+        g->calls++;
+        g->ms += ms;
+        g->bytes += r.bytes;
+        g->flops += r.flops;
+    }
+    std::string out;
+    char line[256];
+    for (auto &x : aggs) {
+        snprintf(line, sizeof(line), "%s %ld %.6f %.0f %.0f\n", x.name.c_str(), x.calls, x.ms, x.bytes, x.flops);
+        out += line;
+    }
+    if (out.size() + 1 > len) return fail(ECPU_ERR_PARAM, "ecpu_hip_profile_read: buffer too small");
+    memcpy(buf, out.c_str(), out.size() + 1);
+    return ECPU_OK;
+}
+
+}  // extern "C"

@@ -9,11 +9,14 @@
 // device is added whose memory is HBM.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include <sys/sysinfo.h>
 
@@ -21,7 +24,6 @@
 
 namespace pilm {
 
-static thread_local char t_err[512];
 static char g_err[512];
 static std::mutex g_err_mu;
 
@@ -33,7 +35,6 @@ int fail(int rc, const char *fmt, ...) {
     va_end(ap);
     std::lock_guard<std::mutex> lk(g_err_mu);
     memcpy(g_err, buf, sizeof(g_err));
-    memcpy(t_err, buf, sizeof(t_err));
     return rc;
 }
 
@@ -73,56 +74,85 @@ int check_launch(const char *fn) {
     return ECPU_OK;
 }
 
-// ---- split-K scratch (one buffer per device) ------------------------------
-static constexpr int kMaxDevices = 16;
-static float *g_scratch[kMaxDevices];
-static size_t g_scratch_n[kMaxDevices];
+// ---- split-K scratch, one set per device ----------------------------------
+// Shared by every stream of the device: two split-path calls that overlap in
+// time on one GPU (different streams) would race on it.  A graph captured on
+// any stream can use it as long as the set was sized before the capture.
+struct Scratch {
+    int dev;
+    float *P;
+    size_t nP;
+    int *T;
+    size_t nT;
+};
+static std::vector<Scratch> g_scratch;
+static std::vector<std::pair<int, void *>> g_retired;
 static std::mutex g_scratch_mu;
 
-float *scratch_floats(size_t n, int *rc, const char *fn) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        *rc = fail(ECPU_ERR_DEVICE, "%s: no usable current HIP device", fn);
+static void *dev_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
         return nullptr;
     }
+    return p;
+}
+
+int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, int **T, const char *fn) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(ECPU_ERR_DEVICE, "%s: no current HIP device", fn);
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (g_scratch_n[dev] < n) {
-        size_t want = n < (1u << 20) ? (1u << 20) : n;
-        if (g_scratch[dev]) {
-            // Work already queued may still read the old buffer.
-            (void)hipDeviceSynchronize();
-            (void)hipFree(g_scratch[dev]);
-            g_scratch[dev] = nullptr;
-            g_scratch_n[dev] = 0;
-        }
-        void *p = nullptr;
-        if (hipMalloc(&p, want * sizeof(float)) != hipSuccess) {
-            (void)hipGetLastError();
-            *rc = fail(ECPU_ERR_MEM, "%s: hipMalloc of %zu bytes of split-K scratch failed", fn,
-                       want * sizeof(float));
-            return nullptr;
-        }
-        g_scratch[dev] = (float *)p;
-        g_scratch_n[dev] = want;
+    Scratch *sc = nullptr;
+    (void)stream;
+    for (auto &e : g_scratch)
+        if (e.dev == dev) sc = &e;
+    if (!sc) {
+        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0});
+        sc = &g_scratch.back();
     }
-    *rc = ECPU_OK;
-    return g_scratch[dev];
+    if (sc->nP < nfloat) {
+        const size_t want = std::max<size_t>(nfloat, 1u << 18);
+        float *p = (float *)dev_alloc(want * sizeof(float));
+        if (!p) return fail(ECPU_ERR_MEM, "%s: hipMalloc of %zu bytes of split-K scratch failed", fn, want * 4);
+        if (sc->P) g_retired.push_back({dev, sc->P});
+        sc->P = p;
+        sc->nP = want;
+    }
+    if (sc->nT < nticket) {
+        const size_t want = std::max<size_t>(nticket, 4096);
+        int *t = (int *)dev_alloc(want * sizeof(int));
+        if (!t) return fail(ECPU_ERR_MEM, "%s: hipMalloc of split-K tickets failed", fn);
+        if (hipMemset(t, 0, want * sizeof(int)) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(t);
+            return fail(ECPU_ERR_DEVICE, "%s: clearing split-K tickets failed", fn);
+        }
+        if (sc->T) g_retired.push_back({dev, sc->T});
+        sc->T = t;
+        sc->nT = want;
+    }
+    *P = sc->P;
+    *T = sc->T;
+    return ECPU_OK;
 }
 
 static void free_scratch() {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    for (int d = 0; d < kMaxDevices; d++) {
-        if (g_scratch[d]) {
-            int cur = 0;
-            (void)hipGetDevice(&cur);
-            (void)hipSetDevice(d);
-            (void)hipDeviceSynchronize();
-            (void)hipFree(g_scratch[d]);
-            (void)hipSetDevice(cur);
-        }
-        g_scratch[d] = nullptr;
-        g_scratch_n[d] = 0;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    auto release = [](int dev, void *p) {
+        (void)hipSetDevice(dev);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(p);
+    };
+    for (auto &r : g_retired) release(r.first, r.second);
+    for (auto &e : g_scratch) {
+        if (e.P) release(e.dev, e.P);
+        if (e.T) release(e.dev, e.T);
     }
+    g_retired.clear();
+    g_scratch.clear();
+    (void)hipSetDevice(cur);
 }
 
 }  // namespace pilm
