@@ -15,11 +15,21 @@ replayed.
 Printed JSON line:
   value        algorithmic GB/s of the whole step (weights + scales +
                activations + outputs, each counted once) / wall time
-  roofline     the g128 GEMV kernel's algorithmic GB/s from per-call HIP
-               events on its stream, against the 8 TB/s HBM peak
+  roofline     the g128 GEMV kernel's algorithmic GB/s per launch: HIP events
+               on the replay stream around the timed replays, divided by the
+               launches (it is the step's only kernel), against 8 TB/s
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
-  sweep        per-shape GB/s at M = 1, 4, 16 (configuration sweep)
+  sweep        per-shape GB/s at M = 1, 4, 16 (only with --sweep)
+
+Profiling helpers (rocprofv3 runs the program, these read its output):
+  --pmc-pass            eager steps plus a plain copy kernel of known size,
+                        for one rocprofv3 --pmc counter pass
+  --traffic F W         FETCH_SIZE / WRITE_SIZE counter CSVs of two such
+                        passes -> HBM bytes per GEMV launch, calibrated by
+                        the copy kernel; written to profiles/ and reported as
+                        roofline.traffic while the kernel source is unchanged
+  --stats-summary CSV   rocprofv3 --kernel-trace --stats output -> summary
 """
 from __future__ import annotations
 
@@ -35,6 +45,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+KERNEL_SRC = ROOT / "pilm_amd" / "csrc" / "linear_exact.hip"
+GEMV_KERNEL = "gemv_exact_kernel<3, 1>"          # W4A16 group-128, one activation row
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_exact_w4a16g128_m1_qwen3_1p7b_decode.traffic.txt"
+CALIB_BYTES = 1 << 30                              # copy kernel: reads and writes 1 GiB
 LAYERS = 28
 HIDDEN = 2048
 LAYER_SHAPES = [("q_proj", 4096, 2048), ("k_proj", 1024, 2048), ("v_proj", 1024, 2048), ("o_proj", 2048, 2048),
@@ -105,35 +119,51 @@ def capture(torch, run):
     return g
 
 
-def time_graph(torch, g, steps: int, warmup: int) -> float:
+def time_graph(torch, g, steps: int, warmup: int, events: bool = False):
+    """Wall seconds for `steps` replays; with events=True also the GPU
+    seconds between HIP events recorded on the replay stream around them."""
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record()
     for _ in range(steps):
         g.replay()
+    e1.record()
     torch.cuda.synchronize()
-    return time.perf_counter() - t0
+    wall = time.perf_counter() - t0
+    return (wall, e0.elapsed_time(e1) / 1e3) if events else wall
 
 
-def roofline(torch, run, reps: int = 3) -> dict:
-    """Per-call HIP event timing of the g128 GEMV (eager launches)."""
-    from pilm_amd import bindings as abi
-    run()
-    torch.cuda.synchronize()
-    abi.profile_begin()
-    for _ in range(reps):
-        run()
-    abi.profile_end()
-    prof = abi.profile_read()
-    fam = prof["w4a16g128_gemv"]
-    sec = fam["ms"] / 1e3
-    achieved = fam["bytes"] / sec / 1e9
+def roofline(gpu_sec: float, launches: int, bytes_per_launch: float) -> dict:
+    """The g128 GEMV is the only kernel of the step: its average launch
+    duration is the HIP-event time of the timed replays over the launches."""
+    avg = gpu_sec / launches
+    achieved = bytes_per_launch / avg / 1e9
+    traffic, traffic_note = measured_traffic()
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gemv_exact_kernel<W4G128,1> (+ group_fold_kernel when K is split)",
-            "calls": fam["calls"], "avg_launch_us": round(fam["ms"] * 1e3 / fam["calls"], 3),
-            "alg_bytes_per_launch": round(fam["bytes"] / fam["calls"])}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": GEMV_KERNEL + " (K split folded inside the kernel)",
+            "launches": launches, "avg_launch_us": round(avg * 1e6, 3),
+            "alg_bytes_per_launch": round(bytes_per_launch), "traffic_source": traffic_note}
+
+
+def source_hash() -> str:
+    import hashlib
+    return hashlib.sha256(KERNEL_SRC.read_bytes()).hexdigest()
+
+
+def measured_traffic():
+    """HBM bytes per launch from the committed counter summary, if it was
+    measured on the current kernel source; (None, reason) otherwise."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text().strip().splitlines()[-1])
+    except (OSError, ValueError, IndexError):
+        return None, "no counter summary"
+    if rec.get("source_sha256") != source_hash():
+        return None, "counter summary is for another kernel source"
+    return rec["traffic"], TRAFFIC_FILE.name
 
 
 def sweep(torch, dev, ms=(1, 4, 16), reps: int = 20) -> dict:
@@ -209,6 +239,81 @@ def cpu_baseline(budget_s: float = 12.0) -> dict | None:
             "cpu": _cpu_model()}
 
 
+def pmc_pass(torch, dev, steps: int) -> None:
+    """Eager steps (every dispatch visible to counter collection), then a
+    plain copy kernel of known size: out = -x over CALIB_BYTES of fp32."""
+    xs, calls = build_step(torch, dev, 1)
+    run = launcher(torch, xs, calls, 1)
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    del calls, xs, run
+    torch.cuda.empty_cache()
+    x = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(f"[bench] pmc pass: {steps} eager steps of {len(step_shapes())} calls, 3 copy kernels of "
+          f"{CALIB_BYTES} B", flush=True)
+
+
+def _counter_means(csv_path: str, counter: str) -> dict:
+    """{kernel name: mean counter value per dispatch} from a rocprofv3
+    counter_collection.csv."""
+    import csv
+    acc = {}
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            a = acc.setdefault(r["Kernel_Name"], [0.0, 0])
+            a[0] += float(r["Counter_Value"])
+            a[1] += 1
+    return {k: (v[0] / v[1], v[1]) for k, v in acc.items()}
+
+
+def _pick(means: dict, needle: str):
+    hits = [(k, v) for k, v in means.items() if needle in k]
+    if len(hits) != 1:
+        raise SystemExit(f"expected one kernel matching {needle!r}, found {len(hits)}")
+    return hits[0][1]
+
+
+def traffic_summary(fetch_csv: str, write_csv: str) -> dict:
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the GEMV and of the
+    copy kernel; the copy kernel moves CALIB_BYTES each way, which fixes the
+    bytes each counter unit stands for."""
+    f = _counter_means(fetch_csv, "FETCH_SIZE")
+    w = _counter_means(write_csv, "WRITE_SIZE")
+    (gf, nf), (cf, _) = _pick(f, GEMV_KERNEL), _pick(f, "neg_kernel")
+    (gw, nw), (cw, _) = _pick(w, GEMV_KERNEL), _pick(w, "neg_kernel")
+    ff, fw = CALIB_BYTES / (cf * 1024), CALIB_BYTES / (cw * 1024)
+    fetch_b, write_b = gf * 1024 * ff, gw * 1024 * fw
+    step_alg = sum(alg_bytes(1, n, k) for (_, n, k) in step_shapes())
+    return {"traffic": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+            "alg_bytes_per_launch": round(step_alg / len(step_shapes())),
+            "fetch_kib_raw": round(gf, 3), "write_kib_raw": round(gw, 3),
+            "copy_fetch_kib_raw": round(cf, 3), "copy_write_kib_raw": round(cw, 3),
+            "fetch_factor": round(ff, 4), "write_factor": round(fw, 4),
+            "dispatches": [nf, nw], "source_sha256": source_hash()}
+
+
+def stats_summary(stats_csv: str, top: int = 8) -> str:
+    import csv
+    rows = list(csv.DictReader(open(stats_csv, newline="")))
+    lines = ["| kernel | calls | total ms | avg us | min us | max us | % |", "|---|---|---|---|---|---|---|"]
+    for r in rows[:top]:
+        name = r["Name"]
+        short = name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+        if len(short) > 90:
+            short = short[:87] + "..."
+        lines.append(f"| `{short}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                     f"{float(r['AverageNs']) / 1e3:.3f} | {float(r['MinNs']) / 1e3:.3f} | "
+                     f"{float(r['MaxNs']) / 1e3:.3f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(lines)
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -224,10 +329,28 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="add the per-shape M=1,4,16 sweep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--stats-summary", metavar="STATS_CSV")
     args = ap.parse_args(argv)
+    if args.traffic:
+        rec = traffic_summary(*args.traffic)
+        TRAFFIC_FILE.parent.mkdir(exist_ok=True)
+        TRAFFIC_FILE.write_text(
+            f"# HBM traffic per launch of {GEMV_KERNEL}, Qwen3-1.7B W4A16-g128 decode step (M=1)\n"
+            "# passes: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -d DIR -o run "
+            "-- python bench.py --pmc-pass --steps 2\n"
+            f"# then:  python bench.py --traffic DIR_F/run_counter_collection.csv DIR_W/run_counter_collection.csv\n"
+            f"# counter KiB x (copy kernel's known {CALIB_BYTES} B / its counter KiB) = bytes\n"
+            + json.dumps(rec) + "\n")
+        print(json.dumps(rec))
+        return 0
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the decode GEMV would shard by output rows, see DESIGN.md", file=sys.stderr)
@@ -238,6 +361,9 @@ def main(argv=None) -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.pmc_pass:
+        pmc_pass(torch, dev, args.steps)
+        return 0
     m = 1
     print(f"[bench] building step: {len(step_shapes())} W4A16-g128 linears, M={m}", flush=True)
     xs, calls = build_step(torch, dev, m)
@@ -245,9 +371,10 @@ def main(argv=None) -> int:
     step_bytes = sum(alg_bytes(m, n, k) for (_, n, k, *_rest) in calls)
     g = capture(torch, run)
     print(f"[bench] graph captured; timing {args.steps} steps after {args.warmup} warmup", flush=True)
-    sec = time_graph(torch, g, args.steps, args.warmup)
+    sec, gpu_sec = time_graph(torch, g, args.steps, args.warmup, events=True)
     ms_per_step = sec / args.steps * 1e3
     value = step_bytes * args.steps / sec / 1e9
+    roof = roofline(gpu_sec, args.steps * len(calls), step_bytes / len(calls))
 
     # eager (no graph) step time, for reference
     torch.cuda.synchronize()
@@ -257,8 +384,6 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) / 3 * 1e3
 
-    print("[bench] per-call event timing", flush=True)
-    roof = roofline(torch, run)
     del g
     out = {
         "metric": "quant GEMV HBM GB/s (% of peak) + Qwen3-1.7B W4A16 decode tok/s, 1 GPU",
@@ -281,7 +406,7 @@ def main(argv=None) -> int:
         "eager_ms_per_step": round(eager_ms, 3),
         "roofline": roof,
     }
-    if not args.no_sweep:
+    if args.sweep:
         print("[bench] shape sweep M=1,4,16", flush=True)
         del calls, xs, run
         torch.cuda.empty_cache()

@@ -7,7 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 
-#include "../../include/ecpu_hip.h"
+#include "ecpu_hip.h"
 
 namespace pilm {
 

@@ -13,19 +13,20 @@
 // out around the chains rather than across them:
 //
 //   * one lane owns one output row (all of that row's chains live in its
-//     registers); a wave covers 64 consecutive rows;
-//   * the wave streams its 64 rows in 64-byte "stripes": four coalesced
-//     16-byte loads per lane fetch 64 rows x 64 B, an XOR-swizzled LDS round
-//     trip hands every lane its own row's 64 B (conflict-free on 64 banks);
+//     registers); a wave covers a tile of 64 consecutive rows;
+//   * the wave streams its rows in 128-byte stripes (one cache line per row)
+//     that a global -> LDS DMA lands XOR-swizzled in an 8 KB slot, from where
+//     every lane reads its own row conflict-free;
 //   * activations are the same for all lanes of a wave (same k), so they
 //     arrive through scalar loads and feed v_fma_mix_f32 / v_fma_f32 as SGPR
 //     operands;
 //   * int4 nibbles become exact fp16 values with one and-or against the 1024
 //     exponent pattern plus one packed fp16 add (or fma) per nibble pair;
 //     v_fma_mix_f32 then performs fma(a, w, acc) with w widened exactly;
-//   * group-scaled formats may split K across waves: each wave then stores
-//     its per-group block sums and a small second kernel folds them with the
-//     scales in group order (the only serial part of the group formula).
+//   * group-scaled formats may divide K among several waves: the per-group
+//     block sums meet in LDS (waves of one workgroup) or in global memory
+//     (several workgroups), and one lane per row folds them with the scales
+//     in group order (the only serial part of the group formula).
 //
 // Shapes the stripe loop cannot take (K not a multiple of the stripe,
 // unaligned pointers) run a one-thread-per-output kernel that follows the
@@ -61,11 +62,13 @@ struct GemvArgs {
     int *T;                  // per-tile tickets (zero between launches)
     int M, N, K;
     int row_bytes;           // bytes per weight row
-    int nstripes;            // 64-byte stripes per row (fast path)
-    int sps;                 // stripes per split
-    int nsplit;
+    int nstripes;            // 128-byte stripes per row (fast path)
+    int sps;                 // stripes per part
+    int pl;                  // parts of a tile inside one workgroup (one wave each)
+    int pg;                  // workgroups per tile (group formats; block sums meet in global memory)
     int ntiles;              // ceil(N / 64)
     int G;                   // scale groups per row (group formats)
+    int scale_slot_bytes;    // LDS per wave for the scales of one stripe
 };
 
 // Activations are read through the constant address space: the address is the
@@ -178,7 +181,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kStripe = 128;        // bytes of each row per stripe: one full cache line
 constexpr int kLoads = 8;           // 16-byte DMA loads per lane per stripe (64 rows x 128 B)
-constexpr int kWaves = 4;           // independent waves per block
+constexpr int kMaxParts = 8;        // waves (K parts of one tile) per workgroup, at most
+constexpr int kSlotBytes = 64 * kLoads * 16;   // one stripe: 64 rows x 128 B
 constexpr int kNT = 2;              // cache policy of the weight stream: non-temporal
 
 template <int FMT>
@@ -220,23 +224,37 @@ __device__ __forceinline__ void issue_stripe(const uint8_t *const (&src)[kLoads]
     }
 }
 
-// Stripe-streaming exact kernel.  Block = kWaves independent waves; a wave
-// task = (64-row tile, K split).  MT activation rows starting at m0.
+// Stripe-streaming exact kernel.
 //
-// Each wave streams its 64 rows in stripes of 64 rows x 128 B through one
-// 8 KB LDS slot filled by global_load_lds_dwordx4 (global -> LDS without
-// VGPRs, non-temporal): the wave waits for stripe s, copies it to registers,
+// A wave owns a tile of 64 consecutive rows (lane = row) and a contiguous
+// range of that tile's 128-byte stripes.  The stripes of a tile are divided
+// into p.pl parts inside one workgroup (one wave per part) and, for group
+// formats only, into p.pg workgroups:
+//   * pg == 1: part 0 folds its own groups as it goes; parts 1.. leave their
+//     per-group block sums (and scales) in LDS, and after a barrier part 0
+//     continues the fold with them in group order;
+//   * pg > 1: every part stores its block sums to global memory, and the last
+//     wave of the tile to arrive folds all of them in group order.
+// Per-row formats keep one part per tile (their FMA chains run over all K).
+//
+// Each wave streams its stripes (64 rows x 128 B) through one 8 KB LDS slot
+// filled by global_load_lds_dwordx4 (global -> LDS without VGPRs,
+// non-temporal): the wave waits for stripe s, copies it to registers,
 // refills the slot with stripe s + 1 and computes stripe s meanwhile.
 // Lane t of DMA instruction i fetches row 8i + t/8, 16-byte chunk
 // (t & 7) ^ ((row >> 1) & 7): the eight lanes of a row cover its full line,
 // and the data lands XOR-swizzled so that lane r reading its own row is
 // free of LDS bank conflicts.
+//
+// Dynamic LDS: pl slots of kSlotBytes, pl scale slots of p.scale_slot_bytes,
+// then (pg == 1, pl > 1) the fold area: float blocks[G - G0][MT][64] followed
+// by float scales[G - G0][64], where G0 = groups of part 0.
 template <int FMT, int MT>
-__global__ __launch_bounds__(64 * kWaves) void gemv_exact_kernel(const void *__restrict__ A_,
-                                                               const uint8_t *__restrict__ W_,
-                                                               const float *__restrict__ S_, void *__restrict__ C_,
-                                                               float *__restrict__ P_, int *__restrict__ T_,
-                                                               GemvArgs p, int m0) {
+__global__ __launch_bounds__(64 * kMaxParts) void gemv_exact_kernel(const void *__restrict__ A_,
+                                                                   const uint8_t *__restrict__ W_,
+                                                                   const float *__restrict__ S_, void *__restrict__ C_,
+                                                                   float *__restrict__ P_, int *__restrict__ T_,
+                                                                   GemvArgs p, int m0) {
     p.A = A_;
     p.W = W_;
     p.S = S_;
@@ -244,21 +262,22 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_exact_kernel(const void *__r
     p.P = P_;
     p.T = T_;
     using F = StripeFmt<FMT>;
-    __shared__ u32x4 slot[kWaves][64 * kLoads];
-    __shared__ float scale_slot[F::group ? kWaves : 1][64 * F::scale_words];
+    extern __shared__ __align__(16) unsigned char lds[];
     // threadIdx.x >> 6 is the same for all lanes of a wave; readfirstlane
-    // tells the compiler so, which keeps the task indices in SGPRs.
+    // tells the compiler so, which keeps the part indices in SGPRs.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int task = blockIdx.x * kWaves + wave;
-    if (task >= p.ntiles * p.nsplit) return;   // uniform per wave
-    const int tile = task / p.nsplit;
-    const int split = task - tile * p.nsplit;
+    const int tile = blockIdx.x / p.pg;
+    const int part = (blockIdx.x - tile * p.pg) * p.pl + wave;
+    const int nparts = p.pg * p.pl;
+    const bool global_split = F::group && p.pg > 1;
+    const bool local_split = F::group && !global_split && p.pl > 1;
     const int row0 = tile * 64;
     const int n = row0 + lane;
     const int nc = n < p.N ? n : p.N - 1;
-    const int s0 = split * p.sps;
+    const int s0 = min(part * p.sps, p.nstripes);
     const int s1 = min(s0 + p.sps, p.nstripes);
+    const int G0 = min(p.sps * F::groups_per_stripe, p.G);   // groups of part 0 (local split)
 
     const uint8_t *src[kLoads];
 #pragma unroll
@@ -268,13 +287,15 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_exact_kernel(const void *__r
         src[i] = p.W + (size_t)min(row0 + r, p.N - 1) * p.row_bytes + q * 16;
     }
     const int swz = (lane >> 1) & 7;
-    // When this wave folds the groups itself, the lane's group scales ride
+    // Unless the block sums go to global memory, the lane's group scales ride
     // along with each stripe.
-    const bool scale_dma = F::group && p.nsplit == 1;
+    const bool scale_dma = F::group && !global_split;
     const float *ssrc = p.S + (size_t)nc * p.G;
-    u32x4 *my_slot = &slot[wave][0];
-    float *my_scales = &scale_slot[F::group ? wave : 0][0];
-    issue_stripe<FMT>(src, ssrc, s0, scale_dma, my_slot, my_scales);
+    u32x4 *my_slot = (u32x4 *)(lds + wave * kSlotBytes);
+    float *my_scales = (float *)(lds + p.pl * kSlotBytes + wave * p.scale_slot_bytes);
+    float *fold_blocks = (float *)(lds + p.pl * (kSlotBytes + p.scale_slot_bytes));
+    float *fold_scales = fold_blocks + (size_t)(p.G - G0) * MT * 64;
+    if (s0 < s1) issue_stripe<FMT>(src, ssrc, s0, scale_dma, my_slot, my_scales);
 
     // int8: lo[m][l] are the 8 lanes.  int4: lo/hi are the two 8-lane halves.
     float lo[MT][8], hi[MT][8], gacc[MT];
@@ -360,10 +381,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_exact_kernel(const void *__r
                         if ((c + 1) % kChunksPerGroup == 0) {
                             const int gl = c / kChunksPerGroup;                 // group within the stripe
                             const int g = F::groups_per_stripe * s + gl;
-                            if (p.nsplit == 1) {
+                            if (!global_split) {
+                                if (wave == 0) {
 #pragma unroll
-                                for (int m = 0; m < MT; ++m)
-                                    gacc[m] = __builtin_fmaf(w4_block_and_reset(lo[m], hi[m]), gscale[gl], gacc[m]);
+                                    for (int m = 0; m < MT; ++m)
+                                        gacc[m] =
+                                            __builtin_fmaf(w4_block_and_reset(lo[m], hi[m]), gscale[gl], gacc[m]);
+                                } else {
+                                    // a later part of a locally split tile: park the block sums
+                                    const int gi = g - G0;
+#pragma unroll
+                                    for (int m = 0; m < MT; ++m)
+                                        fold_blocks[(gi * MT + m) * 64 + lane] = w4_block_and_reset(lo[m], hi[m]);
+                                    fold_scales[gi * 64 + lane] = gscale[gl];
+                                }
                             } else {
 #pragma unroll
                                 for (int m = 0; m < MT; ++m) {
@@ -381,18 +412,28 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_exact_kernel(const void *__r
     }
 
     if constexpr (F::group) {
-        if (p.nsplit > 1) {
+        if (local_split) {
+            // Every part of the tile has parked its block sums; part 0 folds
+            // them after its own groups, in group order.
+            __syncthreads();
+            if (wave != 0) return;
+            for (int gi = 0; gi < p.G - G0; ++gi) {
+                const float sc = fold_scales[gi * 64 + lane];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) gacc[m] = __builtin_fmaf(fold_blocks[(gi * MT + m) * 64 + lane], sc, gacc[m]);
+            }
+        } else if (global_split) {
             // The block sums went out as agent-scope stores (written through
             // to the device-coherent level, no L2 write-back needed); once
             // they have completed (vmcnt 0) the wave takes a ticket.  The last
-            // of the tile's nsplit waves reads every block back with
-            // agent-scope loads and folds the groups in order.
+            // of the tile's parts reads every block back with agent-scope
+            // loads and folds the groups in order.
             wait_vmcnt<0>();
             int ticket = 0;
             if (lane == 0)
                 ticket = __hip_atomic_fetch_add(p.T + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ticket = __builtin_amdgcn_readfirstlane(ticket);
-            if (ticket != p.nsplit - 1) return;
+            if (ticket != nparts - 1) return;
             if (n < p.N) {
                 const size_t gstride = (size_t)p.M * p.N;
                 const float *srow = p.S + (size_t)n * p.G;
@@ -508,24 +549,52 @@ __global__ __launch_bounds__(256) void gemv_literal_kernel(GemvArgs p, int group
 
 // --------------------------------------------------------------- launch
 
+constexpr size_t kMaxLds = 160 * 1024;   // LDS per workgroup on gfx950
+
+template <int FMT, int MT>
+static int launch_one(dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemvArgs &a, int m0) {
+    // Dynamic LDS above the default limit has to be allowed once per kernel.
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_exact_kernel<FMT, MT>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    gemv_exact_kernel<FMT, MT><<<grid, block, lds, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0);
+    return ECPU_OK;
+}
+
 template <int FMT>
-static void launch_exact_mt(int mt, dim3 grid, hipStream_t st, const GemvArgs &a, int m0) {
+static int launch_exact_mt(int mt, dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemvArgs &a, int m0) {
     switch (mt) {
-        case 1: gemv_exact_kernel<FMT, 1><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
-        case 2: gemv_exact_kernel<FMT, 2><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
-        case 3: gemv_exact_kernel<FMT, 3><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
-        default: gemv_exact_kernel<FMT, 4><<<grid, 64 * kWaves, 0, st>>>(a.A, a.W, a.S, a.C, a.P, a.T, a, m0); break;
+        case 1: return launch_one<FMT, 1>(grid, block, lds, st, a, m0);
+        case 2: return launch_one<FMT, 2>(grid, block, lds, st, a, m0);
+        case 3: return launch_one<FMT, 3>(grid, block, lds, st, a, m0);
+        default: return launch_one<FMT, 4>(grid, block, lds, st, a, m0);
     }
 }
 
-static void launch_exact(int fmt, int mt, dim3 grid, hipStream_t st, const GemvArgs &a, int m0) {
+static int launch_exact(int fmt, int mt, dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemvArgs &a,
+                        int m0) {
     switch (fmt) {
-        case F_W8A32: launch_exact_mt<F_W8A32>(mt, grid, st, a, m0); break;
-        case F_W8A16: launch_exact_mt<F_W8A16>(mt, grid, st, a, m0); break;
-        case F_W4ROW: launch_exact_mt<F_W4ROW>(mt, grid, st, a, m0); break;
-        case F_W4G128: launch_exact_mt<F_W4G128>(mt, grid, st, a, m0); break;
-        default: launch_exact_mt<F_W4G32>(mt, grid, st, a, m0); break;
+        case F_W8A32: return launch_exact_mt<F_W8A32>(mt, grid, block, lds, st, a, m0);
+        case F_W8A16: return launch_exact_mt<F_W8A16>(mt, grid, block, lds, st, a, m0);
+        case F_W4ROW: return launch_exact_mt<F_W4ROW>(mt, grid, block, lds, st, a, m0);
+        case F_W4G128: return launch_exact_mt<F_W4G128>(mt, grid, block, lds, st, a, m0);
+        default: return launch_exact_mt<F_W4G32>(mt, grid, block, lds, st, a, m0);
     }
+}
+
+// Dynamic LDS of one workgroup: stripe slots and scale slots of its pl waves,
+// plus the fold area when a tile is split inside the workgroup.
+static size_t exact_lds_bytes(const GemvArgs &a, int groups_per_stripe, int mt) {
+    size_t bytes = (size_t)a.pl * (kSlotBytes + a.scale_slot_bytes);
+    if (a.pg == 1 && a.pl > 1) {
+        const int g0 = std::min(a.sps * groups_per_stripe, a.G);
+        bytes += (size_t)(a.G - g0) * 64 * (mt + 1) * sizeof(float);
+    }
+    return bytes;
 }
 
 // ---- per-call timing (HIP events on the launch stream) -------------------
@@ -589,7 +658,6 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     a.row_bytes = (int)(w8 ? K : (K + 1) / 2);
     a.G = group ? (int)((K + group - 1) / group) : 0;
     a.ntiles = (int)((N + 63) / 64);
-    a.nsplit = 1;
 
     const size_t stripe_k = w8 ? kStripe : 2 * kStripe;   // weights per 128-byte stripe
     const bool aligned = (((uintptr_t)W | (uintptr_t)A) & 15) == 0 &&
@@ -608,23 +676,50 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     }
 
     a.nstripes = (int)(K / stripe_k);
+    a.pl = 1;
+    a.pg = 1;
+    a.sps = a.nstripes;
+    a.scale_slot_bytes = fmt == F_W4G128 ? 2 * 64 * 4 : (fmt == F_W4G32 ? 8 * 64 * 4 : 0);
+    const int groups_per_stripe = fmt == F_W4G128 ? 2 : (fmt == F_W4G32 ? 8 : 0);
     if (group) {
-        // Split K across waves when the row tiles alone cannot fill the GPU.
-        const int target = env_int("PILM_HIP_SPLIT_TARGET", 2048);
-        int nsplit = env_int("PILM_HIP_NSPLIT", 0);
-        if (nsplit <= 0) nsplit = std::max(1, std::min(a.nstripes, (target + a.ntiles - 1) / a.ntiles));
-        nsplit = std::min(nsplit, a.nstripes);
-        a.sps = (a.nstripes + nsplit - 1) / nsplit;
-        a.nsplit = (a.nstripes + a.sps - 1) / a.sps;
-    } else {
-        a.sps = a.nstripes;
+        // K is divided among the waves of one workgroup (block sums meet in
+        // LDS): 4 parts per tile once there are >= 256 tiles, which lets the
+        // hardware balance quarter tiles across SIMDs, 8 below that.  Few
+        // tiles with long rows are also divided across workgroups (block
+        // sums meet in global memory), aiming at ~1024 waves, as long as every
+        // part keeps a stripe.  (Chosen from measured per-shape times.)
+        int pl = a.ntiles >= 256 ? 4 : kMaxParts;
+        pl = std::min(pl, a.nstripes);
+        const int spw = (a.nstripes + pl - 1) / pl;
+        int pg = 1;
+        if (a.ntiles < 256 && spw >= 3) pg = std::min(spw, (1024 + a.ntiles * pl - 1) / (a.ntiles * pl));
+        const int env_pl = env_int("PILM_HIP_PL", 0), env_pg = env_int("PILM_HIP_PG", 0);
+        const int env_ns = env_int("PILM_HIP_NSPLIT", 0);
+        if (env_pl > 0 || env_pg > 0) {
+            pl = std::max(1, std::min(env_pl > 0 ? env_pl : 1, kMaxParts));
+            pg = std::max(1, env_pg > 0 ? env_pg : 1);
+        } else if (env_ns > 0) {
+            pl = 1;
+            pg = env_ns;
+        }
+        pl = std::min(pl, a.nstripes);
+        pg = std::max(1, std::min(pg, (a.nstripes + pl - 1) / pl));
+        a.sps = (a.nstripes + pl * pg - 1) / (pl * pg);
+        a.pl = pl;
+        a.pg = pg;
+        // A locally split tile parks the block sums of parts 1.. in LDS; fewer
+        // parts when that would not fit (long K with group 32).
+        while (a.pg == 1 && a.pl > 1 && exact_lds_bytes(a, groups_per_stripe, (int)std::min<size_t>(4, M)) > kMaxLds) {
+            a.pl = (a.pl + 1) / 2;
+            a.sps = (a.nstripes + a.pl - 1) / a.pl;
+        }
     }
-    if (a.nsplit > 1) {
+    if (a.pg > 1) {
         const int rc = split_scratch(st, (size_t)a.G * M * N, (size_t)a.ntiles, &a.P, &a.T, fn);
         if (rc != ECPU_OK) return rc;
     }
-    const int tasks = a.ntiles * a.nsplit;
-    const dim3 grid((tasks + kWaves - 1) / kWaves);
+    const dim3 grid((unsigned)(a.ntiles * a.pg));
+    const dim3 block((unsigned)(64 * a.pl));
     hipEvent_t ev0 = nullptr;
     if (g_prof_on) {
         std::lock_guard<std::mutex> lk(g_prof_mu);
@@ -633,7 +728,9 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     }
     for (size_t m0 = 0; m0 < M; m0 += 4) {
         const int mt = (int)std::min<size_t>(4, M - m0);
-        launch_exact(fmt, mt, grid, st, a, (int)m0);
+        if (launch_exact(fmt, mt, grid, block, exact_lds_bytes(a, groups_per_stripe, mt), st, a, (int)m0) !=
+            ECPU_OK)
+            return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
     }
     if (ev0) {
         std::lock_guard<std::mutex> lk(g_prof_mu);

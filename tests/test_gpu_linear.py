@@ -60,17 +60,22 @@ def test_golden(case, dev):
     GV.check_output(case, y)
 
 
-@pytest.mark.parametrize("nsplit", ["1", "2", "3", "16"])
-def test_group_split_variants_identical(nsplit, dev, monkeypatch):
-    """Splitting K across waves must not change a single bit."""
-    monkeypatch.setenv("PILM_HIP_NSPLIT", nsplit)
-    for case in GV.linear_cases(prefix="config2_w4g128_M1"):
-        if case["N"] > 20000:
-            continue
-        _say(f"[gpu] nsplit={nsplit} {case['name']}")
-        GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
-    for case in GV.linear_cases(prefix="w4g32_cancel"):
-        GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
+SPLITS = [{"PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_NSPLIT": "2"}, {"PILM_HIP_NSPLIT": "3"},
+          {"PILM_HIP_NSPLIT": "16"}, {"PILM_HIP_PL": "2"}, {"PILM_HIP_PL": "3"}, {"PILM_HIP_PL": "8"},
+          {"PILM_HIP_PL": "2", "PILM_HIP_PG": "3"}, {"PILM_HIP_PL": "8", "PILM_HIP_PG": "2"}]
+
+
+@pytest.mark.parametrize("env", SPLITS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
+def test_group_split_variants_identical(env, dev, monkeypatch):
+    """Splitting K across waves (in LDS or in global memory) must not change a single bit."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    for prefix in ("config2_w4g128_M1", "config2_w4g128_M4", "w4g32_cancel", "w4g128_cancel"):
+        for case in GV.linear_cases(prefix=prefix):
+            if case["N"] > 20000:
+                continue
+            _say(f"[gpu] split {env} {case['name']}")
+            GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
 
 
 def test_literal_path_identical(dev, monkeypatch):
