@@ -32,4 +32,13 @@ int check_launch(const char *fn);
 // device (different streams) must not both take the split path.
 int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, int **T, const char *fn);
 
+// Integer value of environment variable `name` (tuning overrides), else dflt.
+int env_int(const char *name, int dflt);
+
+// Exact GEMV of the per-row formats (fmt 0 W8A32, 1 W8A16, 2 W4A16 per-row)
+// for K a multiple of the 128-byte stripe and 16-byte aligned W and A;
+// enqueued on `st`.
+int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+             hipStream_t st, const char *fn);
+
 }  // namespace pilm

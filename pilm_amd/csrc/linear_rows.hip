@@ -1,0 +1,652 @@
+// Exact GEMV / small-M GEMM for the per-row formats on gfx950: int8 weights
+// with fp32 or bf16 activations (W8A32, W8A16) and nibble-packed int4 with
+// one scale per row (W4A16, bundle v2).
+//
+// These formats accumulate every output row in independent FMA chains that
+// each run over all of K -- 8 chains for int8 (chain l owns k = l mod 8,
+// kernels.c:78-109, 330-393) and 16 for int4 (lo[l] owns k = 16c + l, hi[l]
+// owns 16c + 8 + l, kernels.c:111-225) -- so K cannot be divided without
+// changing the roundings.  The chains of a row are divided instead: a
+// workgroup of four waves owns a tile of 64 rows (lane = row) and wave w owns
+//   int8: chains 4(w>>1) + 2(w&1) + {0, 1}, i.e. bytes 2(w&1), 2(w&1)+1 of
+//         the row's dwords of parity w>>1;
+//   int4: the lo (w < 2) or hi (w >= 2) chains of every 16-element chunk,
+//         nibble pairs (0,4),(1,5) for even w, (2,6),(3,7) for odd w.
+// At the end the chains meet in LDS and wave 0 combines them exactly as the
+// reference does: hsum ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) of the 8 lanes
+// (int4: of lo[l]+hi[l]), times the row scale, then bf16 for W8A16 / W4A16.
+//
+// The four waves stream the tile through a ring of D stripe slots (64 rows
+// x 128 B each) filled by global -> LDS DMA; each wave issues two of a
+// stripe's eight DMA instructions.  One barrier per stripe: once every wave
+// has waited for its own part of stripe s, the stripe is complete in LDS, and
+// every wave has finished reading stripe s-1, whose slot then receives
+// stripe s+D-1.  D-1 stripes stay in flight per tile, enough to cover HBM
+// latency when only a few tiles share the GPU.  Activations come through
+// scalar loads (the same k for every lane), up to 32 dwords at a time.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <mutex>
+
+#include "gemv_device.h"
+#include "internal.h"
+
+namespace pilm {
+
+namespace {
+
+constexpr int kRowWaves = 4;                 // waves per tile, one per SIMD
+
+template <int FMT, int MT>
+struct RowPlan {
+    static constexpr bool w8 = FMT != F_W4ROW;
+    static constexpr int chains = w8 ? 2 : 4;                  // chains per wave
+    static constexpr int apd = FMT == F_W8A16 ? 1 : 2;         // activation dwords per step and row
+    static constexpr int sub = MT <= 1 ? 1 : (MT <= 2 ? 2 : 4);  // sub-blocks per stripe
+    static constexpr int steps = 16 / sub;                     // row dwords per sub-block
+    static constexpr int words = steps * apd;                  // activation dwords per sub-block and row
+
+    // Activation dwords of sub-block b of stripe s for rows m0 .. m0+MT-1.
+    //   W8A32: fp32 k = 128s + 4d + 2(w&1) + {0,1}, d = 2t + (w>>1)
+    //   W8A16: the bf16 pair holding those two k
+    //   W4A16: chunk t, k0 = 256s + 16t + 8(w>>1): the bf16 pairs at k0 + {0,4}
+    //          (even w) or k0 + {2,6} (odd w)
+    static __device__ __forceinline__ void load_act(uint32_t (&act)[MT][words], const cu32 *A, size_t row_dw, int s,
+                                                    int b, int par, int sub_) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const cu32 *a = A + (size_t)m * row_dw;
+#pragma unroll
+            for (int tt = 0; tt < steps; ++tt) {
+                const int t = b * steps + tt;
+                if constexpr (FMT == F_W8A32) {
+                    const size_t k = (size_t)s * 128 + 8 * t + 4 * par + 2 * sub_;
+                    act[m][2 * tt] = a[k];
+                    act[m][2 * tt + 1] = a[k + 1];
+                } else if constexpr (FMT == F_W8A16) {
+                    act[m][tt] = a[(size_t)s * 64 + 4 * t + 2 * par + sub_];
+                } else {
+                    const size_t dw = (size_t)s * 128 + 8 * t + 4 * par + sub_;
+                    act[m][2 * tt] = a[dw];
+                    act[m][2 * tt + 1] = a[dw + 2];
+                }
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int D>
+__device__ __forceinline__ void wait_ring(bool tail) {
+    if (tail)
+        wait_vmcnt<0>();
+    else
+        wait_vmcnt<2 * (D - 2)>();
+}
+
+// The stripe loop of one wave; SUB = w & 1 selects the bytes (int8) or the
+// nibble pairs (int4) of each dword, so that selection costs no instruction.
+template <int FMT, int MT, int D, int SUB, int CH, int ROWS>
+__device__ __forceinline__ void rows_loop(float (&acc)[MT][CH], unsigned char *lds,
+                                          const uint8_t *const (&src)[2], const uint32_t (&off)[8], const cu32 *A,
+                                          size_t row_dw, int ns, int wave, int par) {
+    using R = RowPlan<FMT, MT>;
+    constexpr int kInst = ROWS / 8;                 // DMA instructions per stripe
+    constexpr int kSlot = ROWS * kStripe;
+    const int nmine = (wave < kInst) + (wave + 4 < kInst);   // this wave's share: i = wave, wave + 4
+    auto issue = [&](int st) {
+        unsigned char *slot = lds + (st % D) * kSlot;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+            if (wave + 4 * ii < kInst)
+                __builtin_amdgcn_global_load_lds((const void *)(src[ii] + (size_t)st * kStripe),
+                                                 (lds_void *)(slot + (wave + 4 * ii) * 1024), 16, 0, kNT);
+    };
+#pragma unroll
+    for (int t = 0; t < D - 1; ++t)
+        if (t < ns) issue(t);
+    const uint32_t magic = opaque_magic();
+
+    for (int s = 0; s < ns; ++s) {
+        // this wave's part of stripe s has landed (its later stripes may fly)
+        if (s + D - 2 >= ns || nmine == 0)
+            wait_vmcnt<0>();
+        else if (nmine == 1)
+            wait_vmcnt<D - 2>();
+        else
+            wait_vmcnt<2 * (D - 2)>();
+        lds_barrier();
+        if (s + D - 1 < ns) issue(s + D - 1);
+        uint32_t x[16];
+        const unsigned char *slot = lds + (s % D) * kSlot;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[2 * j] = *(const uint32_t *)(slot + off[j]);
+            x[2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+#pragma unroll
+        for (int b = 0; b < R::sub; ++b) {
+            uint32_t a[MT][R::words];
+            R::load_act(a, A, row_dw, s, b, par, SUB);
+            // all loads of this block are issued before any use: one wait
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int tt = 0; tt < R::steps; ++tt) {
+                const uint32_t w = x[b * R::steps + tt];
+                if constexpr (R::w8) {
+                    const float w0 = (float)(int)(int8_t)(uint8_t)(w >> (16 * SUB));
+                    const float w1 = (float)(int)(int8_t)(uint8_t)(w >> (16 * SUB + 8));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        float a0, a1;
+                        if constexpr (FMT == F_W8A32) {
+                            a0 = __uint_as_float(a[m][2 * tt]);
+                            a1 = __uint_as_float(a[m][2 * tt + 1]);
+                        } else {
+                            a0 = bf16_lo(a[m][tt]);
+                            a1 = bf16_hi(a[m][tt]);
+                        }
+                        acc[m][0] = __builtin_fmaf(a0, w0, acc[m][0]);
+                        acc[m][1] = __builtin_fmaf(a1, w1, acc[m][1]);
+                    }
+                } else {
+                    // two exact fp16 nibble pairs of this dword (see dequant_w4)
+                    const uint32_t u = w ^ 0x88888888u;
+                    const uint32_t v = SUB ? (u >> 8) : u;
+                    const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+                    const h2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+                    const h2 bias16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+                    const h2 qa = __builtin_bit_cast(h2, (v & 0x000F000Fu) | magic) + bias;
+                    const h2 qb = __builtin_bit_cast(h2, (v & 0x00F000F0u) | magic) * sixteenth + bias16;
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const uint32_t p0 = a[m][2 * tt], p1 = a[m][2 * tt + 1];
+                        acc[m][0] = __builtin_fmaf(bf16_lo(p0), (float)qa.x, acc[m][0]);   // chain 0 / 2
+                        acc[m][1] = __builtin_fmaf(bf16_lo(p1), (float)qa.y, acc[m][1]);   // chain 4 / 6
+                        acc[m][2] = __builtin_fmaf(bf16_hi(p0), (float)qb.x, acc[m][2]);   // chain 1 / 3
+                        acc[m][3] = __builtin_fmaf(bf16_hi(p1), (float)qb.y, acc[m][3]);   // chain 5 / 7
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+template <int FMT, int MT, int D, int ROWS>
+__global__ __launch_bounds__(64 * kRowWaves) void gemv_rows_kernel(const void *__restrict__ A_,
+                                                                  const uint8_t *__restrict__ W,
+                                                                  const float *__restrict__ S, void *__restrict__ C,
+                                                                  int M, int N, int K, int m0) {
+    using R = RowPlan<FMT, MT>;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int row = lane & (ROWS - 1);        // lanes beyond ROWS repeat rows and write nothing
+    const int par = wave >> 1, sub = wave & 1;
+    const int row0 = blockIdx.x * ROWS;
+    const int n = row0 + row;
+    const size_t row_bytes = R::w8 ? (size_t)K : (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    const size_t row_dw = FMT == F_W8A32 ? (size_t)K : (size_t)K / 2;   // activation dwords per row
+    const cu32 *A = as_const(A_) + (size_t)m0 * row_dw;
+
+    // This wave's DMA instructions per stripe: i = w and w + 4 (those below
+    // ROWS / 8), each fetching rows 8i + lane/8, chunk (lane & 7) ^ ((row >> 1) & 7).
+    const uint8_t *src[2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const int r = (8 * (wave + 4 * ii) + (lane >> 3)) & (ROWS - 1);
+        const int q = (lane & 7) ^ ((r >> 1) & 7);
+        src[ii] = W + (size_t)min(row0 + r, N - 1) * row_bytes + q * 16;
+    }
+    // Byte offsets of the lane's dwords in a slot: row `row`, chunk j stored at
+    // position j ^ ((row >> 1) & 7); this wave reads words par and 2 + par.
+    const int swz = (row >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = row * kStripe + ((j ^ swz) << 4) + 4 * par;
+
+    float acc[MT][R::chains];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int c = 0; c < R::chains; ++c) acc[m][c] = 0.0f;
+    if (sub)
+        rows_loop<FMT, MT, D, 1, R::chains, ROWS>(acc, lds, src, off, A, row_dw, ns, wave, par);
+    else
+        rows_loop<FMT, MT, D, 0, R::chains, ROWS>(acc, lds, src, off, A, row_dw, ns, wave, par);
+
+    // The chains meet in LDS (the ring is free once every wave is past its
+    // last stripe): ex[chain][m][64], 8 chains for int8, 16 (lo then hi) for int4.
+    float *ex = (float *)lds;
+    lds_barrier();
+#pragma unroll
+    for (int c = 0; c < R::chains; ++c) {
+        int chain;
+        if constexpr (R::w8) {
+            chain = 4 * par + 2 * sub + c;
+        } else {
+            const int lo_ids[4] = {0, 4, 1, 5};
+            chain = 8 * par + lo_ids[c] + 2 * sub;
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) ex[(chain * MT + m) * 64 + lane] = acc[m][c];
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= ROWS || n >= N) return;
+    const float scale = S[n];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        float l[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            l[c] = ex[(c * MT + m) * 64 + lane];
+            if constexpr (!R::w8) l[c] = l[c] + ex[((8 + c) * MT + m) * 64 + lane];
+        }
+        const float y = hsum8(l) * scale;
+        const size_t o = (size_t)(m0 + m) * N + n;
+        if constexpr (FMT == F_W8A32)
+            ((float *)C)[o] = y;
+        else
+            ((uint16_t *)C)[o] = f32_to_bf16(y);
+    }
+}
+
+constexpr size_t kRowMaxLds = 160 * 1024;
+
+template <int FMT, int MT, int D, int ROWS>
+int launch_rows_one(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int M, int N, int K,
+                    int m0) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_rows_kernel<FMT, MT, D, ROWS>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = std::max<size_t>((size_t)D * ROWS * kStripe, (size_t)16 * MT * 64 * sizeof(float));
+    const dim3 grid((unsigned)((N + ROWS - 1) / ROWS));
+    gemv_rows_kernel<FMT, MT, D, ROWS><<<grid, 64 * kRowWaves, lds, st>>>(A, W, S, C, M, N, K, m0);
+    return ECPU_OK;
+}
+
+template <int FMT, int D, int ROWS>
+int launch_rows_mt(int mt, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int M, int N,
+                   int K, int m0) {
+    switch (mt) {
+        case 1: return launch_rows_one<FMT, 1, D, ROWS>(st, A, W, S, C, M, N, K, m0);
+        case 2: return launch_rows_one<FMT, 2, D, ROWS>(st, A, W, S, C, M, N, K, m0);
+        case 3: return launch_rows_one<FMT, 3, D, ROWS>(st, A, W, S, C, M, N, K, m0);
+        default: return launch_rows_one<FMT, 4, D, ROWS>(st, A, W, S, C, M, N, K, m0);
+    }
+}
+
+template <int FMT>
+int launch_rows_fmt(int rows, int depth, int mt, hipStream_t st, const void *A, const uint8_t *W, const float *S,
+                    void *C, int M, int N, int K, int m0) {
+    if (rows == 16) return launch_rows_mt<FMT, 16, 16>(mt, st, A, W, S, C, M, N, K, m0);
+    if (rows == 32) return launch_rows_mt<FMT, 16, 32>(mt, st, A, W, S, C, M, N, K, m0);
+    switch (depth) {
+        case 16: return launch_rows_mt<FMT, 16, 64>(mt, st, A, W, S, C, M, N, K, m0);
+        case 8: return launch_rows_mt<FMT, 8, 64>(mt, st, A, W, S, C, M, N, K, m0);
+        default: return launch_rows_mt<FMT, 4, 64>(mt, st, A, W, S, C, M, N, K, m0);
+    }
+}
+
+// ------------------------------------------------------------------ quad
+// A CU streams only ~25-30 GB/s however deep its prefetch, so a GEMV must
+// spread over all CUs; 64-row tiles leave most of them idle when N is a few
+// thousand rows.  The quad kernel uses 16-row tiles: lane = 4r + c serves row
+// r of the tile with chain group c = lane & 3,
+//   int8: chains {2c, 2c+1} = bytes 2(c&1), 2(c&1)+1 of the dwords of parity
+//         c >> 1 (k = 8T + 2c + {0,1});
+//   int4: the lo (c < 2) or hi (c >= 2) chains of each chunk, nibble pairs
+//         (0,4),(1,5) for even c and (2,6),(3,7) for odd c;
+// and the four partial chain sets of a row meet through DPP quad permutes in
+// the reference's hsum order.  The activations of a chain group are not the
+// same for all lanes any more, so each workgroup first copies its activation
+// rows into LDS (global -> LDS DMA) and every lane reads its own words:
+//   W8A32  fp32 a[8T + 2c], a[8T + 2c + 1]            (T = k / 8)
+//   W8A16  the bf16 pair dword 4T + c
+//   W4A16  the bf16 pair dwords 8T + 4(c>>1) + (c&1) + {0, 2}   (T = k / 16)
+// Each wave owns a 16-row tile and its own ring of D stripe slots (16 rows x
+// 128 B, two DMA instructions per stripe), so no barrier is needed per stripe.
+
+constexpr int kQuadSlotBytes = 16 * kStripe;   // one stripe: 16 rows x 128 B
+
+template <int FMT>
+struct QuadFmt {
+    static constexpr bool w8 = FMT != F_W4ROW;
+    static constexpr int chains = w8 ? 2 : 4;
+    static constexpr int apd = FMT == F_W8A16 ? 1 : 2;   // activation dwords per lane and step
+    // activation dwords per row
+    static __device__ __forceinline__ int row_dw(int K) { return FMT == F_W8A32 ? K : K / 2; }
+    // first activation dword of step T for chain group c; the second one
+    // (apd 2) follows at +1 (fp32) or +2 (bf16 pairs of int4 nibble pairs)
+    static __device__ __forceinline__ int act_index(int T, int c) {
+        if constexpr (FMT == F_W8A32)
+            return 8 * T + 2 * c;
+        else if constexpr (FMT == F_W8A16)
+            return 4 * T + c;
+        else
+            return 8 * T + 4 * (c >> 1) + (c & 1);
+    }
+    static constexpr int second = FMT == F_W8A32 ? 1 : 2;
+};
+
+__device__ __forceinline__ float dpp_quad_add(float x, int ctrl_is_swap2) {
+    // x + x of the partner lane in the quad: [2,3,0,1] (ctrl 0x4E) or [1,0,3,2] (0xB1)
+    const int xi = __builtin_bit_cast(int, x);
+    const int y = ctrl_is_swap2 ? __builtin_amdgcn_update_dpp(0, xi, 0x4E, 0xF, 0xF, false)
+                                : __builtin_amdgcn_update_dpp(0, xi, 0xB1, 0xF, 0xF, false);
+    return x + __builtin_bit_cast(float, y);
+}
+
+template <int FMT, int MT, int D>
+__global__ __launch_bounds__(256) void gemv_quad_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W,
+                                                       const float *__restrict__ S, void *__restrict__ C, int M,
+                                                       int N, int K, int m0, int ntiles) {
+    using Q = QuadFmt<FMT>;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wpb = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 2, c = lane & 3, par = c >> 1;
+    const int tile = blockIdx.x * wpb + wave;
+    const int row0 = tile * 16;
+    const size_t row_bytes = Q::w8 ? (size_t)K : (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    const int rdw = Q::row_dw(K);
+    unsigned char *act = lds + (size_t)wpb * D * kQuadSlotBytes;
+
+    // Activation rows m0 .. m0+MT-1 (contiguous in A) into LDS: 16-byte DMA,
+    // 256 dwords per instruction, instructions dealt round-robin to the waves.
+    {
+        const int total = MT * rdw;
+        const uint32_t *a = (const uint32_t *)A_ + (size_t)m0 * rdw;
+        int issued = 0;
+        for (int q = wave; q * 256 < total; q += wpb) {
+            const int g = q * 256 + 4 * lane;
+            if (g < total)
+                __builtin_amdgcn_global_load_lds((const void *)(a + g), (lds_void *)(act + (size_t)q * 1024), 16, 0,
+                                                 0);
+            if ((++issued & 15) == 0) wait_vmcnt<16>();   // keep the wave's outstanding loads bounded
+        }
+    }
+
+    // This wave's stripe DMA: instruction i fetches rows 8i + lane/8 of the
+    // tile, chunk (lane & 7) ^ ((row >> 1) & 7).
+    const uint8_t *src[2];
+    const bool live = tile < ntiles;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rr = 8 * i + (lane >> 3);
+        const int q = (lane & 7) ^ ((rr >> 1) & 7);
+        src[i] = W + (size_t)min(row0 + rr, N - 1) * row_bytes + q * 16;
+    }
+    unsigned char *ring = lds + (size_t)wave * D * kQuadSlotBytes;
+    auto issue = [&](int st) {
+        unsigned char *slot = ring + (st % D) * kQuadSlotBytes;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)st * kStripe),
+                                             (lds_void *)(slot + i * 1024), 16, 0, kNT);
+    };
+    if (live) {
+#pragma unroll
+        for (int t = 0; t < D - 2; ++t)
+            if (t < ns) issue(t);
+    }
+    // This wave's activation copies are older than its (at most 2(D-2))
+    // stripe loads; after the barrier every wave's copies have landed.
+    if (live && ns >= D - 2)
+        wait_vmcnt<2 * (D - 2)>();
+    else
+        wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");
+    if (!live) return;
+
+    // Lane's word offsets in a slot: row r, chunk j at position j ^ ((r >> 1) & 7),
+    // words par and par + 2.
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = r * kStripe + ((j ^ swz) << 4) + 4 * par;
+    const uint32_t *my_act = (const uint32_t *)act + Q::act_index(0, c);
+    const uint32_t shift = Q::w8 ? 16u * (c & 1) : 8u * (c & 1);
+    const uint32_t magic = opaque_magic();
+
+    float acc[MT][Q::chains];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int k = 0; k < Q::chains; ++k) acc[m][k] = 0.0f;
+
+    // One stripe's words (x) and activations (av) for the lane.
+    auto load = [&](int st, uint32_t (&x)[16], uint32_t (&av)[MT][16 * Q::apd]) {
+        const unsigned char *slot = ring + (st % D) * kQuadSlotBytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[2 * j] = *(const uint32_t *)(slot + off[j]);
+            x[2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const uint32_t *ap = my_act + (size_t)m * rdw + Q::act_index(16 * st + t, 0);
+                if constexpr (Q::apd == 2) {
+                    av[m][2 * t] = ap[0];
+                    av[m][2 * t + 1] = ap[Q::second];
+                } else {
+                    av[m][t] = ap[0];
+                }
+            }
+    };
+    auto compute = [&](const uint32_t (&x)[16], const uint32_t (&av)[MT][16 * Q::apd]) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t w = x[t];
+            if constexpr (Q::w8) {
+                const uint32_t ws = w >> shift;
+                const float w0 = (float)(int)(int8_t)(uint8_t)ws;
+                const float w1 = (float)(int)(int8_t)(uint8_t)(ws >> 8);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float a0, a1;
+                    if constexpr (FMT == F_W8A32) {
+                        a0 = __uint_as_float(av[m][2 * t]);
+                        a1 = __uint_as_float(av[m][2 * t + 1]);
+                    } else {
+                        a0 = bf16_lo(av[m][t]);
+                        a1 = bf16_hi(av[m][t]);
+                    }
+                    acc[m][0] = __builtin_fmaf(a0, w0, acc[m][0]);
+                    acc[m][1] = __builtin_fmaf(a1, w1, acc[m][1]);
+                }
+            } else {
+                const uint32_t v = (w ^ 0x88888888u) >> shift;
+                const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+                const h2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+                const h2 bias16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+                const h2 qa = __builtin_bit_cast(h2, (v & 0x000F000Fu) | magic) + bias;
+                const h2 qb = __builtin_bit_cast(h2, (v & 0x00F000F0u) | magic) * sixteenth + bias16;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const uint32_t p0 = av[m][2 * t], p1 = av[m][2 * t + 1];
+                    acc[m][0] = __builtin_fmaf(bf16_lo(p0), (float)qa.x, acc[m][0]);   // chain 0 / 2
+                    acc[m][1] = __builtin_fmaf(bf16_lo(p1), (float)qa.y, acc[m][1]);   // chain 4 / 6
+                    acc[m][2] = __builtin_fmaf(bf16_hi(p0), (float)qb.x, acc[m][2]);   // chain 1 / 3
+                    acc[m][3] = __builtin_fmaf(bf16_hi(p1), (float)qb.y, acc[m][3]);   // chain 5 / 7
+                }
+            }
+        }
+    };
+    // Software pipeline, two stripes per round: while stripe s is computed
+    // from registers, stripe s+1 is read from LDS (LDS reads complete in
+    // order, so only the reads of s+1 are waited for, when they are used).
+    // Slots are refilled only at the top of a round, with the stripes of the
+    // two slots consumed in the previous round, so no DMA can overtake a read
+    // of its slot; D-2 stripes stay in flight.
+    uint32_t xa[16], xb[16];
+    uint32_t aa[MT][16 * Q::apd], ab[MT][16 * Q::apd];
+    if (ns >= D - 2)
+        wait_vmcnt<2 * (D - 3)>();   // stripe 0 of the D-2 issued
+    else
+        wait_vmcnt<0>();
+    load(0, xa, aa);
+    int s = 0;
+    for (; s + 1 < ns; s += 2) {
+        if (s + D - 2 < ns) issue(s + D - 2);   // slot of stripe s-2
+        if (s + D - 1 < ns) issue(s + D - 1);   // slot of stripe s-1
+        if (s + D <= ns)
+            wait_vmcnt<2 * (D - 2)>();          // stripe s+1 (s+2 .. s+D-1 may fly)
+        else
+            wait_vmcnt<0>();
+        load(s + 1, xb, ab);
+        compute(xa, aa);
+        if (s + 2 < ns) {
+            if (s + D <= ns)
+                wait_vmcnt<2 * (D - 3)>();      // stripe s+2 (s+3 .. s+D-1 may fly)
+            else
+                wait_vmcnt<0>();
+            load(s + 2, xa, aa);
+        }
+        compute(xb, ab);
+    }
+    if (s < ns) compute(xa, aa);
+
+
+    // Reference order of the 8-lane horizontal sum (int4: of lo[l] + hi[l]):
+    //   ((l0+l4)+(l1+l5)) + ((l2+l6)+(l3+l7)).
+    // int8: c holds (l_{2c}, l_{2c+1}); c ^ 2 holds (l_{2c+4}, l_{2c+5}).
+    // int4: c holds lo (c < 2) or hi (c >= 2) of chains {0,4,1,5} (even c) or
+    //       {2,6,3,7} (odd c); c ^ 2 holds the other half of the same chains.
+    const int n = row0 + r;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        float h;
+        if constexpr (Q::w8) {
+            const float p0 = dpp_quad_add(acc[m][0], 1);   // l_{2c} + l_{2c+4}
+            const float p1 = dpp_quad_add(acc[m][1], 1);   // l_{2c+1} + l_{2c+5}
+            h = dpp_quad_add(p0 + p1, 0);                   // c = 0: (l0+l4)+(l1+l5) + (l2+l6)+(l3+l7)
+        } else {
+            const float s0 = dpp_quad_add(acc[m][0], 1);   // s0 / s2  (lo + hi)
+            const float s4 = dpp_quad_add(acc[m][1], 1);   // s4 / s6
+            const float s1 = dpp_quad_add(acc[m][2], 1);   // s1 / s3
+            const float s5 = dpp_quad_add(acc[m][3], 1);   // s5 / s7
+            h = dpp_quad_add((s0 + s4) + (s1 + s5), 0);
+        }
+        if (c == 0 && n < N) {
+            const float y = h * S[n];
+            const size_t o = (size_t)(m0 + m) * N + n;
+            if constexpr (FMT == F_W8A32)
+                ((float *)C)[o] = y;
+            else
+                ((uint16_t *)C)[o] = f32_to_bf16(y);
+        }
+    }
+}
+
+template <int FMT, int MT, int D>
+int launch_quad_one(int wpb, int ntiles, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C,
+                    int M, int N, int K, int m0) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_quad_kernel<FMT, MT, D>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t rdw = FMT == F_W8A32 ? (size_t)K : (size_t)K / 2;
+    const size_t lds = (size_t)wpb * D * kQuadSlotBytes + (size_t)MT * rdw * 4;
+    if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
+    const dim3 grid((unsigned)((ntiles + wpb - 1) / wpb));
+    gemv_quad_kernel<FMT, MT, D><<<grid, 64 * wpb, lds, st>>>(A, W, S, C, M, N, K, m0, ntiles);
+    return ECPU_OK;
+}
+
+template <int FMT, int D>
+int launch_quad_mt(int mt, int wpb, int ntiles, hipStream_t st, const void *A, const uint8_t *W, const float *S,
+                   void *C, int M, int N, int K, int m0) {
+    switch (mt) {
+        case 1: return launch_quad_one<FMT, 1, D>(wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+        case 2: return launch_quad_one<FMT, 2, D>(wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+        case 3: return launch_quad_one<FMT, 3, D>(wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+        default: return launch_quad_one<FMT, 4, D>(wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+    }
+}
+
+template <int FMT>
+int launch_quad_fmt(int depth, int mt, int wpb, int ntiles, hipStream_t st, const void *A, const uint8_t *W,
+                    const float *S, void *C, int M, int N, int K, int m0) {
+    switch (depth) {
+        case 16: return launch_quad_mt<FMT, 16>(mt, wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+        case 8: return launch_quad_mt<FMT, 8>(mt, wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+        default: return launch_quad_mt<FMT, 4>(mt, wpb, ntiles, st, A, W, S, C, M, N, K, m0);
+    }
+}
+
+}  // namespace
+
+// Per-row formats on the stripe path: K a multiple of the stripe (128 int8
+// or 256 int4 weights), 16-byte aligned weights and activations.
+int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+             hipStream_t st, const char *fn) {
+    // Below 65536 rows the 16-row quad kernel (measured faster there); above,
+    // the 64-row chain-split kernel, whose scalar activations cost less VALU.
+    if (env_int("PILM_HIP_QUAD", N < 65536 ? 1 : 0) != 0) {
+        // 16-row tiles; one wave per workgroup while there are few tiles (more
+        // CUs), four beyond (fewer copies of the activations).
+        const int qt = (int)((N + 15) / 16);
+        const int wpb = qt >= 2048 ? 4 : 1;
+        int depth = (qt <= 512) ? 16 : 8;
+        const int env_depth = env_int("PILM_HIP_RING", 0);
+        if (env_depth == 4 || env_depth == 8 || env_depth == 16) depth = env_depth;
+        bool ok = true;
+        for (size_t m0 = 0; m0 < M && ok; m0 += 4) {
+            const int mt = (int)std::min<size_t>(4, M - m0);
+            int rc;
+            switch (fmt) {
+                case F_W8A32: rc = launch_quad_fmt<F_W8A32>(depth, mt, wpb, qt, st, A, W, S, C, (int)M, (int)N, (int)K, (int)m0); break;
+                case F_W8A16: rc = launch_quad_fmt<F_W8A16>(depth, mt, wpb, qt, st, A, W, S, C, (int)M, (int)N, (int)K, (int)m0); break;
+                default: rc = launch_quad_fmt<F_W4ROW>(depth, mt, wpb, qt, st, A, W, S, C, (int)M, (int)N, (int)K, (int)m0); break;
+            }
+            if (rc == ECPU_ERR_DEVICE) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+            if (rc != ECPU_OK) {
+                if (m0 != 0) return fail(ECPU_ERR_DEVICE, "%s: activation staging does not fit in LDS", fn);
+                ok = false;   // activations too long for LDS: chain-split kernel below
+            }
+        }
+        if (ok) return ECPU_OK;
+    }
+    const int ntiles = (int)((N + 63) / 64);
+    // Tile height: a CU streams only ~25-30 GB/s, so fewer than 256 tiles of
+    // 64 rows would leave CUs idle; 16- or 32-row tiles (the other lanes idle)
+    // spread the rows over more CUs.  Ring depth: the slots of all resident
+    // tiles share the 160 KB of LDS: 16 while the tiles fit on the CUs at once,
+    // 8 up to two tiles per CU, 4 beyond.
+    int rows = ntiles >= 256 ? 64 : (ntiles >= 128 ? 32 : 16);
+    const int env_rows = env_int("PILM_HIP_ROWTILE", 0);
+    if (env_rows == 16 || env_rows == 32 || env_rows == 64) rows = env_rows;
+    int depth = ntiles <= 256 ? 16 : (ntiles <= 512 ? 8 : 4);
+    const int env_depth = env_int("PILM_HIP_RING", 0);
+    if (env_depth == 4 || env_depth == 8 || env_depth == 16) depth = env_depth;
+    for (size_t m0 = 0; m0 < M; m0 += 4) {
+        const int mt = (int)std::min<size_t>(4, M - m0);
+        int rc;
+        switch (fmt) {
+            case F_W8A32: rc = launch_rows_fmt<F_W8A32>(rows, depth, mt, st, A, W, S, C, (int)M, (int)N, (int)K, (int)m0); break;
+            case F_W8A16: rc = launch_rows_fmt<F_W8A16>(rows, depth, mt, st, A, W, S, C, (int)M, (int)N, (int)K, (int)m0); break;
+            default: rc = launch_rows_fmt<F_W4ROW>(rows, depth, mt, st, A, W, S, C, (int)M, (int)N, (int)K, (int)m0); break;
+        }
+        if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+    }
+    return ECPU_OK;
+}
+
+}  // namespace pilm

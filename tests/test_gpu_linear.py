@@ -78,6 +78,28 @@ def test_group_split_variants_identical(env, dev, monkeypatch):
             GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
 
 
+ROW_PATHS = [{"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "4"},
+             {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "8"},
+             {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "16"},
+             {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "32"}, {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "16"},
+             {"PILM_HIP_QUAD": "1", "PILM_HIP_RING": "4"}, {"PILM_HIP_QUAD": "1", "PILM_HIP_RING": "16"},
+             {"PILM_HIP_ROWS": "0"}]
+
+
+@pytest.mark.parametrize("env", ROW_PATHS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
+def test_row_format_paths_identical(env, dev, monkeypatch):
+    """Per-row formats: every tile height and ring depth of the chain-split
+    kernels (four waves per tile, or four lanes per row), and the
+    one-wave-per-tile kernel, give the same bits."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    for case in GV.linear_cases(max_elems=1 << 24):
+        if case["fmt"] not in ("w8a32", "w8a16", "w4") or case["K"] % 256:
+            continue
+        _say(f"[gpu] rows {env} {case['name']}")
+        GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
+
+
 def test_literal_path_identical(dev, monkeypatch):
     """The one-thread-per-output kernel gives the same bits on stripe-aligned shapes."""
     monkeypatch.setenv("PILM_HIP_LITERAL", "1")
