@@ -32,6 +32,16 @@ int check_launch(const char *fn);
 // device (different streams) must not both take the split path.
 int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, int **T, const char *fn);
 
+// Dequant-GEMM on the matrix cores for M >= mfma_min_m() (env
+// PILM_HIP_MFMA_MIN_M, default 64; 0 keeps every M on the exact kernels)
+// when mfma_supports(): K a multiple of 64, 16-byte aligned A and W.
+// Outputs are within 1e-2 (in practice ~1e-3) of the reference, not
+// bit-identical.
+int mfma_min_m();
+bool mfma_supports(size_t K, const void *A, const uint8_t *W);
+int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+             hipStream_t st, const char *fn);
+
 // Integer value of environment variable `name` (tuning overrides), else dflt.
 int env_int(const char *name, int dflt);
 

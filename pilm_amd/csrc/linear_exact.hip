@@ -548,6 +548,11 @@ static hipEvent_t pooled_event() {
     return e;
 }
 
+static const char *mfma_family_name(int fmt) {
+    static const char *names[5] = {"w8a32_mfma", "w8a16_mfma", "w4a16_mfma", "w4a16g128_mfma", "w4a16g32_mfma"};
+    return names[fmt];
+}
+
 static const char *family_name(int fmt, size_t M) {
     static const char *names[5][3] = {
         {"w8a32_gemv", "w8a32_m2to4", "w8a32_m5plus"},
@@ -589,7 +594,12 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     const bool aligned = (((uintptr_t)W | (uintptr_t)A) & 15) == 0 &&
                          (fmt != F_W4G32 || ((uintptr_t)S & 15) == 0) && ((uintptr_t)S & 3) == 0;
     const bool fast = K > 0 && K % stripe_k == 0 && aligned && env_int("PILM_HIP_LITERAL", 0) == 0;
-    if (!fast) {
+    // Prefill / verify shapes go to the matrix cores (within 1e-2 of the
+    // reference); decode shapes stay on the exact kernels.
+    const int min_m = mfma_min_m();
+    const bool use_mfma = min_m > 0 && M >= (size_t)min_m && mfma_supports(K, A, W) &&
+                          env_int("PILM_HIP_LITERAL", 0) == 0;
+    if (!fast && !use_mfma) {
         const size_t total = M * N;
         switch (fmt) {
             case F_W8A32: gemv_literal_kernel<F_W8A32><<<(total + 255) / 256, 256, 0, st>>>(a, 0); break;
@@ -607,7 +617,7 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     a.sps = a.nstripes;
     a.scale_slot_bytes = fmt == F_W4G128 ? 2 * 64 * 4 : (fmt == F_W4G32 ? 8 * 64 * 4 : 0);
     const int groups_per_stripe = fmt == F_W4G128 ? 2 : (fmt == F_W4G32 ? 8 : 0);
-    if (group) {
+    if (group && !use_mfma) {
         // K is divided among the waves of one workgroup (block sums meet in
         // LDS): 4 parts per tile once there are >= 256 tiles, which lets the
         // hardware balance quarter tiles across SIMDs, 8 below that.  Few
@@ -652,7 +662,10 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         ev0 = pooled_event();
         (void)hipEventRecord(ev0, st);
     }
-    if (!group && env_int("PILM_HIP_ROWS", 1) != 0) {
+    if (use_mfma) {
+        const int rc = run_mfma(fmt, M, N, K, A, W, S, C, st, fn);
+        if (rc != ECPU_OK) return rc;
+    } else if (!group && env_int("PILM_HIP_ROWS", 1) != 0) {
         // per-row formats: the chains of a row are divided among four waves
         const int rc = run_rows(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK) return rc;
@@ -671,7 +684,8 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         const double a_elt = (fmt == F_W8A32) ? 4.0 : 2.0;
         const double scale_bytes = 4.0 * (double)N * (group ? (double)a.G : 1.0);
         const double bytes = (double)N * a.row_bytes + scale_bytes + a_elt * (double)(M * K) + a_elt * (double)(M * N);
-        g_prof.push_back({ev0, ev1, family_name(fmt, M), bytes, 2.0 * (double)M * (double)N * (double)K});
+        g_prof.push_back({ev0, ev1, use_mfma ? mfma_family_name(fmt) : family_name(fmt, M), bytes,
+                          2.0 * (double)M * (double)N * (double)K});
     }
     return check_launch(fn);
 }

@@ -1,0 +1,395 @@
+// Dequant-GEMM on MFMA for the prefill / verify shapes (M >= 64 activation
+// rows) on gfx950.
+//
+// The exact GEMV kernels spend one VALU FMA per weight and activation row, so
+// at M >= 64 they would be ~30x slower than the matrix cores.  Here the
+// product runs on v_mfma_f32_32x32x16_f16 (fp16 x fp16 -> fp32 accumulate):
+//   * weights are unpacked exactly into fp16 integers (int4: -8..7, int8:
+//     -128..127) with the exponent-magic trick of the GEMV kernels; for the
+//     group formats the fp16 weights of a group are multiplied by the group
+//     scale rounded to fp16 (relative error <= 2^-11), per-row scales are
+//     applied in fp32 at the end;
+//   * activations are converted to fp16 once per tile: bf16 -> fp16 is exact
+//     for |a| in [2^-14, 65504]; an fp32 activation becomes two fp16 parts,
+//     hi = fp16(a) and lo = fp16(a - hi), multiplied by two MFMAs (22 of its
+//     24 bits survive, so cancelling fp32 activations stay accurate);
+//   * products are exact in the MFMA, sums are fp32 in an order that differs
+//     from the reference: outputs agree with the reference to ~1e-3 relative
+//     (the MFMA path tolerance is 1e-2).
+// The weight unpack pairs nibbles (k, k+4) (int4) or bytes (k, k+2) (int8)
+// into one fp16x2 register, so every 8-element block of the activation tile is
+// stored in the matching order: int4 (0,4,1,5,2,6,3,7), int8 (0,2,1,3,4,6,5,7).
+//
+// Tiling: a workgroup of four waves computes BM x BN outputs (waves WM x WN,
+// each (BM/WM) x (BN/WN) in 32 x 32 MFMA tiles) over K in steps of 64, with a
+// double-buffered LDS stage: the weights of step t+1 arrive by global -> LDS
+// DMA and the activations of step t+1 through registers (converted and
+// permuted on the way) while step t is multiplied.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <mutex>
+
+#include "gemv_device.h"
+#include "internal.h"
+
+namespace pilm {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 64;           // K per stage
+constexpr int kMfmaThreads = 256;
+
+template <int FMT>
+struct MF {
+    static constexpr bool w8 = FMT == F_W8A32 || FMT == F_W8A16;
+    static constexpr bool a32 = FMT == F_W8A32;
+    static constexpr int group = FMT == F_W4G128 ? 128 : (FMT == F_W4G32 ? 32 : 0);
+    static constexpr int wrow = w8 ? kBK : kBK / 2;   // weight bytes per row per stage
+    static constexpr int planes = a32 ? 2 : 1;        // fp16 parts per activation
+};
+
+// fp16 pair of two bf16 values (exact in the fp16 normal range), packed lo/hi.
+__device__ __forceinline__ uint32_t f16x2_of_f32(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+// Converts one 8-element activation block (k0..k7, as fp32 values) into the
+// fp16 order the weight unpack produces, 4 dwords.  (Values that are exact in
+// fp16 -- bf16 activations -- may use the truncating pack.)
+template <int FMT>
+__device__ __forceinline__ u32x4 act_block(const float (&v)[8]) {
+    u32x4 o;
+    if constexpr (MF<FMT>::w8) {   // (0,2) (1,3) (4,6) (5,7)
+        o[0] = f16x2_of_f32(v[0], v[2]);
+        o[1] = f16x2_of_f32(v[1], v[3]);
+        o[2] = f16x2_of_f32(v[4], v[6]);
+        o[3] = f16x2_of_f32(v[5], v[7]);
+    } else {                       // (0,4) (1,5) (2,6) (3,7)
+        o[0] = f16x2_of_f32(v[0], v[4]);
+        o[1] = f16x2_of_f32(v[1], v[5]);
+        o[2] = f16x2_of_f32(v[2], v[6]);
+        o[3] = f16x2_of_f32(v[3], v[7]);
+    }
+    return o;
+}
+
+// fp32 activations: v = hi + lo with hi = fp16(v) (round to nearest) and
+// lo = fp16(v - hi); v - hi is exact in fp32.  Overwrites v with lo.
+__device__ __forceinline__ void split_hi(float (&v)[8], float (&hi)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float h = (float)(_Float16)v[e];
+        hi[e] = h;
+        v[e] = (float)(_Float16)(v[e] - h);
+    }
+}
+
+// blockIdx.z selects a contiguous range of K steps (split K); with more than
+// one split the raw fp32 sums go to P[z][M][N] and split_reduce_kernel adds
+// them in split order (deterministic) and finishes the outputs.
+template <int FMT, int BM, int BN, int WM>
+__global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__restrict__ A_,
+                                                                const uint8_t *__restrict__ W,
+                                                                const float *__restrict__ S, void *__restrict__ C,
+                                                                float *__restrict__ P, int M, int N, int K,
+                                                                int steps_per_split) {
+    using F = MF<FMT>;
+    constexpr int WN = 4 / WM;
+    constexpr int TM = BM / WM / 32;     // 32x32 tiles per wave along M
+    constexpr int TN = BN / WN / 32;     // ... along N
+    constexpr int A_PLANE = BM * kBK * 2;
+    constexpr int A_BYTES = A_PLANE * F::planes;
+    constexpr int W_BYTES = BN * F::wrow;
+    constexpr int STAGE = A_BYTES + W_BYTES;
+    constexpr int A_BLOCKS = BM * kBK / 8 / kMfmaThreads;   // 8-element blocks per thread per stage
+    constexpr int W_LOADS = W_BYTES / 16 / kMfmaThreads;     // 16-byte DMA per thread per stage
+    static_assert(A_BLOCKS >= 1 && W_LOADS >= 1, "tile too small");
+    __shared__ __align__(16) unsigned char lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int wm = wave % WM, wn = wave / WM;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const size_t row_bytes = F::w8 ? (size_t)K : (size_t)K / 2;
+    const int t0 = blockIdx.z * steps_per_split;
+    const int nsteps = min(steps_per_split, K / kBK - t0);   // >= 1 (host guarantees)
+
+    // ---- staging of one K step into buffer b
+    float areg[A_BLOCKS][8];
+    auto load_a = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < A_BLOCKS; ++i) {
+            const int blk = tid + i * kMfmaThreads;
+            const int row = blk / (kBK / 8), kb = blk % (kBK / 8);
+            const int m = min(m0 + row, M - 1);
+            const size_t k = (size_t)(t0 + t) * kBK + 8 * kb;
+            if constexpr (F::a32) {
+                const f32x4 *p = (const f32x4 *)((const float *)A_ + (size_t)m * K + k);
+                const f32x4 x0 = p[0], x1 = p[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    areg[i][e] = x0[e];
+                    areg[i][4 + e] = x1[e];
+                }
+            } else {
+                const u32x4 x = *(const u32x4 *)((const uint16_t *)A_ + (size_t)m * K + k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    areg[i][2 * e] = bf16_lo(x[e]);
+                    areg[i][2 * e + 1] = bf16_hi(x[e]);
+                }
+            }
+        }
+    };
+    // Activation tile: row r holds 8 blocks of 16 B; block kb sits at position
+    // kb ^ ((r >> 1) & 7) so that 16 lanes reading one block of 16 rows cover
+    // all banks.
+    auto store_a = [&](int b) {
+        unsigned char *as = lds + b * STAGE;
+#pragma unroll
+        for (int i = 0; i < A_BLOCKS; ++i) {
+            const int blk = tid + i * kMfmaThreads;
+            const int row = blk / (kBK / 8), kb = blk % (kBK / 8);
+            const int off = row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4);
+            if constexpr (F::planes == 2) {
+                float hi[8];
+                split_hi(areg[i], hi);   // areg now holds the low parts (exact in fp16)
+                *(u32x4 *)(as + off) = act_block<FMT>(hi);
+                *(u32x4 *)(as + A_PLANE + off) = act_block<FMT>(areg[i]);
+            } else {
+                *(u32x4 *)(as + off) = act_block<FMT>(areg[i]);
+            }
+        }
+    };
+    // Weight tile: row-major, wrow bytes per row, by DMA (16 B per lane).
+    auto load_w = [&](int t, int b) {
+        unsigned char *ws = lds + b * STAGE + A_BYTES;
+#pragma unroll
+        for (int i = 0; i < W_LOADS; ++i) {
+            const int idx = tid + i * kMfmaThreads;            // 16-byte chunk of the tile
+            const int row = idx / (F::wrow / 16), ch = idx % (F::wrow / 16);
+            const int n = min(n0 + row, N - 1);
+            const uint8_t *src = W + (size_t)n * row_bytes + (size_t)(t0 + t) * F::wrow + ch * 16;
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(ws + (i * kMfmaThreads + wave * 64) * 16),
+                                             16, 0, 0);
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+
+    const int mrow_base = wm * (BM / WM);
+    const int ncol_base = wn * (BN / WN);
+    // Group scales of the lane's weight rows for one stage: one per group the
+    // stage touches (g128: 1, g32: 2), loaded a stage ahead.
+    constexpr int SPS = F::group == 32 ? 2 : 1;
+    const int G = F::group > 0 ? (K + F::group - 1) / F::group : 1;
+    float sreg[TN][SPS];
+    auto load_scales = [&](int t) {
+        if constexpr (F::group > 0) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = min(n0 + ncol_base + j * 32 + (lane & 31), N - 1);
+#pragma unroll
+                for (int g = 0; g < SPS; ++g) sreg[j][g] = S[(size_t)n * G + ((t0 + t) * kBK) / F::group + g];
+            }
+        }
+    };
+
+    load_scales(0);
+    load_a(0);
+    load_w(0, 0);
+    store_a(0);
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    const uint32_t magic = opaque_magic();
+    for (int t = 0; t < nsteps; ++t) {
+        const int b = t & 1;
+        h2 spair[TN][SPS];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < SPS; ++g) {
+                const _Float16 h = (_Float16)sreg[j][g];
+                spair[j][g] = h2{h, h};
+            }
+        if (t + 1 < nsteps) {
+            load_scales(t + 1);
+            load_a(t + 1);
+            load_w(t + 1, b ^ 1);
+        }
+        const unsigned char *as = lds + b * STAGE;
+        const unsigned char *ws = as + A_BYTES;
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            half8 af[F::planes][TM], bfr[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int row = mrow_base + i * 32 + (lane & 31);
+                const int kb = 2 * kk + (lane >> 5);
+#pragma unroll
+                for (int pl = 0; pl < F::planes; ++pl)
+                    af[pl][i] = *(const half8 *)(as + pl * A_PLANE + row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int nl = ncol_base + j * 32 + (lane & 31);
+                u32x4 q;
+                if constexpr (F::w8) {
+                    // bytes k..k+7 of row nl: k = 16 kk + 8 (lane >> 5)
+                    const uint32_t *p = (const uint32_t *)(ws + nl * F::wrow + 16 * kk + 8 * (lane >> 5));
+                    const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        const uint32_t u = p[d] ^ 0x80808080u;
+                        const h2 lo = __builtin_bit_cast(h2, (u & 0x00FF00FFu) | magic) + bias;
+                        const h2 hi = __builtin_bit_cast(h2, ((u >> 8) & 0x00FF00FFu) | magic) + bias;
+                        q[2 * d] = __builtin_bit_cast(uint32_t, lo);
+                        q[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
+                    }
+                } else {
+                    const uint32_t x = *(const uint32_t *)(ws + nl * F::wrow + 8 * kk + 4 * (lane >> 5));
+                    h2 qq[4];
+                    dequant_w4(x, magic, qq);
+                    if constexpr (F::group > 0) {
+                        const h2 sp = spair[j][SPS == 2 ? (kk >> 1) : 0];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) qq[e] = qq[e] * sp;
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) q[e] = __builtin_bit_cast(uint32_t, qq[e]);
+                }
+                bfr[j] = __builtin_bit_cast(half8, q);
+            }
+#pragma unroll
+            for (int pl = 0; pl < F::planes; ++pl)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[pl][i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (t + 1 < nsteps) {
+            store_a(b ^ 1);
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: lane holds column (lane & 31) of each tile, rows
+    // 8q + 4 (lane >> 5) + r for element 4q + r.
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n0 + ncol_base + j * 32 + (lane & 31);
+        if (n >= N) continue;
+        const float sc = (F::group > 0 || P) ? 1.0f : S[n];
+        float *pz = P ? P + (size_t)blockIdx.z * M * N : nullptr;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + mrow_base + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (m >= M) continue;
+                if (pz) {
+                    pz[(size_t)m * N + n] = acc[i][j][e];
+                    continue;
+                }
+                const float y = acc[i][j][e] * sc;
+                if constexpr (F::a32)
+                    ((float *)C)[(size_t)m * N + n] = y;
+                else
+                    ((uint16_t *)C)[(size_t)m * N + n] = f32_to_bf16(y);
+            }
+    }
+}
+
+// Sum of the split partials in split order, then the per-row scale (per-row
+// formats) and the output conversion.
+template <int FMT>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restrict__ P, const float *__restrict__ S,
+                                                          void *__restrict__ C, int M, int N, int splits) {
+    using F = MF<FMT>;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t total = (size_t)M * N;
+    if (idx >= total) return;
+    float y = 0.0f;
+    for (int z = 0; z < splits; ++z) y += P[(size_t)z * total + idx];
+    if constexpr (F::group == 0) y *= S[idx % N];
+    if constexpr (F::a32)
+        ((float *)C)[idx] = y;
+    else
+        ((uint16_t *)C)[idx] = f32_to_bf16(y);
+}
+
+template <int FMT, int BM, int BN, int WM>
+void launch_mfma(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, float *P, int splits,
+                 int sps, int M, int N, int K) {
+    const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
+    gemm_mfma_kernel<FMT, BM, BN, WM><<<grid, kMfmaThreads, 0, st>>>(A, W, S, C, splits > 1 ? P : nullptr, M, N, K,
+                                                                     sps);
+    if (splits > 1) {
+        const size_t total = (size_t)M * N;
+        split_reduce_kernel<FMT><<<(unsigned)((total + 255) / 256), 256, 0, st>>>(P, S, C, M, N, splits);
+    }
+}
+
+template <int FMT>
+void launch_mfma_fmt(bool big, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, float *P,
+                     int splits, int sps, int M, int N, int K) {
+    if (big)
+        launch_mfma<FMT, 128, 128, 2>(st, A, W, S, C, P, splits, sps, M, N, K);
+    else
+        launch_mfma<FMT, 64, 128, 2>(st, A, W, S, C, P, splits, sps, M, N, K);
+}
+
+}  // namespace
+
+int mfma_min_m() { return env_int("PILM_HIP_MFMA_MIN_M", 64); }
+
+bool mfma_supports(size_t K, const void *A, const uint8_t *W) {
+    return K > 0 && K % kBK == 0 && ((((uintptr_t)A) | ((uintptr_t)W)) & 15) == 0;
+}
+
+// Shapes that mfma_supports(); M, N, K below 2^31 (checked by the caller).
+int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+             hipStream_t st, const char *fn) {
+    if (!mfma_supports(K, A, W)) return fail(ECPU_ERR_UNSUPPORTED, "%s: shape not taken by the matrix-core path", fn);
+    const bool big = M >= 128;
+    const int bm = big ? 128 : 64;
+    const size_t blocks = ((N + 127) / 128) * ((M + bm - 1) / bm);
+    const int nsteps = (int)(K / kBK);
+    // Split K while the output tiles alone leave the GPU under-filled: aim at
+    // ~1024 workgroups, each keeping at least two K steps.
+    int splits = 1;
+    if (blocks < 512) splits = (int)std::min<size_t>((size_t)std::max(1, nsteps / 2), (1024 + blocks - 1) / blocks);
+    const int env_splits = env_int("PILM_HIP_MFMA_SPLITS", 0);
+    if (env_splits > 0) splits = std::min(env_splits, nsteps);
+    const int sps = (nsteps + splits - 1) / splits;
+    splits = (nsteps + sps - 1) / sps;   // every split non-empty
+    float *P = nullptr;
+    if (splits > 1) {
+        int *T = nullptr;
+        const int rc = split_scratch(st, (size_t)splits * M * N, 1, &P, &T, fn);
+        if (rc != ECPU_OK) return rc;
+    }
+    switch (fmt) {
+        case F_W8A32: launch_mfma_fmt<F_W8A32>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W8A16: launch_mfma_fmt<F_W8A16>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W4ROW: launch_mfma_fmt<F_W4ROW>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W4G128: launch_mfma_fmt<F_W4G128>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        default: launch_mfma_fmt<F_W4G32>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+    }
+    return ECPU_OK;
+}
+
+}  // namespace pilm

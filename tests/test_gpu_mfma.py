@@ -1,0 +1,123 @@
+"""GPU: the matrix-core dequant-GEMM taken by M >= 64 activation rows.
+
+This path is not bit-identical to the reference (fp16 operands, fp32 sums in
+another order); the tolerance for it is a 1e-2 maximum relative error,
+measured per output row against that row's largest magnitude:
+
+    max_n |y[m,n] - ref[m,n]|  <=  1e-2 * max_n |ref[m,n]|      for every m
+
+where ref is the oracle (bit-identical to the reference CPU kernels).  The
+typical error is far smaller, so the tests also bound the RMS error at 3e-3 of
+the RMS output -- a misplaced nibble, scale or row would break both bounds.
+Calls go through the C ABI like piLM's own (pilm_amd.ckernel).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from pilm_amd import synth as S
+from tests import _golden as GV
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from tests.test_gpu_linear import run_gpu  # noqa: E402
+
+TOL_MAX_REL = 1e-2     # the MFMA path tolerance, per output row
+TOL_RMS_REL = 3e-3
+
+FMTS = ["w8a32", "w8a16", "w4", "w4g32", "w4g128"]
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def as_f32(fmt: str, y: np.ndarray) -> np.ndarray:
+    return y.astype(np.float64) if fmt == "w8a32" else S.bf16_bits_to_f32(y).astype(np.float64)
+
+
+def check_close(fmt, y, ref, what):
+    yf, rf = as_f32(fmt, y), as_f32(fmt, ref)
+    assert np.all(np.isfinite(yf)), what
+    err = np.abs(yf - rf)
+    rowmax = np.abs(rf).max(axis=1)
+    bad = err.max(axis=1) > TOL_MAX_REL * rowmax
+    assert not bad.any(), f"{what}: rows {np.nonzero(bad)[0][:8]} exceed {TOL_MAX_REL} (max rel {(err.max(axis=1) / np.maximum(rowmax, 1e-30)).max():.3g})"
+    rms = np.sqrt((err ** 2).mean()) / max(np.sqrt((rf ** 2).mean()), 1e-30)
+    assert rms <= TOL_RMS_REL, f"{what}: rms relative error {rms:.3g}"
+    return float((err.max(axis=1) / np.maximum(rowmax, 1e-30)).max())
+
+
+SHAPES = [(64, 32, 64), (64, 100, 192), (80, 200, 512), (128, 128, 1024), (200, 513, 320), (256, 1000, 2048),
+          (129, 64, 4096)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_mfma_against_oracle(fmt, shape, dev):
+    m, n, k = shape
+    gen = GV._gen()
+    x, w, s = gen.make_inputs(fmt, m, n, k, 4242 + m + n + k)
+    _say(f"[gpu] mfma {fmt} M={m} N={n} K={k}")
+    y = run_gpu(fmt, x, w, s, dev)
+    ref = gen.run(fmt, x, w, s, "oracle")
+    check_close(fmt, y, ref, f"{fmt} {shape}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mfma_config3_shape(fmt, dev):
+    """One prefill shape of the 8B model (gate/up rows, K = hidden) at M=256."""
+    m, n, k = 256, 2048, 4096
+    gen = GV._gen()
+    x, w, s = gen.make_inputs(fmt, m, n, k, 99)
+    _say(f"[gpu] mfma config3 {fmt} M={m} N={n} K={k}")
+    y = run_gpu(fmt, x, w, s, dev)
+    ref = gen.run(fmt, x, w, s, "oracle")
+    check_close(fmt, y, ref, f"{fmt} config3")
+
+
+@pytest.mark.parametrize("fmt", ["w8a16", "w4g128"])
+def test_below_threshold_stays_exact(fmt, dev, monkeypatch):
+    """M below the threshold, or the threshold disabled, keeps the exact kernels."""
+    gen = GV._gen()
+    x, w, s = gen.make_inputs(fmt, 63, 96, 512, 7)
+    _say(f"[gpu] exact M=63 {fmt}")
+    y = run_gpu(fmt, x, w, s, dev)
+    assert np.array_equal(y.view(np.uint8), gen.run(fmt, x, w, s, "oracle").view(np.uint8))
+    monkeypatch.setenv("PILM_HIP_MFMA_MIN_M", "0")
+    x, w, s = gen.make_inputs(fmt, 128, 96, 512, 8)
+    _say(f"[gpu] exact M=128 {fmt} (matrix cores off)")
+    y = run_gpu(fmt, x, w, s, dev)
+    assert np.array_equal(y.view(np.uint8), gen.run(fmt, x, w, s, "oracle").view(np.uint8))
+
+
+def test_mfma_zero_and_sign_extremes(dev):
+    """All-(-8) int4 weights, all-(-128) int8 weights and zero activations."""
+    gen = GV._gen()
+    for fmt in FMTS:
+        x, w, s = gen.make_inputs(fmt, 96, 64, 256, 5, special="min_w")
+        _say(f"[gpu] mfma min_w {fmt}")
+        check_close(fmt, run_gpu(fmt, x, w, s, dev), gen.run(fmt, x, w, s, "oracle"), f"{fmt} min_w")
+        x, w, s = gen.make_inputs(fmt, 96, 64, 256, 6, special="zero_x")
+        y = as_f32(fmt, run_gpu(fmt, x, w, s, dev))
+        assert np.all(y == 0.0), fmt
+
+
+@pytest.mark.parametrize("splits", ["1", "3", "7"])
+def test_mfma_split_k(splits, dev, monkeypatch):
+    """Split K (fp32 partials summed in split order): same tolerance, and the
+    same bits on every run."""
+    monkeypatch.setenv("PILM_HIP_MFMA_SPLITS", splits)
+    gen = GV._gen()
+    for fmt in FMTS:
+        x, w, s = gen.make_inputs(fmt, 96, 160, 1024, 31)
+        _say(f"[gpu] mfma splits={splits} {fmt}")
+        y = run_gpu(fmt, x, w, s, dev)
+        check_close(fmt, y, gen.run(fmt, x, w, s, "oracle"), f"{fmt} splits={splits}")
+        assert np.array_equal(y.view(np.uint8), run_gpu(fmt, x, w, s, dev).view(np.uint8)), "not deterministic"
