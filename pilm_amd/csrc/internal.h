@@ -32,6 +32,10 @@ int check_launch(const char *fn);
 // device (different streams) must not both take the split path.
 int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, int **T, const char *fn);
 
+// Per-device buffer of at least `bytes` for the matrix-core path's converted
+// activations; same growth, retirement and sharing rules as split_scratch.
+int act_scratch(size_t bytes, void **X, const char *fn);
+
 // Dequant-GEMM on the matrix cores for M >= mfma_min_m() (env
 // PILM_HIP_MFMA_MIN_M, default 64; 0 keeps every M on the exact kernels)
 // when mfma_supports(): K a multiple of 64, 16-byte aligned A and W.

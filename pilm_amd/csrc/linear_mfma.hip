@@ -20,11 +20,13 @@
 // into one fp16x2 register, so every 8-element block of the activation tile is
 // stored in the matching order: int4 (0,4,1,5,2,6,3,7), int8 (0,2,1,3,4,6,5,7).
 //
+// A small pre-pass converts the activations once into that fp16 layout (two
+// planes, hi and lo, for fp32 activations) in a per-device scratch buffer.
 // Tiling: a workgroup of four waves computes BM x BN outputs (waves WM x WN,
 // each (BM/WM) x (BN/WN) in 32 x 32 MFMA tiles) over K in steps of 64, with a
-// double-buffered LDS stage: the weights of step t+1 arrive by global -> LDS
-// DMA and the activations of step t+1 through registers (converted and
-// permuted on the way) while step t is multiplied.
+// double-buffered LDS stage filled by global -> LDS DMA (activation blocks
+// XOR-swizzled by row, weights row-major) while the previous step is
+// multiplied; weights are unpacked from LDS into registers per 16-k step.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -89,11 +91,44 @@ __device__ __forceinline__ void split_hi(float (&v)[8], float (&hi)[8]) {
     }
 }
 
+// Activations [M, K] (bf16 or fp32) -> X[plane][M][K] fp16, each 8-element
+// block in the weight unpack order; one thread per block.
+template <int FMT>
+__global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ A, u32x4 *__restrict__ X,
+                                                      size_t blocks) {
+    using F = MF<FMT>;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= blocks) return;
+    float v[8];
+    if constexpr (F::a32) {
+        const f32x4 *p = (const f32x4 *)A + 2 * i;
+        const f32x4 x0 = p[0], x1 = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = x0[e];
+            v[4 + e] = x1[e];
+        }
+        float hi[8];
+        split_hi(v, hi);
+        X[i] = act_block<FMT>(hi);
+        X[blocks + i] = act_block<FMT>(v);
+    } else {
+        const u32x4 x = ((const u32x4 *)A)[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = bf16_lo(x[e]);
+            v[2 * e + 1] = bf16_hi(x[e]);
+        }
+        X[i] = act_block<FMT>(v);
+    }
+}
+
 // blockIdx.z selects a contiguous range of K steps (split K); with more than
 // one split the raw fp32 sums go to P[z][M][N] and split_reduce_kernel adds
 // them in split order (deterministic) and finishes the outputs.
+// X: the activations prepared by act_prep_kernel (fp16, planes x M x K).
 template <int FMT, int BM, int BN, int WM>
-__global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__restrict__ A_,
+__global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 *__restrict__ X,
                                                                 const uint8_t *__restrict__ W,
                                                                 const float *__restrict__ S, void *__restrict__ C,
                                                                 float *__restrict__ P, int M, int N, int K,
@@ -106,9 +141,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__r
     constexpr int A_BYTES = A_PLANE * F::planes;
     constexpr int W_BYTES = BN * F::wrow;
     constexpr int STAGE = A_BYTES + W_BYTES;
-    constexpr int A_BLOCKS = BM * kBK / 8 / kMfmaThreads;   // 8-element blocks per thread per stage
-    constexpr int W_LOADS = W_BYTES / 16 / kMfmaThreads;     // 16-byte DMA per thread per stage
-    static_assert(A_BLOCKS >= 1 && W_LOADS >= 1, "tile too small");
+    constexpr int A_LOADS = A_PLANE / 16 / kMfmaThreads;     // 16-byte DMA per thread per plane and stage
+    constexpr int W_LOADS = W_BYTES / 16 / kMfmaThreads;
+    static_assert(A_LOADS >= 1 && W_LOADS >= 1, "tile too small");
     __shared__ __align__(16) unsigned char lds[2 * STAGE];
 
     const int tid = threadIdx.x;
@@ -119,53 +154,27 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__r
     const size_t row_bytes = F::w8 ? (size_t)K : (size_t)K / 2;
     const int t0 = blockIdx.z * steps_per_split;
     const int nsteps = min(steps_per_split, K / kBK - t0);   // >= 1 (host guarantees)
+    const size_t plane = (size_t)M * K;
 
-    // ---- staging of one K step into buffer b
-    float areg[A_BLOCKS][8];
-    auto load_a = [&](int t) {
-#pragma unroll
-        for (int i = 0; i < A_BLOCKS; ++i) {
-            const int blk = tid + i * kMfmaThreads;
-            const int row = blk / (kBK / 8), kb = blk % (kBK / 8);
-            const int m = min(m0 + row, M - 1);
-            const size_t k = (size_t)(t0 + t) * kBK + 8 * kb;
-            if constexpr (F::a32) {
-                const f32x4 *p = (const f32x4 *)((const float *)A_ + (size_t)m * K + k);
-                const f32x4 x0 = p[0], x1 = p[1];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    areg[i][e] = x0[e];
-                    areg[i][4 + e] = x1[e];
-                }
-            } else {
-                const u32x4 x = *(const u32x4 *)((const uint16_t *)A_ + (size_t)m * K + k);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    areg[i][2 * e] = bf16_lo(x[e]);
-                    areg[i][2 * e + 1] = bf16_hi(x[e]);
-                }
-            }
-        }
-    };
     // Activation tile: row r holds 8 blocks of 16 B; block kb sits at position
     // kb ^ ((r >> 1) & 7) so that 16 lanes reading one block of 16 rows cover
-    // all banks.
-    auto store_a = [&](int b) {
+    // all banks.  The DMA writes positions in lane order, so each lane fetches
+    // the block that belongs at its position.
+    auto load_a = [&](int t, int b) {
         unsigned char *as = lds + b * STAGE;
 #pragma unroll
-        for (int i = 0; i < A_BLOCKS; ++i) {
-            const int blk = tid + i * kMfmaThreads;
-            const int row = blk / (kBK / 8), kb = blk % (kBK / 8);
-            const int off = row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4);
-            if constexpr (F::planes == 2) {
-                float hi[8];
-                split_hi(areg[i], hi);   // areg now holds the low parts (exact in fp16)
-                *(u32x4 *)(as + off) = act_block<FMT>(hi);
-                *(u32x4 *)(as + A_PLANE + off) = act_block<FMT>(areg[i]);
-            } else {
-                *(u32x4 *)(as + off) = act_block<FMT>(areg[i]);
+        for (int pl = 0; pl < F::planes; ++pl)
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i) {
+                const int c = i * kMfmaThreads + tid;            // 16-byte position in the plane
+                const int row = c >> 3, pos = c & 7;
+                const int kb = pos ^ ((row >> 1) & 7);
+                const int m = min(m0 + row, M - 1);
+                const _Float16 *src = X + pl * plane + (size_t)m * K + (size_t)(t0 + t) * kBK + 8 * kb;
+                __builtin_amdgcn_global_load_lds((const void *)src,
+                                                 (lds_void *)(as + pl * A_PLANE + (i * kMfmaThreads + wave * 64) * 16),
+                                                 16, 0, 0);
             }
-        }
     };
     // Weight tile: row-major, wrow bytes per row, by DMA (16 B per lane).
     auto load_w = [&](int t, int b) {
@@ -206,9 +215,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__r
     };
 
     load_scales(0);
-    load_a(0);
+    load_a(0, 0);
     load_w(0, 0);
-    store_a(0);
     wait_vmcnt<0>();
     __syncthreads();
 
@@ -225,33 +233,25 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__r
             }
         if (t + 1 < nsteps) {
             load_scales(t + 1);
-            load_a(t + 1);
+            load_a(t + 1, b ^ 1);
             load_w(t + 1, b ^ 1);
         }
         const unsigned char *as = lds + b * STAGE;
         const unsigned char *ws = as + A_BYTES;
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
-            half8 af[F::planes][TM], bfr[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int row = mrow_base + i * 32 + (lane & 31);
-                const int kb = 2 * kk + (lane >> 5);
-#pragma unroll
-                for (int pl = 0; pl < F::planes; ++pl)
-                    af[pl][i] = *(const half8 *)(as + pl * A_PLANE + row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4));
-            }
+            half8 bfr[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int nl = ncol_base + j * 32 + (lane & 31);
                 u32x4 q;
                 if constexpr (F::w8) {
                     // bytes k..k+7 of row nl: k = 16 kk + 8 (lane >> 5)
-                    const uint32_t *p = (const uint32_t *)(ws + nl * F::wrow + 16 * kk + 8 * (lane >> 5));
+                    const uint32_t *pw = (const uint32_t *)(ws + nl * F::wrow + 16 * kk + 8 * (lane >> 5));
                     const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
                     for (int d = 0; d < 2; ++d) {
-                        const uint32_t u = p[d] ^ 0x80808080u;
+                        const uint32_t u = pw[d] ^ 0x80808080u;
                         const h2 lo = __builtin_bit_cast(h2, (u & 0x00FF00FFu) | magic) + bias;
                         const h2 hi = __builtin_bit_cast(h2, ((u >> 8) & 0x00FF00FFu) | magic) + bias;
                         q[2 * d] = __builtin_bit_cast(uint32_t, lo);
@@ -272,17 +272,20 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const void *__r
                 bfr[j] = __builtin_bit_cast(half8, q);
             }
 #pragma unroll
-            for (int pl = 0; pl < F::planes; ++pl)
+            for (int i = 0; i < TM; ++i) {
+                const int row = mrow_base + i * 32 + (lane & 31);
+                const int kb = 2 * kk + (lane >> 5);
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                for (int pl = 0; pl < F::planes; ++pl) {
+                    const half8 af =
+                        *(const half8 *)(as + pl * A_PLANE + row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4));
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[pl][i], bfr[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bfr[j], acc[i][j], 0, 0, 0);
+                }
+            }
         }
-        if (t + 1 < nsteps) {
-            store_a(b ^ 1);
-            wait_vmcnt<0>();
-        }
+        if (t + 1 < nsteps) wait_vmcnt<0>();
         __syncthreads();
     }
 
@@ -332,10 +335,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 }
 
 template <int FMT, int BM, int BN, int WM>
-void launch_mfma(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, float *P, int splits,
+void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const float *S, void *C, float *P, int splits,
                  int sps, int M, int N, int K) {
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
-    gemm_mfma_kernel<FMT, BM, BN, WM><<<grid, kMfmaThreads, 0, st>>>(A, W, S, C, splits > 1 ? P : nullptr, M, N, K,
+    gemm_mfma_kernel<FMT, BM, BN, WM><<<grid, kMfmaThreads, 0, st>>>(X, W, S, C, splits > 1 ? P : nullptr, M, N, K,
                                                                      sps);
     if (splits > 1) {
         const size_t total = (size_t)M * N;
@@ -343,13 +346,19 @@ void launch_mfma(hipStream_t st, const void *A, const uint8_t *W, const float *S
     }
 }
 
+// Output tile per workgroup: 256 x 128 (waves 2 x 2 of 128 x 64) from M =
+// 2048, 128 x 128 from 128, 64 x 128 below (measured).
 template <int FMT>
-void launch_mfma_fmt(bool big, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, float *P,
-                     int splits, int sps, int M, int N, int K) {
-    if (big)
-        launch_mfma<FMT, 128, 128, 2>(st, A, W, S, C, P, splits, sps, M, N, K);
+void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, const uint8_t *W, const float *S,
+                     void *C, float *P, int splits, int sps, int M, int N, int K) {
+    const size_t blocks = (size_t)M * K / 8;
+    act_prep_kernel<FMT><<<(unsigned)((blocks + 255) / 256), 256, 0, st>>>(A, (u32x4 *)X, blocks);
+    if (bm == 256)
+        launch_mfma<FMT, 256, 128, 2>(st, X, W, S, C, P, splits, sps, M, N, K);
+    else if (bm == 128)
+        launch_mfma<FMT, 128, 128, 2>(st, X, W, S, C, P, splits, sps, M, N, K);
     else
-        launch_mfma<FMT, 64, 128, 2>(st, A, W, S, C, P, splits, sps, M, N, K);
+        launch_mfma<FMT, 64, 128, 2>(st, X, W, S, C, P, splits, sps, M, N, K);
 }
 
 }  // namespace
@@ -364,8 +373,7 @@ bool mfma_supports(size_t K, const void *A, const uint8_t *W) {
 int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn) {
     if (!mfma_supports(K, A, W)) return fail(ECPU_ERR_UNSUPPORTED, "%s: shape not taken by the matrix-core path", fn);
-    const bool big = M >= 128;
-    const int bm = big ? 128 : 64;
+    const int bm = M >= 2048 ? 256 : (M >= 128 ? 128 : 64);
     const size_t blocks = ((N + 127) / 128) * ((M + bm - 1) / bm);
     const int nsteps = (int)(K / kBK);
     // Split K while the output tiles alone leave the GPU under-filled: aim at
@@ -382,12 +390,19 @@ int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
         const int rc = split_scratch(st, (size_t)splits * M * N, 1, &P, &T, fn);
         if (rc != ECPU_OK) return rc;
     }
+    void *X = nullptr;
+    const size_t xbytes = (size_t)M * K * 2 * (fmt == F_W8A32 ? 2 : 1);
+    {
+        const int rc = act_scratch(xbytes, &X, fn);
+        if (rc != ECPU_OK) return rc;
+    }
+    const _Float16 *Xh = (const _Float16 *)X;
     switch (fmt) {
-        case F_W8A32: launch_mfma_fmt<F_W8A32>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        case F_W8A16: launch_mfma_fmt<F_W8A16>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        case F_W4ROW: launch_mfma_fmt<F_W4ROW>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        case F_W4G128: launch_mfma_fmt<F_W4G128>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        default: launch_mfma_fmt<F_W4G32>(big, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W8A32: launch_mfma_fmt<F_W8A32>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W8A16: launch_mfma_fmt<F_W8A16>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W4ROW: launch_mfma_fmt<F_W4ROW>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W4G128: launch_mfma_fmt<F_W4G128>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        default: launch_mfma_fmt<F_W4G32>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
     }
     return ECPU_OK;
 }

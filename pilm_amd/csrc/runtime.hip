@@ -84,6 +84,8 @@ struct Scratch {
     size_t nP;
     int *T;
     size_t nT;
+    void *X;       // converted activations of the matrix-core path
+    size_t nX;
 };
 static std::vector<Scratch> g_scratch;
 static std::vector<std::pair<int, void *>> g_retired;
@@ -107,7 +109,7 @@ int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, 
     for (auto &e : g_scratch)
         if (e.dev == dev) sc = &e;
     if (!sc) {
-        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0});
+        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0});
         sc = &g_scratch.back();
     }
     if (sc->nP < nfloat) {
@@ -136,6 +138,29 @@ int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, 
     return ECPU_OK;
 }
 
+int act_scratch(size_t bytes, void **X, const char *fn) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(ECPU_ERR_DEVICE, "%s: no current HIP device", fn);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    Scratch *sc = nullptr;
+    for (auto &e : g_scratch)
+        if (e.dev == dev) sc = &e;
+    if (!sc) {
+        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0});
+        sc = &g_scratch.back();
+    }
+    if (sc->nX < bytes) {
+        const size_t want = std::max<size_t>(bytes, 1u << 20);
+        void *p = dev_alloc(want);
+        if (!p) return fail(ECPU_ERR_MEM, "%s: hipMalloc of %zu bytes of activation scratch failed", fn, want);
+        if (sc->X) g_retired.push_back({dev, sc->X});
+        sc->X = p;
+        sc->nX = want;
+    }
+    *X = sc->X;
+    return ECPU_OK;
+}
+
 static void free_scratch() {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     int cur = 0;
@@ -149,6 +174,7 @@ static void free_scratch() {
     for (auto &e : g_scratch) {
         if (e.P) release(e.dev, e.P);
         if (e.T) release(e.dev, e.T);
+        if (e.X) release(e.dev, e.X);
     }
     g_retired.clear();
     g_scratch.clear();
