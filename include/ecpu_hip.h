@@ -170,7 +170,43 @@ int ekernel_linear_w4a16g128_bf16(const ekernel_linear_w8a32_desc_t *desc, const
                                   ekernel_isa_t isa);
 
 /* ---- kernel/api.h:195-198: bf16 SwiGLU (required by _configure) -------- */
+/* out[i] = bf16(silu(g) * u), silu(g) = g / (1 + expf(-g)); expf as the
+ * reference's C library evaluates it, so outputs are bit-identical. */
 int ekernel_swiglu_bf16(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n);
+
+/* ---- fused epilogues ---------------------------------------------------- */
+
+/* Greedy decode's lm_head: argmax over n of bf16(scales[n] * A[0,:].W[n,:])
+ * for one activation row (M must be 1, N and K nonzero, else
+ * ECPU_ERR_UNSUPPORTED); ties and +-0 go to the lowest index, NaN never wins,
+ * (-inf, 0) when no value exceeds -inf.  out_index / out_value may each be
+ * host memory -- the reference binding's ctypes byref; the call then waits
+ * for the result -- or device memory, written by the kernel without waiting.
+ *                                          kernel/api.h:66-72, kernels.c:658-737 */
+int ekernel_linear_w8a16_bf16_argmax(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                                     const int8_t *W, const float *scales, size_t *out_index,
+                                     float *out_value, ekernel_isa_t isa);
+
+/*                                                          kernel/api.h:44-50 */
+typedef struct {
+    size_t M;
+    size_t hidden_size;
+    size_t intermediate_size;
+    size_t gate_up_in_features;
+    size_t down_in_features;
+} ekernel_w4a16_swiglu_desc_t;
+
+/* The W4 SwiGLU MLP of one token (M must be 1 and down_in_features equal to
+ * intermediate_size, else ECPU_ERR_UNSUPPORTED): gate_up_W is packed int4
+ * [2I, ceil(K/2)] with per-row scales [2I] (gate rows first), down_W is
+ * [H, ceil(I/2)] with scales [H]; C[h] = bf16(down_scales[h] * hidden.down_W[h])
+ * with hidden[i] = bf16(silu(g_i) * u_i), g_i and u_i the bf16 outputs of gate
+ * row i and up row I+i.  The hidden row lives in a per-device scratch buffer.
+ *                                        kernel/api.h:203-214, kernels.c:1598-1735 */
+int ekernel_swiglu_w4a16_bf16(const ekernel_w4a16_swiglu_desc_t *desc, const uint16_t *A,
+                              const uint8_t *gate_up_W, const float *gate_up_scales,
+                              const uint8_t *down_W, const float *down_scales, uint16_t *C,
+                              ekernel_isa_t isa);
 
 /* ---- additions (no counterpart in the reference) ----------------------- */
 

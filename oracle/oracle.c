@@ -20,6 +20,8 @@
  *     658-737  ekernel_linear_w8a16_bf16_argmax
  *     1002-1087 ekernel_linear_w4a16_bf16
  *     1089-1157 linear_w4a16g_bf16_impl (+ g32 / g128 entry points)
+ *     1580-1596 ekernel_swiglu_bf16
+ *     1598-1735 ekernel_swiglu_w4a16_bf16
  *
  * The reference is compiled by GCC in GNU C mode with FMA available, where
  * floating-point contraction defaults to "fast": every scalar `s += a * b`
@@ -41,7 +43,9 @@
  *   4 high nibble taken as the even k
  *   5 nibble decoded as v - 8 (a zero point) instead of sign extension
  *   6 bf16 output truncated instead of rounded to nearest even
- *   7 int4 dot with one 8-lane accumulator instead of lo/hi halves */
+ *   7 int4 dot with one 8-lane accumulator instead of lo/hi halves
+ *   8 SwiGLU gate/up sums scaled but not rounded to bf16 before silu
+ *   9 silu(g) with expf(g) instead of expf(-g) */
 #ifndef ORACLE_PLANT
 #define ORACLE_PLANT 0
 #endif
@@ -228,6 +232,63 @@ int oracle_linear_w4a16g_bf16(size_t M, size_t N, size_t K, size_t group_size, c
             C[(size_t)mi * N + (size_t)ni] = f32_to_bf16(acc);
         }
     return 0;
+}
+
+/* kernels.c:1580-1596: out = bf16(silu(g) * u), silu(g) = g / (1 + expf(-g)),
+ * expf from the C library as in the reference build. */
+static inline uint16_t swiglu_f32(float g, float u) {
+#if ORACLE_PLANT == 9
+    float silu = g / (1.0f + expf(g));
+#else
+    float silu = g / (1.0f + expf(-g));
+#endif
+    return f32_to_bf16(silu * u);
+}
+
+static inline uint16_t swiglu_one(uint16_t g_bits, uint16_t u_bits) {
+    return swiglu_f32(bf16_to_f32(g_bits), bf16_to_f32(u_bits));
+}
+
+int oracle_swiglu_bf16(const uint16_t *gate, const uint16_t *up, uint16_t *out, size_t n) {
+    if (!gate || !up || !out) return -1;
+    for (size_t i = 0; i < n; i++) out[i] = swiglu_one(gate[i], up[i]);
+    return 0;
+}
+
+/* kernels.c:1598-1735: M = 1; gate row i and up row I+i of the packed int4
+ * gate_up matrix (per-row scales), each rounded to bf16 like a linear output,
+ * hidden[i] = bf16(silu(g) * u), then the W4 per-row linear of hidden with the
+ * down matrix.  Both dots are the per-row int4 dot (kernels.c:1639-1640 and
+ * 1679 use the same 8-row / single-row dot functions as
+ * ekernel_linear_w4a16_bf16). */
+int oracle_swiglu_w4a16_bf16(size_t H, size_t I, size_t K, const uint16_t *A, const uint8_t *gate_up_W,
+                             const float *gate_up_scales, const uint8_t *down_W, const float *down_scales,
+                             uint16_t *C, uint16_t *hidden) {
+    if (!A || !gate_up_W || !gate_up_scales || !down_W || !down_scales || !C || !hidden) return -1;
+    if (H == 0 || I == 0 || K == 0) return -5;
+    const size_t gpk = (K + 1) / 2, dpk = (I + 1) / 2;
+    #pragma omp parallel for schedule(static)
+    for (long long ii = 0; ii < (long long)I; ii++) {
+        const size_t i = (size_t)ii;
+        float gs = dot_i4(A, gate_up_W + i * gpk, K) * gate_up_scales[i];
+        float us = dot_i4(A, gate_up_W + (I + i) * gpk, K) * gate_up_scales[I + i];
+#if ORACLE_PLANT == 8
+        hidden[i] = swiglu_f32(gs, us);
+#else
+        hidden[i] = swiglu_one(f32_to_bf16(gs), f32_to_bf16(us));
+#endif
+    }
+    #pragma omp parallel for schedule(static)
+    for (long long hh = 0; hh < (long long)H; hh++) {
+        const size_t h = (size_t)hh;
+        C[h] = f32_to_bf16(dot_i4(hidden, down_W + h * dpk, I) * down_scales[h]);
+    }
+    return 0;
+}
+
+/* The C library's expf over an array (used to pin the device expf). */
+void oracle_expf(const float *x, float *out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = expf(x[i]);
 }
 
 /* bf16 helpers exported for the Python side of the oracle. */

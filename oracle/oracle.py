@@ -37,6 +37,12 @@ class _Desc(ctypes.Structure):
     _fields_ = [("M", _S), ("N", _S), ("K", _S)]
 
 
+class _SwiGLUDesc(ctypes.Structure):
+    # ekernel_w4a16_swiglu_desc_t, src/ecpu/include/kernel/api.h:44-50
+    _fields_ = [("M", _S), ("hidden_size", _S), ("intermediate_size", _S), ("gate_up_in_features", _S),
+                ("down_in_features", _S)]
+
+
 _oracle = None
 _ref = None
 _planted: dict[int, ctypes.CDLL] = {}
@@ -49,9 +55,14 @@ def _configure_oracle(lib):
     lib.oracle_linear_w4a16g_bf16.argtypes = [_S, _S, _S, _S, _P, _P, _P, _P]
     lib.oracle_linear_w8a16_bf16_argmax.argtypes = [_S, _S, _P, _P, _P, ctypes.POINTER(_S),
                                                      ctypes.POINTER(ctypes.c_float)]
+    lib.oracle_swiglu_bf16.argtypes = [_P, _P, _P, _S]
+    lib.oracle_swiglu_w4a16_bf16.argtypes = [_S, _S, _S, _P, _P, _P, _P, _P, _P, _P]
     for f in ("oracle_linear_w8a32", "oracle_linear_w8a16_bf16", "oracle_linear_w4a16_bf16",
-              "oracle_linear_w4a16g_bf16", "oracle_linear_w8a16_bf16_argmax"):
+              "oracle_linear_w4a16g_bf16", "oracle_linear_w8a16_bf16_argmax", "oracle_swiglu_bf16",
+              "oracle_swiglu_w4a16_bf16"):
         getattr(lib, f).restype = ctypes.c_int
+    lib.oracle_expf.argtypes = [_P, _P, _S]
+    lib.oracle_expf.restype = None
     return lib
 
 
@@ -59,8 +70,8 @@ def planted_lib(variant: int):
     """A deliberately wrong build of the restatement (ORACLE_PLANT=variant)."""
     if variant not in _planted:
         path = HERE / "_build" / f"liboracle_plant{variant}.so"
-        if not path.exists():
-            subprocess.run(["make", "-s", "-C", str(HERE), "plant", f"PLANT={variant}"], check=True)
+        # make rebuilds a variant older than oracle.c
+        subprocess.run(["make", "-s", "-C", str(HERE), "plant", f"PLANT={variant}"], check=True)
         _planted[variant] = _configure_oracle(ctypes.CDLL(str(path)))
     return _planted[variant]
 
@@ -68,7 +79,7 @@ def planted_lib(variant: int):
 def oracle_lib():
     global _oracle
     if _oracle is None:
-        if not ORACLE_LIB.exists():
+        if not ORACLE_LIB.exists() or (HERE / "oracle.c").stat().st_mtime > ORACLE_LIB.stat().st_mtime:
             build(ref=False)
         _oracle = _configure_oracle(ctypes.CDLL(str(ORACLE_LIB)))
     return _oracle
@@ -93,6 +104,10 @@ def ref_lib():
                                                          ctypes.POINTER(_S), ctypes.POINTER(ctypes.c_float),
                                                          ctypes.c_int]
         lib.ekernel_linear_w8a16_bf16_argmax.restype = ctypes.c_int
+        lib.ekernel_swiglu_bf16.argtypes = [_P, _P, _P, _S]
+        lib.ekernel_swiglu_bf16.restype = ctypes.c_int
+        lib.ekernel_swiglu_w4a16_bf16.argtypes = [ctypes.POINTER(_SwiGLUDesc), _P, _P, _P, _P, _P, _P, ctypes.c_int]
+        lib.ekernel_swiglu_w4a16_bf16.restype = ctypes.c_int
         _ref = lib
     return _ref
 
@@ -200,6 +215,59 @@ def linear_w4a16g_bf16(x_bits: np.ndarray, qweight: np.ndarray, scales: np.ndarr
         fn = {32: ref_lib().ekernel_linear_w4a16g32_bf16, 128: ref_lib().ekernel_linear_w4a16g128_bf16}[group_size]
         rc = fn(ctypes.byref(d), _ptr(x_bits), _ptr(qweight), _ptr(scales), _ptr(out), 1)
     _check(rc, f"linear_w4a16g{group_size}_bf16")
+    return out
+
+
+# ------------------------------------------------------------- SwiGLU
+
+def swiglu_bf16(g_bits: np.ndarray, u_bits: np.ndarray, impl: str = "oracle") -> np.ndarray:
+    """kernels.c:1580-1596 on bf16 bit patterns of equal shape."""
+    g_bits = np.ascontiguousarray(g_bits, np.uint16)
+    u_bits = np.ascontiguousarray(u_bits, np.uint16)
+    assert g_bits.shape == u_bits.shape
+    out = np.empty_like(g_bits)
+    if impl != "ref":
+        rc = _olib(impl).oracle_swiglu_bf16(_ptr(g_bits), _ptr(u_bits), _ptr(out), g_bits.size)
+    else:
+        rc = ref_lib().ekernel_swiglu_bf16(_ptr(g_bits), _ptr(u_bits), _ptr(out), g_bits.size)
+    _check(rc, "swiglu_bf16")
+    return out
+
+
+def swiglu_w4a16_bf16(x_bits: np.ndarray, gate_up_qweight: np.ndarray, gate_up_scales: np.ndarray,
+                      down_qweight: np.ndarray, down_scales: np.ndarray, intermediate_size: int,
+                      impl: str = "oracle", return_hidden: bool = False):
+    """kernels.c:1598-1735: x [1, K] bf16, gate_up int4 [2I, ceil(K/2)] with
+    scales [2I], down int4 [H, ceil(I/2)] with scales [H] -> bf16 [1, H]
+    (and, for the restatement, the bf16 hidden row [I])."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint16).reshape(1, -1)
+    gu = np.ascontiguousarray(gate_up_qweight, np.uint8)
+    gs = np.ascontiguousarray(gate_up_scales, np.float32)
+    dw = np.ascontiguousarray(down_qweight, np.uint8)
+    ds = np.ascontiguousarray(down_scales, np.float32)
+    k = x_bits.shape[1]
+    i_sz = int(intermediate_size)
+    h = dw.shape[0]
+    assert gu.shape == (2 * i_sz, (k + 1) // 2) and gs.shape == (2 * i_sz,)
+    assert dw.shape == (h, (i_sz + 1) // 2) and ds.shape == (h,)
+    out = np.empty((1, h), np.uint16)
+    hidden = np.empty((i_sz,), np.uint16)
+    if impl != "ref":
+        rc = _olib(impl).oracle_swiglu_w4a16_bf16(h, i_sz, k, _ptr(x_bits), _ptr(gu), _ptr(gs), _ptr(dw), _ptr(ds),
+                                                  _ptr(out), _ptr(hidden))
+    else:
+        d = _SwiGLUDesc(1, h, i_sz, k, i_sz)
+        rc = ref_lib().ekernel_swiglu_w4a16_bf16(ctypes.byref(d), _ptr(x_bits), _ptr(gu), _ptr(gs), _ptr(dw),
+                                                 _ptr(ds), _ptr(out), 1)
+    _check(rc, "swiglu_w4a16_bf16")
+    return (out, hidden) if return_hidden and impl != "ref" else out
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The C library's expf, element by element."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    oracle_lib().oracle_expf(_ptr(x), _ptr(out), x.size)
     return out
 
 

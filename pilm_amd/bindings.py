@@ -126,6 +126,16 @@ class EkernelLinearW8A32Desc(ctypes.Structure):
     ]
 
 
+class EkernelW4A16SwiGLUDesc(ctypes.Structure):
+    _fields_ = [
+        ("M", ctypes.c_size_t),
+        ("hidden_size", ctypes.c_size_t),
+        ("intermediate_size", ctypes.c_size_t),
+        ("gate_up_in_features", ctypes.c_size_t),
+        ("down_in_features", ctypes.c_size_t),
+    ]
+
+
 _LINEAR_ARGTYPES = [ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p,
                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
 
@@ -157,6 +167,17 @@ def _configure(lib):
             fn.restype = ctypes.c_int
     lib.ekernel_swiglu_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
     lib.ekernel_swiglu_bf16.restype = ctypes.c_int
+    if hasattr(lib, "ekernel_linear_w8a16_bf16_argmax"):
+        # out_index / out_value as plain pointers: host (ctypes byref) or device
+        lib.ekernel_linear_w8a16_bf16_argmax.argtypes = [
+            ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        lib.ekernel_linear_w8a16_bf16_argmax.restype = ctypes.c_int
+    if hasattr(lib, "ekernel_swiglu_w4a16_bf16"):
+        lib.ekernel_swiglu_w4a16_bf16.argtypes = [
+            ctypes.POINTER(EkernelW4A16SwiGLUDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        lib.ekernel_swiglu_w4a16_bf16.restype = ctypes.c_int
     if hasattr(lib, "ecpu_hip_profile_read"):
         lib.ecpu_hip_profile_begin.restype = ctypes.c_int
         lib.ecpu_hip_profile_end.restype = ctypes.c_int
@@ -319,3 +340,51 @@ def swiglu_bf16_ptr(gate_ptr: int, up_ptr: int, out_ptr: int, n: int) -> int:
     lib = _load_lib()
     return lib.ekernel_swiglu_bf16(ctypes.c_void_p(gate_ptr), ctypes.c_void_p(up_ptr),
                                    ctypes.c_void_p(out_ptr), ctypes.c_size_t(n))
+
+
+def linear_w8a16_bf16_argmax_ptr(a_ptr: int, w_ptr: int, scales_ptr: int,
+                                 m: int, n: int, k: int, isa: int | None = None) -> tuple[int, int, float]:
+    """bindings.py:401-420: (rc, index, value), results returned through host memory."""
+    lib = _load_lib()
+    if not hasattr(lib, "ekernel_linear_w8a16_bf16_argmax"):
+        raise RuntimeError("loaded eCPU library does not expose ekernel_linear_w8a16_bf16_argmax")
+    if isa is None:
+        isa = lib.ekernel_detect_isa()
+    desc = EkernelLinearW8A32Desc(m, n, k)
+    out_index = ctypes.c_size_t(0)
+    out_value = ctypes.c_float(0.0)
+    rc = lib.ekernel_linear_w8a16_bf16_argmax(
+        ctypes.byref(desc), ctypes.c_void_p(a_ptr), ctypes.c_void_p(w_ptr), ctypes.c_void_p(scales_ptr),
+        ctypes.addressof(out_index), ctypes.addressof(out_value), int(isa))
+    return int(rc), int(out_index.value), float(out_value.value)
+
+
+def linear_w8a16_bf16_argmax_device_ptr(a_ptr: int, w_ptr: int, scales_ptr: int, index_ptr: int, value_ptr: int,
+                                        m: int, n: int, k: int, isa: int | None = None) -> int:
+    """The same entry point with device outputs (size_t index, float value):
+    enqueued on the current stream, no wait."""
+    lib = _load_lib()
+    if isa is None:
+        isa = lib.ekernel_detect_isa()
+    desc = EkernelLinearW8A32Desc(m, n, k)
+    return lib.ekernel_linear_w8a16_bf16_argmax(
+        ctypes.byref(desc), ctypes.c_void_p(a_ptr), ctypes.c_void_p(w_ptr), ctypes.c_void_p(scales_ptr),
+        ctypes.c_void_p(index_ptr), ctypes.c_void_p(value_ptr), int(isa))
+
+
+def swiglu_w4a16_bf16_ptr(x_ptr: int, gate_up_w_ptr: int, gate_up_scales_ptr: int,
+                          down_w_ptr: int, down_scales_ptr: int, c_ptr: int,
+                          m: int, hidden_size: int, intermediate_size: int,
+                          gate_up_in_features: int, down_in_features: int,
+                          isa: int | None = None) -> int:
+    """bindings.py:567-593."""
+    lib = _load_lib()
+    if not hasattr(lib, "ekernel_swiglu_w4a16_bf16"):
+        raise RuntimeError("loaded eCPU library does not expose ekernel_swiglu_w4a16_bf16")
+    if isa is None:
+        isa = lib.ekernel_detect_isa()
+    desc = EkernelW4A16SwiGLUDesc(m, hidden_size, intermediate_size, gate_up_in_features, down_in_features)
+    return lib.ekernel_swiglu_w4a16_bf16(
+        ctypes.byref(desc), ctypes.c_void_p(x_ptr), ctypes.c_void_p(gate_up_w_ptr),
+        ctypes.c_void_p(gate_up_scales_ptr), ctypes.c_void_p(down_w_ptr), ctypes.c_void_p(down_scales_ptr),
+        ctypes.c_void_p(c_ptr), int(isa))

@@ -240,6 +240,46 @@ def linear_w8a16_bf16(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tens
     return out
 
 
+def linear_w8a16_bf16_argmax(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) -> int:
+    """ckernel.py:233-263: index of the largest bf16 logit of one row (ties ->
+    lowest index); waits for the result."""
+    x2d = _argmax_row(x)
+    x2d, qweight, scales, m, n, k = _check_w8(x2d, qweight, scales, torch.bfloat16, "W8A16 argmax")
+    _bind_stream(x2d)
+    rc, index, _value = abi.linear_w8a16_bf16_argmax_ptr(x2d.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+                                                         m, n, k)
+    if rc != 0:
+        raise _rc_error("ekernel_linear_w8a16_bf16_argmax", rc)
+    return index
+
+
+def linear_w8a16_bf16_argmax_device(x: torch.Tensor, qweight: torch.Tensor,
+                                    scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """As linear_w8a16_bf16_argmax with the (index, value) left on the GPU --
+    int64 [1] and float32 [1] tensors -- and no wait (usable under graph
+    capture)."""
+    x2d = _argmax_row(x)
+    x2d, qweight, scales, m, n, k = _check_w8(x2d, qweight, scales, torch.bfloat16, "W8A16 argmax")
+    index = torch.empty((1,), dtype=torch.int64, device=x2d.device)
+    value = torch.empty((1,), dtype=torch.float32, device=x2d.device)
+    _bind_stream(x2d)
+    rc = abi.linear_w8a16_bf16_argmax_device_ptr(x2d.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+                                                 index.data_ptr(), value.data_ptr(), m, n, k)
+    if rc != 0:
+        raise _rc_error("ekernel_linear_w8a16_bf16_argmax", rc)
+    return index, value
+
+
+def _argmax_row(x: torch.Tensor) -> torch.Tensor:
+    if x.device.type != _GPU or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a GPU torch.bfloat16 tensor")
+    if x.ndim == 1:
+        return x.reshape(1, -1)
+    if x.ndim == 2 and x.shape[0] == 1:
+        return x
+    raise ValueError(f"x must be a single row, got shape={tuple(x.shape)}")
+
+
 def _check_w4(x, qweight, scales, in_features, scale_ndim: int):
     if x.device.type != _GPU or x.dtype != torch.bfloat16 or x.ndim != 2:
         raise ValueError("x must be a 2D GPU torch.bfloat16 tensor")
@@ -311,4 +351,60 @@ def swiglu_bf16(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     rc = abi.swiglu_bf16_ptr(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel())
     if rc != 0:
         raise _rc_error("ekernel_swiglu_bf16", rc)
+    return out
+
+
+def swiglu_w4a16_bf16(
+    x: torch.Tensor,
+    gate_up_qweight: torch.Tensor,
+    gate_up_scales: torch.Tensor,
+    down_qweight: torch.Tensor,
+    down_scales: torch.Tensor,
+    intermediate_size: int,
+    gate_up_in_features: int | None = None,
+    down_in_features: int | None = None,
+) -> torch.Tensor:
+    """ckernel.py:585-649: the fused W4 SwiGLU MLP of one token (M = 1)."""
+    if x.device.type != _GPU or x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise ValueError("x must be a 2D GPU torch.bfloat16 tensor")
+    if gate_up_qweight.device.type != _GPU or gate_up_qweight.dtype != torch.uint8 or gate_up_qweight.ndim != 2:
+        raise ValueError("gate_up_qweight must be a 2D GPU torch.uint8 tensor")
+    if down_qweight.device.type != _GPU or down_qweight.dtype != torch.uint8 or down_qweight.ndim != 2:
+        raise ValueError("down_qweight must be a 2D GPU torch.uint8 tensor")
+    if gate_up_scales.device.type != _GPU or gate_up_scales.dtype != torch.float32 or gate_up_scales.ndim != 1:
+        raise ValueError("gate_up_scales must be a 1D GPU torch.float32 tensor")
+    if down_scales.device.type != _GPU or down_scales.dtype != torch.float32 or down_scales.ndim != 1:
+        raise ValueError("down_scales must be a 1D GPU torch.float32 tensor")
+    _same_device(x, gate_up_qweight, gate_up_scales, down_qweight, down_scales)
+    x = x.contiguous()
+    gate_up_qweight = gate_up_qweight.contiguous()
+    gate_up_scales = gate_up_scales.contiguous()
+    down_qweight = down_qweight.contiguous()
+    down_scales = down_scales.contiguous()
+    m, k = x.shape
+    intermediate_size = int(intermediate_size)
+    gate_up_in_features = k if gate_up_in_features is None else int(gate_up_in_features)
+    down_in_features = intermediate_size if down_in_features is None else int(down_in_features)
+    hidden_size = int(down_qweight.shape[0])
+    if m != 1:
+        raise ValueError("experimental fused W4 SwiGLU currently supports M=1 only")
+    if gate_up_in_features != k:
+        raise ValueError(f"gate_up_in_features={gate_up_in_features} does not match x K={k}")
+    if down_in_features != intermediate_size:
+        raise ValueError("down_in_features must equal intermediate_size")
+    if tuple(gate_up_qweight.shape) != (intermediate_size * 2, (gate_up_in_features + 1) // 2):
+        raise ValueError(
+            "gate_up_qweight shape must be "
+            f"{(intermediate_size * 2, (gate_up_in_features + 1) // 2)}, got {tuple(gate_up_qweight.shape)}")
+    if down_qweight.shape[1] != (down_in_features + 1) // 2:
+        raise ValueError(f"down_qweight packed K does not match down_in_features={down_in_features}")
+    if gate_up_scales.shape[0] != intermediate_size * 2 or down_scales.shape[0] != hidden_size:
+        raise ValueError("scale shapes do not match qweight rows")
+    out = torch.empty((m, hidden_size), dtype=torch.bfloat16, device=x.device)
+    _bind_stream(x)
+    rc = abi.swiglu_w4a16_bf16_ptr(x.data_ptr(), gate_up_qweight.data_ptr(), gate_up_scales.data_ptr(),
+                                   down_qweight.data_ptr(), down_scales.data_ptr(), out.data_ptr(), m,
+                                   hidden_size, intermediate_size, gate_up_in_features, down_in_features)
+    if rc != 0:
+        raise _rc_error("ekernel_swiglu_w4a16_bf16", rc)
     return out

@@ -74,6 +74,61 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((VM & 0xF) | (0x7 << 4) | (0xF << 8) | ((VM >> 4) << 14));
 }
 
+// expf as the reference's C library computes it (kernels.c:1592, 1647-1648
+// call the C library's expf).  glibc's expf (since 2.27; from Arm's
+// optimized-routines) evaluates exp(x) = 2^(k/32) * 2^(r/32) in double: a
+// 32-entry table of 2^(i/32), a degree-3 polynomial in r, one rounding to
+// float at the end.  Its x86-64 build for FMA hardware fuses the products
+// marked below; that build is what the reference runs on.  The same steps in
+// the same order give the same float for every input (|err| of the final
+// result up to 0.502 ulp, i.e. not always the correctly rounded value, which
+// is why a plain exp in double would disagree on a few inputs, e.g. x =
+// -0x1.9cp-4).  Table entries: the bits of 2^(i/32) rounded to double, less
+// i << 47 (the exponent is added back from k).
+__device__ __forceinline__ float ref_expf(float x) {
+#pragma clang fp contract(off)
+    if (!(__builtin_fabsf(x) < 88.0f)) {
+        if (x != x) return x + x;
+        if (x == -__builtin_inff()) return 0.0f;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    constexpr uint64_t T[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);     // fused
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);   // fused
+    const uint64_t t = T[ki % 32] + (ki << 47);
+    const double s = __builtin_bit_cast(double, t);
+    const double z = __builtin_fma(c0, r, c1);            // fused
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);                 // fused
+    y = __builtin_fma(z, r2, y);                          // fused
+    y = y * s;
+    return (float)y;
+}
+
+// kernels.c:1588-1593, 1645-1649: bf16(silu(g) * u), silu(g) = g / (1 + expf(-g)).
+__device__ __forceinline__ uint16_t swiglu_bf16_value(float g, float u) {
+#pragma clang fp contract(off)
+    const float silu = g / (1.0f + ref_expf(-g));
+    return f32_to_bf16(silu * u);
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kStripe = 128;        // bytes of each row per stripe: one full cache line

@@ -46,6 +46,23 @@ bool mfma_supports(size_t K, const void *A, const uint8_t *W);
 int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn);
 
+// Per-call timing of ecpu_hip_profile_begin/end: prof_begin records a start
+// event on `st` when profiling is on (else returns nullptr); prof_end records
+// the stop event and files the pair under `family` with its algorithmic bytes
+// and flops (nothing when ev0 is nullptr; family nullptr drops the start
+// event).
+hipEvent_t prof_begin(hipStream_t st);
+void prof_end(hipEvent_t ev0, hipStream_t st, const char *family, double bytes, double flops);
+
+// Per-device buffer of at least `bytes` for the fused entry points'
+// intermediates (logits, SwiGLU hidden row); same growth, retirement and
+// sharing rules as split_scratch.
+int aux_scratch(size_t bytes, void **Y, const char *fn);
+
+// True when p is device memory of the current HIP runtime (clears any error
+// the query leaves).
+bool is_device_pointer(const void *p);
+
 // Integer value of environment variable `name` (tuning overrides), else dflt.
 int env_int(const char *name, int dflt);
 
@@ -54,5 +71,31 @@ int env_int(const char *name, int dflt);
 // enqueued on `st`.
 int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn);
+
+// Fused W4 SwiGLU gate/up pass (one launch) for M = 1; ECPU_ERR_UNSUPPORTED
+// when the shape or alignment does not suit the stripe kernel.
+int run_swiglu_gate_up(size_t I, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *hidden,
+                       hipStream_t st);
+
+// Every linear format and M on the current stream (exact kernels; matrix
+// cores for M >= mfma_min_m()).
+int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+               const char *fn);
+
+// Elementwise bf16 SwiGLU of n elements on `st`.
+int run_swiglu_bf16(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t st, const char *fn);
+
+// W8A16 GEMV of one row + argmax of its bf16 logits on the current stream.
+// An output flagged *_on_device is written by the kernel (the call returns
+// without waiting); the others are host memory, filled after the stream has
+// been synchronized.
+int run_linear_argmax_w8a16(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S,
+                            size_t *out_index, float *out_value, bool index_on_device, bool value_on_device,
+                            const char *fn);
+
+// The W4 SwiGLU MLP of one token: C[H] = down(bf16(silu(g) * u)) with g, u
+// the first and second I rows of the gate/up GEMV over K inputs.
+int run_swiglu_w4(size_t H, size_t I, size_t K, const uint16_t *A, const uint8_t *Wgu, const float *Sgu,
+                  const uint8_t *Wd, const float *Sd, uint16_t *C, const char *fn);
 
 }  // namespace pilm

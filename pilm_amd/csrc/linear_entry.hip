@@ -1,5 +1,6 @@
-// extern "C" entry points of the quantized matrix-product path plus the two
-// other kernels bindings.py:_configure requires (ekernel_gemm,
+// extern "C" entry points of the quantized matrix-product path (the five
+// linear formats and the two fused epilogues, lm_head argmax and W4 SwiGLU)
+// plus the two other kernels bindings.py:_configure requires (ekernel_gemm,
 // ekernel_swiglu_bf16).  Each entry point keeps the reference's signature
 // and null-pointer rule (ECPU_ERR_PARAM), then checks that every buffer is
 // device memory large enough for the descriptor's shape before anything is
@@ -11,13 +12,8 @@
 #include <cstdint>
 #include <cstdlib>
 
+#include "gemv_device.h"
 #include "internal.h"
-
-namespace pilm {
-int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S,
-               void *C, const char *fn);
-enum : int { F_W8A32 = 0, F_W8A16 = 1, F_W4ROW = 2, F_W4G128 = 3, F_W4G32 = 4 };
-}  // namespace pilm
 
 using namespace pilm;
 
@@ -98,23 +94,6 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float *__restrict__
     C[idx] = acc;
 }
 
-// ------------------------------------------------------------ SwiGLU
-// kernels.c:1580-1596: bf16(silu(g) * u) with silu(g) = g / (1 + exp(-g)).
-// exp is evaluated in double and rounded once to float.
-__global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t *__restrict__ g,
-                                                          const uint16_t *__restrict__ u,
-                                                          uint16_t *__restrict__ out, size_t n) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const float gv = __uint_as_float((uint32_t)g[i] << 16);
-    const float uv = __uint_as_float((uint32_t)u[i] << 16);
-    const float e = (float)exp(-(double)gv);
-    const float silu = gv / (1.0f + e);
-    uint32_t b = __float_as_uint(silu * uv);
-    b += 0x7FFFu + ((b >> 16) & 1u);
-    out[i] = (uint16_t)(b >> 16);
-}
-
 extern "C" {
 
 int ekernel_linear_w8a32(const ekernel_linear_w8a32_desc_t *desc, const float *A, const int8_t *W,
@@ -177,9 +156,63 @@ int ekernel_swiglu_bf16(const uint16_t *gate, const uint16_t *up, uint16_t *out,
     if ((rc = check_buf(gate, n * 2, "gate", fn)) != ECPU_OK) return rc;
     if ((rc = check_buf(up, n * 2, "up", fn)) != ECPU_OK) return rc;
     if ((rc = check_buf(out, n * 2, "out", fn)) != ECPU_OK) return rc;
-    if (n == 0) return ECPU_OK;
-    swiglu_bf16_kernel<<<(n + 255) / 256, 256, 0, current_stream()>>>(gate, up, out, n);
-    return check_launch(fn);
+    return run_swiglu_bf16(gate, up, out, n, current_stream(), fn);
+}
+
+int ekernel_linear_w8a16_bf16_argmax(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A, const int8_t *W,
+                                     const float *scales, size_t *out_index, float *out_value, ekernel_isa_t isa) {
+    const char *fn = "ekernel_linear_w8a16_bf16_argmax";
+    (void)isa;
+    if (!desc || !A || !W || !scales || !out_index || !out_value) return fail(ECPU_ERR_PARAM, "%s: NULL argument", fn);
+    if (desc->M != 1 || desc->N == 0 || desc->K == 0)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: needs M == 1 and N, K > 0 (got M=%zu N=%zu K=%zu)", fn, desc->M,
+                    desc->N, desc->K);
+    const size_t N = desc->N, K = desc->K;
+    const size_t lim = (size_t)1 << 31;
+    if (N >= lim || K >= lim) return fail(ECPU_ERR_PARAM, "%s: N/K must be < 2^31", fn);
+    size_t w_bytes;
+    if (!mul_ok(N, K, &w_bytes)) return fail(ECPU_ERR_PARAM, "%s: shape overflows size_t", fn);
+    int rc;
+    if ((rc = check_buf(A, 2 * K, "A", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(W, w_bytes, "W", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(scales, 4 * N, "scales", fn)) != ECPU_OK) return rc;
+    // out_index / out_value may each be host memory (the reference's ctypes
+    // byref; the call then waits for the result) or device memory (written
+    // by the kernel; the call returns without waiting).
+    const bool idx_dev = is_device_pointer(out_index), val_dev = is_device_pointer(out_value);
+    if (idx_dev && (rc = check_buf(out_index, sizeof(size_t), "out_index", fn)) != ECPU_OK) return rc;
+    if (val_dev && (rc = check_buf(out_value, sizeof(float), "out_value", fn)) != ECPU_OK) return rc;
+    return run_linear_argmax_w8a16(N, K, A, (const uint8_t *)W, scales, out_index, out_value, idx_dev, val_dev, fn);
+}
+
+int ekernel_swiglu_w4a16_bf16(const ekernel_w4a16_swiglu_desc_t *desc, const uint16_t *A, const uint8_t *gate_up_W,
+                              const float *gate_up_scales, const uint8_t *down_W, const float *down_scales,
+                              uint16_t *C, ekernel_isa_t isa) {
+    const char *fn = "ekernel_swiglu_w4a16_bf16";
+    (void)isa;
+    if (!desc || !A || !gate_up_W || !gate_up_scales || !down_W || !down_scales || !C)
+        return fail(ECPU_ERR_PARAM, "%s: NULL argument", fn);
+    if (desc->M != 1 || desc->hidden_size == 0 || desc->intermediate_size == 0 || desc->gate_up_in_features == 0 ||
+        desc->down_in_features != desc->intermediate_size)
+        return fail(ECPU_ERR_UNSUPPORTED,
+                    "%s: needs M == 1, nonzero sizes and down_in_features == intermediate_size "
+                    "(got M=%zu hidden=%zu intermediate=%zu gate_up_in=%zu down_in=%zu)",
+                    fn, desc->M, desc->hidden_size, desc->intermediate_size, desc->gate_up_in_features,
+                    desc->down_in_features);
+    const size_t H = desc->hidden_size, I = desc->intermediate_size, K = desc->gate_up_in_features;
+    if (H >= ((size_t)1 << 31) || I >= ((size_t)1 << 30) || K >= ((size_t)1 << 31))
+        return fail(ECPU_ERR_PARAM, "%s: hidden/gate_up_in must be < 2^31, intermediate < 2^30", fn);
+    size_t gu_bytes, d_bytes;
+    if (!mul_ok(2 * I, (K + 1) / 2, &gu_bytes) || !mul_ok(H, (I + 1) / 2, &d_bytes))
+        return fail(ECPU_ERR_PARAM, "%s: shape overflows size_t", fn);
+    int rc;
+    if ((rc = check_buf(A, 2 * K, "A", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(gate_up_W, gu_bytes, "gate_up_W", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(gate_up_scales, 8 * I, "gate_up_scales", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(down_W, d_bytes, "down_W", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(down_scales, 4 * H, "down_scales", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(C, 2 * H, "C", fn)) != ECPU_OK) return rc;
+    return run_swiglu_w4(H, I, K, A, gate_up_W, gate_up_scales, down_W, down_scales, C, fn);
 }
 
 }  // extern "C"

@@ -563,6 +563,26 @@ static const char *family_name(int fmt, size_t M) {
     return names[fmt][M == 1 ? 0 : (M <= 4 ? 1 : 2)];
 }
 
+hipEvent_t prof_begin(hipStream_t st) {
+    if (!g_prof_on) return nullptr;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    hipEvent_t ev0 = pooled_event();
+    (void)hipEventRecord(ev0, st);
+    return ev0;
+}
+
+void prof_end(hipEvent_t ev0, hipStream_t st, const char *family, double bytes, double flops) {
+    if (!ev0) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (!family) {   // nothing to file: the start event goes back to the pool
+        g_event_pool.push_back(ev0);
+        return;
+    }
+    hipEvent_t ev1 = pooled_event();
+    (void)hipEventRecord(ev1, st);
+    g_prof.push_back({ev0, ev1, family, bytes, flops});
+}
+
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return (v && *v) ? atoi(v) : dflt;
@@ -656,12 +676,7 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
     }
     const dim3 grid((unsigned)(a.ntiles * a.pg));
     const dim3 block((unsigned)(64 * a.pl));
-    hipEvent_t ev0 = nullptr;
-    if (g_prof_on) {
-        std::lock_guard<std::mutex> lk(g_prof_mu);
-        ev0 = pooled_event();
-        (void)hipEventRecord(ev0, st);
-    }
+    hipEvent_t ev0 = prof_begin(st);
     if (use_mfma) {
         const int rc = run_mfma(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK) return rc;
@@ -678,14 +693,11 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         }
     }
     if (ev0) {
-        std::lock_guard<std::mutex> lk(g_prof_mu);
-        hipEvent_t ev1 = pooled_event();
-        (void)hipEventRecord(ev1, st);
         const double a_elt = (fmt == F_W8A32) ? 4.0 : 2.0;
         const double scale_bytes = 4.0 * (double)N * (group ? (double)a.G : 1.0);
         const double bytes = (double)N * a.row_bytes + scale_bytes + a_elt * (double)(M * K) + a_elt * (double)(M * N);
-        g_prof.push_back({ev0, ev1, use_mfma ? mfma_family_name(fmt) : family_name(fmt, M), bytes,
-                          2.0 * (double)M * (double)N * (double)K});
+        prof_end(ev0, st, use_mfma ? mfma_family_name(fmt) : family_name(fmt, M), bytes,
+                 2.0 * (double)M * (double)N * (double)K);
     }
     return check_launch(fn);
 }

@@ -346,11 +346,16 @@ __device__ __forceinline__ float dpp_quad_add(float x, int ctrl_is_swap2) {
     return x + __builtin_bit_cast(float, y);
 }
 
-template <int FMT, int MT, int D>
+// SW: the SwiGLU variant of the W4 per-row kernel (kernels.c:1598-1659).  W
+// holds 2N rows (gate rows 0..N-1, then the up rows), and tile t covers gate
+// rows 8t..8t+7 (lanes 0-31) with their up rows N+8t..N+8t+7 (lanes 32-63);
+// the epilogue writes C[i] = bf16(silu(g) * u) for the N gate rows.
+template <int FMT, int MT, int D, bool SW = false>
 __global__ __launch_bounds__(256) void gemv_quad_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W,
                                                        const float *__restrict__ S, void *__restrict__ C, int M,
                                                        int N, int K, int m0, int ntiles) {
     using Q = QuadFmt<FMT>;
+    static_assert(!SW || (FMT == F_W4ROW && MT == 1), "SwiGLU epilogue: W4 per-row, one activation row");
     extern __shared__ __align__(16) unsigned char lds[];
     const int wpb = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -386,7 +391,9 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(const void *__restrict__
     for (int i = 0; i < 2; ++i) {
         const int rr = 8 * i + (lane >> 3);
         const int q = (lane & 7) ^ ((rr >> 1) & 7);
-        src[i] = W + (size_t)min(row0 + rr, N - 1) * row_bytes + q * 16;
+        const size_t wrow = SW ? (size_t)(i ? N : 0) + (size_t)min(8 * tile + (rr & 7), N - 1)
+                               : (size_t)min(row0 + rr, N - 1);
+        src[i] = W + wrow * row_bytes + q * 16;
     }
     unsigned char *ring = lds + (size_t)wave * D * kQuadSlotBytes;
     auto issue = [&](int st) {
@@ -541,7 +548,16 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(const void *__restrict__
             const float s5 = dpp_quad_add(acc[m][3], 1);   // s5 / s7
             h = dpp_quad_add((s0 + s4) + (s1 + s5), 0);
         }
-        if (c == 0 && n < N) {
+        if constexpr (SW) {
+            // up-row sums of lanes 32-63 meet the gate-row sums of lanes 0-31
+            const float hu = __shfl_xor(h, 32);
+            const int i = 8 * tile + r;
+            if (lane < 32 && c == 0 && i < N) {
+                const float g = __uint_as_float((uint32_t)f32_to_bf16(h * S[i]) << 16);
+                const float u = __uint_as_float((uint32_t)f32_to_bf16(hu * S[N + i]) << 16);
+                ((uint16_t *)C)[(size_t)(m0 + m) * N + i] = swiglu_bf16_value(g, u);
+            }
+        } else if (c == 0 && n < N) {
             const float y = h * S[n];
             const size_t o = (size_t)(m0 + m) * N + n;
             if constexpr (FMT == F_W8A32)
@@ -552,13 +568,13 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(const void *__restrict__
     }
 }
 
-template <int FMT, int MT, int D>
+template <int FMT, int MT, int D, bool SW = false>
 int launch_quad_one(int wpb, int ntiles, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C,
                     int M, int N, int K, int m0) {
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     std::call_once(once, [] {
-        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_quad_kernel<FMT, MT, D>),
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_quad_kernel<FMT, MT, D, SW>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
     });
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
@@ -566,7 +582,7 @@ int launch_quad_one(int wpb, int ntiles, hipStream_t st, const void *A, const ui
     const size_t lds = (size_t)wpb * D * kQuadSlotBytes + (size_t)MT * rdw * 4;
     if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)((ntiles + wpb - 1) / wpb));
-    gemv_quad_kernel<FMT, MT, D><<<grid, 64 * wpb, lds, st>>>(A, W, S, C, M, N, K, m0, ntiles);
+    gemv_quad_kernel<FMT, MT, D, SW><<<grid, 64 * wpb, lds, st>>>(A, W, S, C, M, N, K, m0, ntiles);
     return ECPU_OK;
 }
 
@@ -647,6 +663,26 @@ int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
         if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
     }
     return ECPU_OK;
+}
+
+// Gate/up half of the fused W4 SwiGLU (kernels.c:1623-1659) for M = 1:
+// hidden[i] = bf16(silu(g_i) * u_i) from one pass over the 2I gate/up rows.
+// ECPU_ERR_UNSUPPORTED (nothing launched) when the stripe kernel cannot take
+// the shape: K not a multiple of 256, unaligned A or W, or activations too
+// long for LDS.
+int run_swiglu_gate_up(size_t I, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *hidden,
+                       hipStream_t st) {
+    if (I == 0) return ECPU_OK;
+    if (K == 0 || K % 256 != 0 || (((uintptr_t)A | (uintptr_t)W) & 15) != 0 || I >= ((size_t)1 << 30))
+        return ECPU_ERR_UNSUPPORTED;
+    const int nt = (int)((I + 7) / 8);
+    const int wpb = nt >= 2048 ? 4 : 1;
+    int depth = nt <= 512 ? 16 : 8;
+    const int env_depth = env_int("PILM_HIP_RING", 0);
+    if (env_depth == 8 || env_depth == 16) depth = env_depth;
+    if (depth == 16)
+        return launch_quad_one<F_W4ROW, 1, 16, true>(wpb, nt, st, A, W, S, hidden, 1, (int)I, (int)K, 0);
+    return launch_quad_one<F_W4ROW, 1, 8, true>(wpb, nt, st, A, W, S, hidden, 1, (int)I, (int)K, 0);
 }
 
 }  // namespace pilm

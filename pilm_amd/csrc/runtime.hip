@@ -86,6 +86,8 @@ struct Scratch {
     size_t nT;
     void *X;       // converted activations of the matrix-core path
     size_t nX;
+    void *Y;       // intermediates of the fused entry points
+    size_t nY;
 };
 static std::vector<Scratch> g_scratch;
 static std::vector<std::pair<int, void *>> g_retired;
@@ -109,7 +111,7 @@ int split_scratch(hipStream_t stream, size_t nfloat, size_t nticket, float **P, 
     for (auto &e : g_scratch)
         if (e.dev == dev) sc = &e;
     if (!sc) {
-        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0});
+        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0, nullptr, 0});
         sc = &g_scratch.back();
     }
     if (sc->nP < nfloat) {
@@ -146,7 +148,7 @@ int act_scratch(size_t bytes, void **X, const char *fn) {
     for (auto &e : g_scratch)
         if (e.dev == dev) sc = &e;
     if (!sc) {
-        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0});
+        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0, nullptr, 0});
         sc = &g_scratch.back();
     }
     if (sc->nX < bytes) {
@@ -159,6 +161,40 @@ int act_scratch(size_t bytes, void **X, const char *fn) {
     }
     *X = sc->X;
     return ECPU_OK;
+}
+
+int aux_scratch(size_t bytes, void **Y, const char *fn) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(ECPU_ERR_DEVICE, "%s: no current HIP device", fn);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    Scratch *sc = nullptr;
+    for (auto &e : g_scratch)
+        if (e.dev == dev) sc = &e;
+    if (!sc) {
+        g_scratch.push_back(Scratch{dev, nullptr, 0, nullptr, 0, nullptr, 0, nullptr, 0});
+        sc = &g_scratch.back();
+    }
+    if (sc->nY < bytes) {
+        const size_t want = std::max<size_t>(bytes, 1u << 20);
+        void *p = dev_alloc(want);
+        if (!p) return fail(ECPU_ERR_MEM, "%s: hipMalloc of %zu bytes of fused-op scratch failed", fn, want);
+        if (sc->Y) g_retired.push_back({dev, sc->Y});
+        sc->Y = p;
+        sc->nY = want;
+    }
+    *Y = sc->Y;
+    return ECPU_OK;
+}
+
+bool is_device_pointer(const void *p) {
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    const hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
 }
 
 static void free_scratch() {
@@ -175,6 +211,7 @@ static void free_scratch() {
         if (e.P) release(e.dev, e.P);
         if (e.T) release(e.dev, e.T);
         if (e.X) release(e.dev, e.X);
+        if (e.Y) release(e.dev, e.Y);
     }
     g_retired.clear();
     g_scratch.clear();

@@ -33,7 +33,7 @@ def arrays():
 def linear_cases(max_elems: int | None = None, prefix: str | None = None):
     out = []
     for c in manifest()["cases"]:
-        if c["fmt"] == "w8a16_argmax":
+        if c["fmt"] in ("w8a16_argmax", "swiglu_w4a16", "swiglu_bf16"):
             continue
         if prefix and not c["name"].startswith(prefix):
             continue
@@ -45,6 +45,26 @@ def linear_cases(max_elems: int | None = None, prefix: str | None = None):
 
 def argmax_cases():
     return [c for c in manifest()["cases"] if c["fmt"] == "w8a16_argmax"]
+
+
+def swiglu_cases(max_weights: int | None = None):
+    out = [c for c in manifest()["cases"] if c["fmt"] == "swiglu_w4a16"]
+    if max_weights is not None:
+        out = [c for c in out if c["I"] * (2 * c["K"] + c["N"]) <= max_weights]
+    return out
+
+
+def swiglu_inputs(case: dict):
+    """(x, gate_up_qweight, gate_up_scales, down_qweight, down_scales)."""
+    return _gen().make_swiglu_inputs(case["N"], case["I"], case["K"], case["seed"], case["special"])
+
+
+def swiglu_bf16_cases():
+    return [c for c in manifest()["cases"] if c["fmt"] == "swiglu_bf16"]
+
+
+def swiglu_bf16_inputs(case: dict):
+    return _gen().swiglu_bf16_inputs(case["special"])
 
 
 def inputs(case: dict):

@@ -1,4 +1,5 @@
-"""Write the golden vectors of the quantized linear path.
+"""Write the golden vectors of the quantized linear path and its fused
+epilogues (lm_head argmax, W4 SwiGLU MLP, elementwise SwiGLU).
 
 Run in a container that has the piLM sources, after `make -C oracle`:
 
@@ -148,6 +149,46 @@ def argmax_cases():
     return res
 
 
+def swiglu_cases():
+    """(name, H, I, K, seed, special) of the fused W4 SwiGLU (M = 1)."""
+    res = []
+    seed = 7000
+    for (h, i, k) in ((1, 1, 1), (7, 9, 17), (16, 24, 64), (33, 70, 129), (64, 100, 256), (130, 257, 513),
+                      (96, 256, 512), (200, 1000, 768), (64, 264, 256)):
+        seed += 11
+        res.append((f"swiglu_w4_H{h}_I{i}_K{k}", h, i, k, seed, None))
+    for special in ("large_gate", "tiny_gate"):
+        seed += 11
+        res.append((f"swiglu_w4_{special}", 64, 512, 256, seed, special))
+    # the MLP of the two decode configurations: Qwen3-1.7B and Qwen3-8B
+    res.append(("swiglu_w4_qwen3_1p7b", 2048, 6144, 2048, 7500, None))
+    res.append(("swiglu_w4_qwen3_8b", 4096, 12288, 4096, 7501, None))
+    return res
+
+
+def make_swiglu_inputs(h: int, i: int, k: int, seed: int, special: str | None = None):
+    x = S.activations_bf16(seed, 1, k)
+    gu = S.weights_i4_packed(seed + 1, 2 * i, k)
+    gs = S.scales_uniform(seed + 2, (2 * i,), fp16_round=False)
+    dw = S.weights_i4_packed(seed + 3, h, i)
+    ds = S.scales_uniform(seed + 4, (h,), fp16_round=False)
+    if special == "large_gate":       # |g| up to ~1e3: expf overflows / underflows, silu saturates
+        gs = (gs * np.float32(300.0)).astype(np.float32)
+    elif special == "tiny_gate":      # |g| ~ 1e-6: silu(g) ~ g / 2
+        gs = (gs * np.float32(1e-6)).astype(np.float32)
+    return x, gu, gs, dw, ds
+
+
+def swiglu_bf16_inputs(which: str):
+    """Every bf16 bit pattern as the gate, against u = 1.0 or seeded u bits."""
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    if which == "u_one":
+        u = np.full(65536, 0x3F80, np.uint16)
+    else:
+        u = S.activations_bf16(7900, 1, 65536).reshape(-1)
+    return g, u
+
+
 def main() -> int:
     if not O.ref_available():
         O.build(ref=True)
@@ -173,6 +214,21 @@ def main() -> int:
         manifest["cases"].append({"name": name, "fmt": "w8a16_argmax", "M": 1, "N": n, "K": k, "seed": seed,
                                   "special": "ties" if name == "argmax_ties" else None,
                                   "input_sha256": sha(x, w, s), "index": idx, "value": val})
+    for (name, h, i, k, seed, special) in swiglu_cases():
+        ins = make_swiglu_inputs(h, i, k, seed, special)
+        y = O.swiglu_w4a16_bf16(*ins, i, impl="ref")
+        arrays[name] = y
+        manifest["cases"].append({"name": name, "fmt": "swiglu_w4a16", "M": 1, "N": h, "K": k, "I": i,
+                                  "seed": seed, "special": special, "input_sha256": sha(*ins),
+                                  "output_sha256": sha(y), "full": True})
+    for which in ("u_one", "u_seeded"):
+        g, u = swiglu_bf16_inputs(which)
+        y = O.swiglu_bf16(g, u, impl="ref")
+        name = f"swiglu_bf16_all_gates_{which}"
+        arrays[name] = y
+        manifest["cases"].append({"name": name, "fmt": "swiglu_bf16", "M": 1, "N": 65536, "K": 0, "seed": 7900,
+                                  "special": which, "input_sha256": sha(g, u), "output_sha256": sha(y),
+                                  "full": True})
     np.savez_compressed(OUT / "linear_golden.npz", **arrays)
     (OUT / "linear_golden.json").write_text(json.dumps(manifest, indent=1) + "\n")
     print(f"wrote {len(manifest['cases'])} cases")

@@ -55,7 +55,8 @@ def test_library_loads_and_configures(lib_path):
     assert abi.detect_isa() == "gfx950"
     assert all(abi.available_kernel_symbols()[s] for s in (
         "ekernel_gemm", "ekernel_linear_w8a32", "ekernel_linear_w8a16_bf16", "ekernel_linear_w4a16_bf16",
-        "ekernel_linear_w4a16g32_bf16", "ekernel_linear_w4a16g128_bf16", "ekernel_swiglu_bf16"))
+        "ekernel_linear_w4a16g32_bf16", "ekernel_linear_w4a16g128_bf16", "ekernel_swiglu_bf16",
+        "ekernel_linear_w8a16_bf16_argmax", "ekernel_swiglu_w4a16_bf16"))
     vt = lib.edevice_get  # exported registry accessor
     assert vt is not None
 
@@ -65,6 +66,9 @@ def test_descriptor_layout_matches_reference():
     assert ctypes.sizeof(abi.EkernelLinearW8A32Desc) == 24
     assert abi.EcpuConfig.device_type.offset == 32
     assert ctypes.sizeof(abi.EkernelGemmDesc) == 44 or ctypes.sizeof(abi.EkernelGemmDesc) == 48
+    # ekernel_w4a16_swiglu_desc_t (kernel/api.h:44-50): five size_t
+    assert ctypes.sizeof(abi.EkernelW4A16SwiGLUDesc) == 40
+    assert abi.EkernelW4A16SwiGLUDesc.down_in_features.offset == 32
 
 
 def test_missing_symbol_fails_loudly(tmp_path, monkeypatch):
