@@ -15,9 +15,11 @@ replayed.
 Printed JSON line:
   value        algorithmic GB/s of the whole step (weights + scales +
                activations + outputs, each counted once) / wall time
-  roofline     the g128 GEMV kernel's algorithmic GB/s per launch: HIP events
-               on the replay stream around the timed replays, divided by the
-               launches (it is the step's only kernel), against 8 TB/s
+  roofline     the g128 GEMV kernels' algorithmic GB/s per launch (the
+               group-quad kernel for the 196 projections, the 64-row exact
+               kernel for lm_head; they are the step's only kernels): HIP
+               events on the replay stream around the timed replays, divided
+               by the launches, against 8 TB/s
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
   sweep        per-shape GB/s at M = 1, 4, 16 (only with --sweep)
@@ -45,8 +47,11 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-KERNEL_SRC = ROOT / "pilm_amd" / "csrc" / "linear_exact.hip"
-GEMV_KERNEL = "gemv_exact_kernel<3, 1>"          # W4A16 group-128, one activation row
+KERNEL_SRCS = [ROOT / "pilm_amd" / "csrc" / f for f in ("linear_exact.hip", "linear_rows.hip", "gemv_device.h")]
+# The kernels of the W4A16 group-128 GEMV path at M=1: the group-quad kernel
+# for the projections (N <= 65536), the 64-row exact kernel for lm_head.
+GEMV_KERNELS = ("gemv_gq_kernel<3, 1,", "gemv_exact_kernel<3, 1>")
+GEMV_KERNEL = "gemv_gq_kernel<3, 1, *> + gemv_exact_kernel<3, 1>"
 TRAFFIC_FILE = ROOT / "profiles" / "gemv_exact_w4a16g128_m1_qwen3_1p7b_decode.traffic.txt"
 CALIB_BYTES = 1 << 30                              # copy kernel: reads and writes 1 GiB
 LAYERS = 28
@@ -137,21 +142,25 @@ def time_graph(torch, g, steps: int, warmup: int, events: bool = False):
 
 
 def roofline(gpu_sec: float, launches: int, bytes_per_launch: float) -> dict:
-    """The g128 GEMV is the only kernel of the step: its average launch
-    duration is the HIP-event time of the timed replays over the launches."""
+    """The g128 GEMV kernels are the only kernels of the step: their average
+    launch duration is the HIP-event time of the timed replays over the
+    launches."""
     avg = gpu_sec / launches
     achieved = bytes_per_launch / avg / 1e9
     traffic, traffic_note = measured_traffic()
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": GEMV_KERNEL + " (K split folded inside the kernel)",
+            "kernel": GEMV_KERNEL + " (K divided among waves, folded inside the kernel)",
             "launches": launches, "avg_launch_us": round(avg * 1e6, 3),
             "alg_bytes_per_launch": round(bytes_per_launch), "traffic_source": traffic_note}
 
 
 def source_hash() -> str:
     import hashlib
-    return hashlib.sha256(KERNEL_SRC.read_bytes()).hexdigest()
+    h = hashlib.sha256()
+    for f in KERNEL_SRCS:
+        h.update(f.read_bytes())
+    return h.hexdigest()
 
 
 def measured_traffic():
@@ -280,14 +289,25 @@ def _pick(means: dict, needle: str):
     return hits[0][1]
 
 
+def _pick_all(means: dict, needles) -> tuple:
+    """Dispatch-weighted mean and dispatch count over every kernel whose name
+    contains one of `needles`."""
+    hits = [v for k, v in means.items() if any(n in k for n in needles)]
+    if not hits:
+        raise SystemExit(f"no kernel matching {needles!r}")
+    total = sum(m * n for m, n in hits)
+    count = sum(n for _, n in hits)
+    return total / count, count
+
+
 def traffic_summary(fetch_csv: str, write_csv: str) -> dict:
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the GEMV and of the
     copy kernel; the copy kernel moves CALIB_BYTES each way, which fixes the
     bytes each counter unit stands for."""
     f = _counter_means(fetch_csv, "FETCH_SIZE")
     w = _counter_means(write_csv, "WRITE_SIZE")
-    (gf, nf), (cf, _) = _pick(f, GEMV_KERNEL), _pick(f, "neg_kernel")
-    (gw, nw), (cw, _) = _pick(w, GEMV_KERNEL), _pick(w, "neg_kernel")
+    (gf, nf), (cf, _) = _pick_all(f, GEMV_KERNELS), _pick(f, "neg_kernel")
+    (gw, nw), (cw, _) = _pick_all(w, GEMV_KERNELS), _pick(w, "neg_kernel")
     ff, fw = CALIB_BYTES / (cf * 1024), CALIB_BYTES / (cw * 1024)
     fetch_b, write_b = gf * 1024 * ff, gw * 1024 * fw
     step_alg = sum(alg_bytes(1, n, k) for (_, n, k) in step_shapes())

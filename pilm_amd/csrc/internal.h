@@ -72,6 +72,12 @@ int env_int(const char *name, int dflt);
 int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn);
 
+// Exact GEMV of the group formats (3 W4A16 g128, 4 g32) with 16-row tiles
+// and K divided among up to four waves per tile, for K a multiple of 256 and
+// 16-byte aligned A and W; ECPU_ERR_UNSUPPORTED when LDS cannot hold a row.
+int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+                   hipStream_t st, const char *fn);
+
 // Fused W4 SwiGLU gate/up pass (one launch) for M = 1; ECPU_ERR_UNSUPPORTED
 // when the shape or alignment does not suit the stripe kernel.
 int run_swiglu_gate_up(size_t I, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *hidden,

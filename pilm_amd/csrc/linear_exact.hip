@@ -685,11 +685,18 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         const int rc = run_rows(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK) return rc;
     } else {
-        for (size_t m0 = 0; m0 < M; m0 += 4) {
-            const int mt = (int)std::min<size_t>(4, M - m0);
-            if (launch_exact(fmt, mt, grid, block, exact_lds_bytes(a, groups_per_stripe, mt), st, a, (int)m0) !=
-                ECPU_OK)
-                return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+        // group formats below 65536 rows: 16-row tiles, K divided among waves
+        int rc = ECPU_ERR_UNSUPPORTED;
+        if (group && env_int("PILM_HIP_GQ", N <= 65536 ? 1 : 0) != 0)
+            rc = run_group_quad(fmt, M, N, K, A, W, S, C, st, fn);
+        if (rc != ECPU_OK && rc != ECPU_ERR_UNSUPPORTED) return rc;
+        if (rc == ECPU_ERR_UNSUPPORTED) {
+            for (size_t m0 = 0; m0 < M; m0 += 4) {
+                const int mt = (int)std::min<size_t>(4, M - m0);
+                if (launch_exact(fmt, mt, grid, block, exact_lds_bytes(a, groups_per_stripe, mt), st, a, (int)m0) !=
+                    ECPU_OK)
+                    return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+            }
         }
     }
     if (ev0) {

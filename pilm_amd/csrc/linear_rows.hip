@@ -607,12 +607,573 @@ int launch_quad_fmt(int depth, int mt, int wpb, int ntiles, hipStream_t st, cons
     }
 }
 
+// ------------------------------------------------------------------ chain
+// With few 16-row tiles (a few thousand rows and a long K: o_proj, down) the
+// quad kernel runs one wave per tile, i.e. on one SIMD of a CU, and is VALU
+// bound.  The chain kernel gives each 16-row tile CS waves (CS SIMDs of one
+// CU) and divides the quad lane's chains among them, so every lane carries
+// fewer chains:
+//   int4: CS = 4 (one chain per lane) or 2; lane (r, c) of wave w owns slots
+//         g = w * (4/CS) + i of chain group c, nibble 2(c&1) + (g>>1) + 4(g&1)
+//         of the dwords of parity c>>1 -- the quad kernel's chains
+//         {0,4,1,5} / {2,6,3,7} of the lo (c < 2) or hi half;
+//   int8: CS = 2; wave w owns byte 2(c&1) + w of the dwords of parity c>>1
+//         (chain 2c + w).
+// A weight is decoded with one sign-extending bit-field extract and one
+// conversion.  Each workgroup first converts its activation rows to fp32 in
+// LDS, laid out chain by chain (the 16 values a chain meets in one stripe are
+// contiguous), so a lane reads them with four 16-byte loads that every lane of
+// the chain shares.  The waves share one ring of D stripe slots (waves 0 and
+// 1 issue a stripe's two DMA instructions) with one barrier per stripe; at
+// the end the chain sums meet in LDS and one lane per row adds them in the
+// reference's order.
+template <int FMT, int CS>
+struct ChainFmt {
+    static constexpr bool w8 = FMT != F_W4ROW;
+    static constexpr int nchain = w8 ? 8 : 16;     // chains per row
+    static constexpr int gslots = w8 ? 2 : 4;      // chain slots of a lane group, all waves
+    static constexpr int slots = gslots / CS;      // chain slots per lane
+    static_assert(slots >= 1 && gslots % CS == 0, "chain split");
+    static constexpr int width = w8 ? 8 : 4;       // bits per weight
+    static __device__ __forceinline__ int bit(int c, int g) {
+        return w8 ? 8 * (2 * (c & 1) + g) : 4 * (2 * (c & 1) + (g >> 1) + 4 * (g & 1));
+    }
+    static __device__ __forceinline__ int chain(int c, int g) {
+        return w8 ? 4 * (c >> 1) + 2 * (c & 1) + g : 8 * (c >> 1) + 2 * (c & 1) + (g >> 1) + 4 * (g & 1);
+    }
+    // Position of activation k in the chain-major layout: stripe s, chain,
+    // then the chain's 16 values of the stripe in the lane's word order
+    // t = 2j + qq (chunk j, dword q = parity + 2qq).
+    static __device__ __forceinline__ int perm(int k) {
+        if constexpr (w8) {
+            const int s = k >> 7, j = (k >> 4) & 7, q = (k >> 2) & 3, b = k & 3;
+            return ((s * 8 + 4 * (q & 1) + b) << 4) + 2 * j + (q >> 1);
+        } else {
+            const int s = k >> 8, j = (k >> 5) & 7, q = (k >> 3) & 3, p = k & 7;
+            return ((s * 16 + 8 * (q & 1) + p) << 4) + 2 * j + (q >> 1);
+        }
+    }
+};
+
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int FMT, int MT, int D, int CS>
+__global__ __launch_bounds__(256) void gemv_chain_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W,
+                                                        const float *__restrict__ S, void *__restrict__ C, int N,
+                                                        int K, int m0) {
+    using F = ChainFmt<FMT, CS>;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 2, c = lane & 3, par = c >> 1;
+    const int row0 = blockIdx.x * 16;
+    const size_t row_bytes = F::w8 ? (size_t)K : (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    unsigned char *ring = lds;
+    constexpr int kEbytes = FMT == F_W8A32 ? 4 : 2;   // bytes per activation
+    float *act = (float *)(lds + (size_t)D * kQuadSlotBytes);
+    float *red = act + (size_t)MT * K;
+
+    // Stripe DMA: instruction i (issued by wave i, i < 2) fetches rows
+    // 8i + lane/8 of the tile, chunk (lane & 7) ^ ((row >> 1) & 7).
+    const bool issuer = wave < 2;
+    const int ii = wave & 1;
+    const int rr = 8 * ii + (lane >> 3);
+    const uint8_t *src = W + (size_t)min(row0 + rr, N - 1) * row_bytes + (((lane & 7) ^ ((rr >> 1) & 7)) << 4);
+    auto issue = [&](int st) {
+        __builtin_amdgcn_global_load_lds((const void *)(src + (size_t)st * kStripe),
+                                         (lds_void *)(ring + (st % D) * kQuadSlotBytes + ii * 1024), 16, 0, kNT);
+    };
+    // Rounds of R stripes: the issuers keep D - R stripes in flight; a round
+    // starts once its R stripes have landed (and, by the barrier, once every
+    // wave is done with the previous round, whose slots then take the next R
+    // stripes).  Within a round the LDS reads of stripe u+1 are issued before
+    // stripe u is computed.  Rounds are complete (no branch inside, so each
+    // compute waits only for its own reads); a tail of ns % R stripes follows.
+    constexpr int R = 4;
+    static_assert(D % R == 0 && D >= 2 * R, "ring depth");
+
+    // Activation rows m0.. -> fp32, chain-major (16-byte loads, four per
+    // lane in flight), then the first D - R stripes.  (Copying the
+    // activations by DMA behind the stripes instead measured slower.)
+    {
+        constexpr int epv = 16 / kEbytes;   // elements per 16-byte vector
+        const int nvec = K / epv, nthr = 64 * CS;
+#pragma unroll 1
+        for (int m = 0; m < MT; ++m) {
+            const u32x4 *asrc = (const u32x4 *)((const unsigned char *)A_ + (size_t)(m0 + m) * K * kEbytes);
+            float *dst = act + (size_t)m * K;
+#pragma unroll 1
+            for (int v0 = 0; v0 < nvec; v0 += 4 * nthr) {
+                u32x4 buf[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int v = v0 + u * nthr + (int)threadIdx.x;
+                    if (v < nvec) buf[u] = asrc[v];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int v = v0 + u * nthr + (int)threadIdx.x;
+                    if (v >= nvec) continue;
+#pragma unroll
+                    for (int e = 0; e < epv; ++e) {
+                        const uint32_t word = buf[u][epv == 4 ? e : e >> 1];
+                        dst[F::perm(v * epv + e)] =
+                            epv == 4 ? __uint_as_float(word) : ((e & 1) ? bf16_hi(word) : bf16_lo(word));
+                    }
+                }
+            }
+        }
+    }
+    if (issuer) {
+#pragma unroll 1
+        for (int t = 0; t < D - R; ++t)
+            if (t < ns) issue(t);
+    }
+    // (the first round's barrier orders the activation writes before any read)
+
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = r * kStripe + ((j ^ swz) << 4) + 4 * par;
+    int bits[F::slots], chn[F::slots];
+#pragma unroll
+    for (int i = 0; i < F::slots; ++i) {
+        bits[i] = F::bit(c, wave * F::slots + i);
+        chn[i] = F::chain(c, wave * F::slots + i);
+    }
+    float acc[MT][F::slots];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < F::slots; ++i) acc[m][i] = 0.0f;
+
+    uint32_t xw[2][16];
+    f32x4 av[2][MT][F::slots][4];
+    auto load = [&](int s, int b) {
+        const unsigned char *slot = ring + (s % D) * kQuadSlotBytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            xw[b][2 * j] = *(const uint32_t *)(slot + off[j]);
+            xw[b][2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < F::slots; ++i) {
+                const f32x4 *ap = (const f32x4 *)(act + (size_t)m * K + ((s * F::nchain + chn[i]) << 4));
+#pragma unroll
+                for (int v = 0; v < 4; ++v) av[b][m][i][v] = ap[v];
+            }
+    };
+    auto compute = [&](int b) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < F::slots; ++i)
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const float w = (float)(int)__builtin_amdgcn_sbfe((int)xw[b][t], bits[i], F::width);
+                    acc[m][i] = __builtin_fmaf(av[b][m][i][t >> 2][t & 3], w, acc[m][i]);
+                }
+    };
+
+    const int nfull = ns / R * R;
+#pragma unroll 1
+    for (int s0 = 0; s0 < nfull; s0 += R) {
+        if (issuer) {
+            if (s0 + D - R - 1 < ns)
+                wait_vmcnt<D - 2 * R>();   // stripes s0+R .. s0+D-R-1 may still fly
+            else
+                wait_vmcnt<0>();
+        }
+        lds_sync();
+        if (issuer) {
+#pragma unroll
+            for (int u = 0; u < R; ++u)
+                if (s0 + D - R + u < ns) issue(s0 + D - R + u);
+        }
+        load(s0, 0);
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            // keep the order: reads of u, reads of u+1, then the math of u
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 1 < R) load(s0 + u + 1, (u + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(u & 1);
+        }
+    }
+    // The last ns % R stripes (already issued), one at a time.
+#pragma unroll 1
+    for (int s = nfull; s < ns; ++s) {
+        if (issuer) wait_vmcnt<0>();
+        lds_sync();
+        load(s, 0);
+        compute(0);
+    }
+
+    // The chain sums meet in LDS; lane 4r of wave 0 adds row r's chains in
+    // the reference's order: hsum ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) of the 8
+    // lanes (int4: of lo[l] + hi[l]), times the row scale.
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < F::slots; ++i) red[(m * F::gslots + wave * F::slots + i) * 64 + lane] = acc[m][i];
+    lds_sync();
+    const int n = row0 + r;
+    if (wave != 0 || c != 0 || n >= N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const float *rb = red + m * F::gslots * 64 + 4 * r;
+        float l8[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            if constexpr (F::w8) {
+                const int b = l & 3;
+                l8[l] = rb[(b & 1) * 64 + 2 * (l >> 2) + (b >> 1)];
+            } else {
+                const int cl = (l >> 1) & 1, gl = ((l >> 2) & 1) + 2 * (l & 1);
+                l8[l] = rb[gl * 64 + cl] + rb[gl * 64 + cl + 2];
+            }
+        }
+        const float y = hsum8(l8) * S[n];
+        const size_t o = (size_t)(m0 + m) * N + n;
+        if constexpr (FMT == F_W8A32)
+            ((float *)C)[o] = y;
+        else
+            ((uint16_t *)C)[o] = f32_to_bf16(y);
+    }
+}
+
+template <int FMT, int MT, int D, int CS>
+size_t chain_lds_bytes(int K) {
+    // ring, fp32 activations, chain sums
+    return (size_t)D * kQuadSlotBytes + (size_t)MT * K * 4 + (size_t)MT * ChainFmt<FMT, CS>::gslots * 64 * 4;
+}
+
+template <int FMT, int MT, int D, int CS>
+int launch_chain_one(int ntiles, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int N,
+                     int K, int m0) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_chain_kernel<FMT, MT, D, CS>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = chain_lds_bytes<FMT, MT, D, CS>(K);
+    if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
+    gemv_chain_kernel<FMT, MT, D, CS><<<ntiles, 64 * CS, lds, st>>>(A, W, S, C, N, K, m0);
+    return ECPU_OK;
+}
+
+template <int FMT, int CS>
+int launch_chain_mt(int mt, int ntiles, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C,
+                    int N, int K, int m0) {
+    switch (mt) {
+        case 1: return launch_chain_one<FMT, 1, 16, CS>(ntiles, st, A, W, S, C, N, K, m0);
+        case 2: return launch_chain_one<FMT, 2, 16, CS>(ntiles, st, A, W, S, C, N, K, m0);
+        case 3: return launch_chain_one<FMT, 3, 16, CS>(ntiles, st, A, W, S, C, N, K, m0);
+        default: return launch_chain_one<FMT, 4, 16, CS>(ntiles, st, A, W, S, C, N, K, m0);
+    }
+}
+
+// Activation rows per launch of the chain kernel: 4, 2 or 1, whichever is the
+// largest that fits LDS (the fp32 activations take 4K bytes per row).
+template <int FMT, int CS>
+int chain_rows_per_launch(int K) {
+    if (chain_lds_bytes<FMT, 4, 16, CS>(K) <= kRowMaxLds) return 4;
+    if (chain_lds_bytes<FMT, 2, 16, CS>(K) <= kRowMaxLds) return 2;
+    if (chain_lds_bytes<FMT, 1, 16, CS>(K) <= kRowMaxLds) return 1;
+    return 0;
+}
+
+// ------------------------------------------------------------------ group quad
+// Group formats (W4A16 g128 / g32) with the quad layout: 16-row tiles, lane
+// 4r + c serves row r with the quad kernel's int4 chains (the packing is the
+// per-row format's), and the P waves of a workgroup take consecutive ranges
+// of the tile's stripes.  A group's block sum is the int4 dot over the group
+// (kernels.c:1130-1140: lo/hi chains over its 16-element chunks, hsum of
+// lo + hi), reduced across the quad with DPP in the reference's order as soon
+// as the group's words are done; lane c = 0 parks it in LDS.  After a barrier
+// wave 0 folds every row's blocks in group order, acc = fma(block, scale,
+// acc), the reference's sequence exactly, so K can be divided among the
+// waves without changing a bit.  The row scales of the tile are copied to
+// LDS at the start (DMA, behind the activations), so the fold waits for
+// nothing.
+template <int FMT, int MT, int D, int P>
+__global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restrict__ A, const uint8_t *__restrict__ W,
+                                                     const float *__restrict__ S, uint16_t *__restrict__ C, int N,
+                                                     int K, int m0) {
+    using Q = QuadFmt<F_W4ROW>;
+    constexpr int GS = FMT == F_W4G128 ? 128 : 32;   // group size
+    constexpr int GPS = 256 / GS;                    // groups per stripe: 2 or 8
+    constexpr int WPG = 16 / GPS;                    // lane words per group: 8 or 2
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 2, c = lane & 3, par = c >> 1;
+    const int row0 = blockIdx.x * 16;
+    const size_t row_bytes = (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    const int G = K / GS;
+    const int rdw = K / 2;                          // activation dwords per row
+    const int sps = (ns + P - 1) / P;
+    const int sb = min(ns, wave * sps);
+    const int nsw = min(ns, sb + sps) - sb;         // this wave's stripes (may be 0)
+    unsigned char *act = lds + (size_t)P * D * kQuadSlotBytes;
+    float *scl = (float *)(act + (size_t)MT * rdw * 4);   // [16][G]
+    float *blk = scl + 16 * G;                             // [MT][16][G]
+
+    // Activation rows (16-byte DMA, 256 dwords per instruction) and the
+    // tile's scales (4-byte DMA, 64 per instruction), dealt round-robin.
+    {
+        int issued = 0;
+        const int total = MT * rdw;
+        const uint32_t *a = (const uint32_t *)A + (size_t)m0 * rdw;
+#pragma unroll 1
+        for (int q = wave; q * 256 < total; q += P) {
+            const int g = q * 256 + 4 * lane;
+            if (g < total)
+                __builtin_amdgcn_global_load_lds((const void *)(a + g), (lds_void *)(act + (size_t)q * 1024), 16, 0,
+                                                 0);
+            if ((++issued & 15) == 0) wait_vmcnt<16>();
+        }
+        const int nscl = 16 * G;
+#pragma unroll 1
+        for (int q = wave; q * 64 < nscl; q += P) {
+            const int i = q * 64 + lane;
+            if (i < nscl) {
+                const int rr = i / G, g = i - rr * G;
+                __builtin_amdgcn_global_load_lds((const void *)(S + (size_t)min(row0 + rr, N - 1) * G + g),
+                                                 (lds_void *)(scl + q * 64), 4, 0, 0);
+            }
+            if ((++issued & 15) == 0) wait_vmcnt<16>();
+        }
+    }
+
+    // This wave's stripes sb .. sb+nsw-1 through its own ring of D slots.
+    const uint8_t *src[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rr = 8 * i + (lane >> 3);
+        const int q = (lane & 7) ^ ((rr >> 1) & 7);
+        src[i] = W + (size_t)min(row0 + rr, N - 1) * row_bytes + q * 16;
+    }
+    unsigned char *ring = lds + (size_t)wave * D * kQuadSlotBytes;
+    auto issue = [&](int t) {   // t: index within this wave's range
+        unsigned char *slot = ring + (t % D) * kQuadSlotBytes;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)(sb + t) * kStripe),
+                                             (lds_void *)(slot + i * 1024), 16, 0, kNT);
+    };
+#pragma unroll
+    for (int t = 0; t < D - 2; ++t)
+        if (t < nsw) issue(t);
+    if (nsw >= D - 2)
+        wait_vmcnt<2 * (D - 2)>();   // activation and scale copies, older than the stripes
+    else
+        wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");
+
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = r * kStripe + ((j ^ swz) << 4) + 4 * par;
+    const uint32_t *my_act = (const uint32_t *)act + Q::act_index(0, c);
+    const uint32_t shift = 8u * (c & 1);
+    const uint32_t magic = opaque_magic();
+
+    float acc[MT][4];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[m][k] = 0.0f;
+
+    auto load = [&](int t, uint32_t (&x)[16], uint32_t (&av)[MT][32]) {
+        const unsigned char *slot = ring + (t % D) * kQuadSlotBytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[2 * j] = *(const uint32_t *)(slot + off[j]);
+            x[2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+        const int st = sb + t;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const uint32_t *ap = my_act + (size_t)m * rdw + Q::act_index(16 * st + u, 0);
+                av[m][2 * u] = ap[0];
+                av[m][2 * u + 1] = ap[2];
+            }
+    };
+    // One stripe: GPS groups of WPG words each; after each group its block
+    // sums are reduced across the quad and parked.
+    auto compute = [&](int t, const uint32_t (&x)[16], const uint32_t (&av)[MT][32]) {
+        const int g0 = (sb + t) * GPS;
+#pragma unroll
+        for (int gi = 0; gi < GPS; ++gi) {
+#pragma unroll
+            for (int u = gi * WPG; u < (gi + 1) * WPG; ++u) {
+                const uint32_t v = (x[u] ^ 0x88888888u) >> shift;
+                const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+                const h2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+                const h2 bias16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+                const h2 qa = __builtin_bit_cast(h2, (v & 0x000F000Fu) | magic) + bias;
+                const h2 qb = __builtin_bit_cast(h2, (v & 0x00F000F0u) | magic) * sixteenth + bias16;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const uint32_t p0 = av[m][2 * u], p1 = av[m][2 * u + 1];
+                    acc[m][0] = __builtin_fmaf(bf16_lo(p0), (float)qa.x, acc[m][0]);
+                    acc[m][1] = __builtin_fmaf(bf16_lo(p1), (float)qa.y, acc[m][1]);
+                    acc[m][2] = __builtin_fmaf(bf16_hi(p0), (float)qb.x, acc[m][2]);
+                    acc[m][3] = __builtin_fmaf(bf16_hi(p1), (float)qb.y, acc[m][3]);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const float s0 = dpp_quad_add(acc[m][0], 1);
+                const float s4 = dpp_quad_add(acc[m][1], 1);
+                const float s1 = dpp_quad_add(acc[m][2], 1);
+                const float s5 = dpp_quad_add(acc[m][3], 1);
+                const float h = dpp_quad_add((s0 + s4) + (s1 + s5), 0);
+                if (c == 0) blk[(m * 16 + r) * G + g0 + gi] = h;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[m][k] = 0.0f;
+            }
+        }
+    };
+    uint32_t xa[16], xb[16];
+    uint32_t aa[MT][32], ab[MT][32];
+    if (nsw > 0) {
+        if (nsw >= D - 2)
+            wait_vmcnt<2 * (D - 3)>();
+        else
+            wait_vmcnt<0>();
+        load(0, xa, aa);
+    }
+    int t = 0;
+#pragma unroll 1
+    for (; t + 1 < nsw; t += 2) {
+        if (t + D - 2 < nsw) issue(t + D - 2);
+        if (t + D - 1 < nsw) issue(t + D - 1);
+        if (t + D <= nsw)
+            wait_vmcnt<2 * (D - 2)>();
+        else
+            wait_vmcnt<0>();
+        load(t + 1, xb, ab);
+        compute(t, xa, aa);
+        if (t + 2 < nsw) {
+            if (t + D <= nsw)
+                wait_vmcnt<2 * (D - 3)>();
+            else
+                wait_vmcnt<0>();
+            load(t + 2, xa, aa);
+        }
+        compute(t + 1, xb, ab);
+    }
+    if (t < nsw) compute(t, xa, aa);
+
+    // Fold: row r's blocks in group order (kernels.c:1141-1150), by lane 4r of wave 0.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int n = row0 + r;
+    if (wave != 0 || c != 0 || n >= N) return;
+    const float *sr = scl + r * G;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const float *br = blk + (m * 16 + r) * G;
+        float a = 0.0f;
+#pragma unroll 8
+        for (int g = 0; g < G; ++g) a = __builtin_fmaf(br[g], sr[g], a);
+        C[(size_t)(m0 + m) * N + n] = f32_to_bf16(a);
+    }
+}
+
+template <int FMT, int MT, int D, int P>
+size_t gq_lds_bytes(int K) {
+    const size_t G = (size_t)K / (FMT == F_W4G128 ? 128 : 32);
+    return (size_t)P * D * kQuadSlotBytes + (size_t)MT * K * 2 + 16 * G * 4 + (size_t)MT * 16 * G * 4;
+}
+
+template <int FMT, int MT, int D, int P>
+int launch_gq_one(int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *C,
+                  int N, int K, int m0) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_gq_kernel<FMT, MT, D, P>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = gq_lds_bytes<FMT, MT, D, P>(K);
+    if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
+    gemv_gq_kernel<FMT, MT, D, P><<<ntiles, 64 * P, lds, st>>>(A, W, S, C, N, K, m0);
+    return ECPU_OK;
+}
+
+template <int FMT, int D, int P>
+int launch_gq_mt(int mt, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S,
+                 uint16_t *C, int N, int K, int m0) {
+    switch (mt) {
+        case 1: return launch_gq_one<FMT, 1, D, P>(ntiles, st, A, W, S, C, N, K, m0);
+        case 2: return launch_gq_one<FMT, 2, D, P>(ntiles, st, A, W, S, C, N, K, m0);
+        case 3: return launch_gq_one<FMT, 3, D, P>(ntiles, st, A, W, S, C, N, K, m0);
+        default: return launch_gq_one<FMT, 4, D, P>(ntiles, st, A, W, S, C, N, K, m0);
+    }
+}
+
+template <int FMT>
+int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W,
+                  const float *S, uint16_t *C, int N, int K, int m0) {
+    switch (p) {
+        case 1: return launch_gq_mt<FMT, 16, 1>(mt, ntiles, st, A, W, S, C, N, K, m0);
+        case 2: return launch_gq_mt<FMT, 8, 2>(mt, ntiles, st, A, W, S, C, N, K, m0);
+        case 4:
+            return d == 16 ? launch_gq_mt<FMT, 16, 4>(mt, ntiles, st, A, W, S, C, N, K, m0)
+                           : launch_gq_mt<FMT, 8, 4>(mt, ntiles, st, A, W, S, C, N, K, m0);
+        default:   // eight waves: at most two activation rows (registers)
+            return mt == 1 ? launch_gq_one<FMT, 1, 8, 8>(ntiles, st, A, W, S, C, N, K, m0)
+                           : launch_gq_one<FMT, 2, 8, 8>(ntiles, st, A, W, S, C, N, K, m0);
+    }
+}
+
 }  // namespace
 
 // Per-row formats on the stripe path: K a multiple of the stripe (128 int8
 // or 256 int4 weights), 16-byte aligned weights and activations.
 int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn) {
+    // Few 16-row tiles: the chain kernel (several SIMDs per tile).
+    const int qt_all = (int)((N + 15) / 16);
+    int cs = env_int("PILM_HIP_CS", -1);
+    if (cs < 0) cs = qt_all <= 512 ? (fmt == F_W4ROW ? (qt_all <= 256 ? 4 : 2) : 2) : 0;
+    if (fmt != F_W4ROW && cs == 4) cs = 2;
+    if (cs == 2 || cs == 4) {
+        int per = 0;
+        switch (fmt) {
+            case F_W8A32: per = chain_rows_per_launch<F_W8A32, 2>((int)K); break;
+            case F_W8A16: per = chain_rows_per_launch<F_W8A16, 2>((int)K); break;
+            default: per = cs == 4 ? chain_rows_per_launch<F_W4ROW, 4>((int)K) : chain_rows_per_launch<F_W4ROW, 2>((int)K);
+        }
+        if (per > 0) {
+            for (size_t m0 = 0; m0 < M; m0 += per) {
+                const int mt = (int)std::min<size_t>(per, M - m0);
+                int rc;
+                switch (fmt) {
+                    case F_W8A32: rc = launch_chain_mt<F_W8A32, 2>(mt, qt_all, st, A, W, S, C, (int)N, (int)K, (int)m0); break;
+                    case F_W8A16: rc = launch_chain_mt<F_W8A16, 2>(mt, qt_all, st, A, W, S, C, (int)N, (int)K, (int)m0); break;
+                    default:
+                        rc = cs == 4 ? launch_chain_mt<F_W4ROW, 4>(mt, qt_all, st, A, W, S, C, (int)N, (int)K, (int)m0)
+                                     : launch_chain_mt<F_W4ROW, 2>(mt, qt_all, st, A, W, S, C, (int)N, (int)K, (int)m0);
+                }
+                if (rc == ECPU_ERR_DEVICE)
+                    return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+                if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: chain kernel launch does not fit in LDS", fn);
+            }
+            return ECPU_OK;
+        }
+    }
     // Below 65536 rows the 16-row quad kernel (measured faster there); above,
     // the 64-row chain-split kernel, whose scalar activations cost less VALU.
     if (env_int("PILM_HIP_QUAD", N < 65536 ? 1 : 0) != 0) {
@@ -683,6 +1244,40 @@ int run_swiglu_gate_up(size_t I, size_t K, const uint16_t *A, const uint8_t *W, 
     if (depth == 16)
         return launch_quad_one<F_W4ROW, 1, 16, true>(wpb, nt, st, A, W, S, hidden, 1, (int)I, (int)K, 0);
     return launch_quad_one<F_W4ROW, 1, 8, true>(wpb, nt, st, A, W, S, hidden, 1, (int)I, (int)K, 0);
+}
+
+// Group formats (fmt 3 W4A16 g128, 4 g32) on the group-quad kernel: K a
+// multiple of 256, 16-byte aligned A and W.  P waves per 16-row tile divide
+// its stripes: enough to give ~256 waves when the tiles are few.
+// ECPU_ERR_UNSUPPORTED (nothing launched) when LDS cannot hold one row.
+int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+                   hipStream_t st, const char *fn) {
+    const int ntiles = (int)((N + 15) / 16);
+    const int ns = (int)(K / 256);
+    // four waves per tile, eight once each still gets three stripes (measured)
+    int p = ns >= 24 ? 8 : 4, d = 8;
+    const int env_p = env_int("PILM_HIP_GQ_P", 0), env_d = env_int("PILM_HIP_GQ_D", 0);
+    if (env_p == 1 || env_p == 2 || env_p == 4 || env_p == 8) p = env_p;
+    while (p > 1 && ns < 2 * p) p /= 2;   // at least two stripes per wave
+    d = p == 1 ? 16 : (p == 4 && env_d == 16 ? 16 : 8);
+    // activation rows per launch: the largest of 4, 2, 1 that fits LDS
+    auto fits = [&](int mt) {
+        const size_t G = K / (fmt == F_W4G128 ? 128 : 32);
+        return (size_t)p * d * 2048 + (size_t)mt * K * 2 + 16 * G * 4 + (size_t)mt * 16 * G * 4 <= kRowMaxLds;
+    };
+    const int per = (p < 8 && fits(4)) ? 4 : (fits(2) ? 2 : (fits(1) ? 1 : 0));
+    if (per == 0) return ECPU_ERR_UNSUPPORTED;
+    for (size_t m0 = 0; m0 < M; m0 += per) {
+        const int mt = (int)std::min<size_t>(per, M - m0);
+        const int rc = fmt == F_W4G128
+                           ? launch_gq_fmt<F_W4G128>(p, d, mt, ntiles, st, (const uint16_t *)A, W, S,
+                                                     (uint16_t *)C, (int)N, (int)K, (int)m0)
+                           : launch_gq_fmt<F_W4G32>(p, d, mt, ntiles, st, (const uint16_t *)A, W, S,
+                                                    (uint16_t *)C, (int)N, (int)K, (int)m0);
+        if (rc == ECPU_ERR_DEVICE) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+        if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: group-quad launch does not fit in LDS", fn);
+    }
+    return ECPU_OK;
 }
 
 }  // namespace pilm

@@ -60,14 +60,19 @@ def test_golden(case, dev):
     GV.check_output(case, y)
 
 
-SPLITS = [{"PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_NSPLIT": "2"}, {"PILM_HIP_NSPLIT": "3"},
-          {"PILM_HIP_NSPLIT": "16"}, {"PILM_HIP_PL": "2"}, {"PILM_HIP_PL": "3"}, {"PILM_HIP_PL": "8"},
-          {"PILM_HIP_PL": "2", "PILM_HIP_PG": "3"}, {"PILM_HIP_PL": "8", "PILM_HIP_PG": "2"}]
+SPLITS = [{"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "2"},
+          {"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "3"}, {"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "16"},
+          {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "2"}, {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "3"},
+          {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "8"}, {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "2", "PILM_HIP_PG": "3"},
+          {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "8", "PILM_HIP_PG": "2"},
+          {"PILM_HIP_GQ_P": "1"}, {"PILM_HIP_GQ_P": "2"}, {"PILM_HIP_GQ_P": "4"},
+          {"PILM_HIP_GQ_P": "4", "PILM_HIP_GQ_D": "16"}, {"PILM_HIP_GQ_P": "8"}]
 
 
 @pytest.mark.parametrize("env", SPLITS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
 def test_group_split_variants_identical(env, dev, monkeypatch):
-    """Splitting K across waves (in LDS or in global memory) must not change a single bit."""
+    """Splitting K across waves (in LDS or in global memory; 64-row tiles or
+    the 16-row group-quad tiles) must not change a single bit."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for prefix in ("config2_w4g128_M1", "config2_w4g128_M4", "w4g32_cancel", "w4g128_cancel"):
@@ -78,19 +83,23 @@ def test_group_split_variants_identical(env, dev, monkeypatch):
             GV.check_output(case, run_gpu(case["fmt"], *GV.inputs(case), dev))
 
 
-ROW_PATHS = [{"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "4"},
-             {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "8"},
-             {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "16"},
-             {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "32"}, {"PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "16"},
-             {"PILM_HIP_QUAD": "1", "PILM_HIP_RING": "4"}, {"PILM_HIP_QUAD": "1", "PILM_HIP_RING": "16"},
+ROW_PATHS = [{"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "4"},
+             {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "8"},
+             {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64", "PILM_HIP_RING": "16"},
+             {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "32"},
+             {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "16"},
+             {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "4"},
+             {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "16"},
+             {"PILM_HIP_CS": "2"}, {"PILM_HIP_CS": "4"},
              {"PILM_HIP_ROWS": "0"}]
 
 
 @pytest.mark.parametrize("env", ROW_PATHS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
 def test_row_format_paths_identical(env, dev, monkeypatch):
     """Per-row formats: every tile height and ring depth of the chain-split
-    kernels (four waves per tile, or four lanes per row), and the
-    one-wave-per-tile kernel, give the same bits."""
+    kernels (four waves per 64-row tile, four lanes per row, or two / four
+    waves per 16-row tile), and the one-wave-per-tile kernel, give the same
+    bits."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for case in GV.linear_cases(max_elems=1 << 24):
