@@ -52,7 +52,7 @@ KERNEL_SRCS = [ROOT / "pilm_amd" / "csrc" / f for f in ("linear_exact.hip", "lin
 # for the projections (N <= 65536), the 64-row exact kernel for lm_head.
 GEMV_KERNELS = ("gemv_gq_kernel<3, 1,", "gemv_exact_kernel<3, 1>")
 GEMV_KERNEL = "gemv_gq_kernel<3, 1, *> + gemv_exact_kernel<3, 1>"
-TRAFFIC_FILE = ROOT / "profiles" / "gemv_exact_w4a16g128_m1_qwen3_1p7b_decode.traffic.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_w4a16g128_m1_qwen3_1p7b_decode.traffic.txt"
 CALIB_BYTES = 1 << 30                              # copy kernel: reads and writes 1 GiB
 LAYERS = 28
 HIDDEN = 2048
