@@ -22,7 +22,8 @@ Printed JSON line:
                by the launches, against 8 TB/s
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
-  sweep        per-shape GB/s at M = 1, 4, 16 (only with --sweep)
+  sweep        per-shape times with --sweep [sections]: g128 (default),
+               w4row, w8a32, w8a16, gemm, fused, or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -175,43 +176,145 @@ def measured_traffic():
     return rec["traffic"], TRAFFIC_FILE.name
 
 
-def sweep(torch, dev, ms=(1, 4, 16), reps: int = 20) -> dict:
-    """Per-shape GB/s: each shape replicated across enough copies to bust the
-    256 MB Infinity Cache, launched back to back inside one HIP graph."""
+def _fmt_bytes(fmt: str, m: int, n: int, k: int) -> int:
+    """Algorithmic bytes of one call: weights + scales + activations + outputs."""
+    if fmt == "w8a32":
+        return n * k + 4 * n + 4 * m * k + 4 * m * n
+    if fmt == "w8a16":
+        return n * k + 4 * n + 2 * m * k + 2 * m * n
+    if fmt == "w4row":
+        return n * ((k + 1) // 2) + 4 * n + 2 * m * k + 2 * m * n
+    return alg_bytes(m, n, k)   # w4g128
+
+
+def _fmt_weights(torch, dev, fmt: str, n: int, k: int, gen):
+    if fmt in ("w8a32", "w8a16"):
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=gen)
+        return w, torch.rand((n,), device=dev, generator=gen) * 0.019 + 0.001
+    if fmt == "w4row":
+        w = torch.randint(0, 256, (n, (k + 1) // 2), dtype=torch.uint8, device=dev, generator=gen)
+        return w, (torch.rand((n,), device=dev, generator=gen) * 0.019 + 0.001).half().float()
+    return make_weights(torch, dev, n, k, gen)
+
+
+_ENTRY = {"w8a32": "ekernel_linear_w8a32", "w8a16": "ekernel_linear_w8a16_bf16",
+          "w4row": "ekernel_linear_w4a16_bf16", "w4g128": "ekernel_linear_w4a16g128_bf16"}
+
+
+def time_linear(torch, dev, fmt: str, n: int, k: int, ms, reps: int = 20, min_bytes: int = 512 << 20) -> dict:
+    """One shape of one format at each M: enough distinct weight copies to
+    bust the 256 MB Infinity Cache, launched back to back in one HIP graph."""
     from pilm_amd import bindings as abi
     lib = abi._load_lib()
-    fn = lib.ekernel_linear_w4a16g128_bf16
+    fn = getattr(lib, _ENTRY[fmt])
     gen = torch.Generator(device=dev)
-    gen.manual_seed(1)
+    gen.manual_seed(n * 7 + k)
+    copies = max(2, min(1024, -(-min_bytes // _fmt_bytes(fmt, 1, n, k))))
+    ws = [_fmt_weights(torch, dev, fmt, n, k, gen) for _ in range(copies)]
     res = {}
-    shapes = LAYER_SHAPES + [LM_HEAD]
-    for name, n, k in shapes:
-        per = alg_bytes(1, n, k)
-        copies = max(2, min(1024, -(-(512 << 20) // per)))   # >= 512 MB of distinct weights
-        ws = [make_weights(torch, dev, n, k, gen) for _ in range(copies)]
-        for m in ms:
-            x = torch.randn((m, k), device=dev, generator=gen).to(torch.bfloat16)
-            out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-            d = abi.EkernelLinearW8A32Desc(m, n, k)
+    for m in ms:
+        x = torch.randn((m, k), device=dev, generator=gen)
+        x = x if fmt == "w8a32" else x.to(torch.bfloat16)
+        out = torch.empty((m, n), dtype=torch.float32 if fmt == "w8a32" else torch.bfloat16, device=dev)
+        d = abi.EkernelLinearW8A32Desc(m, n, k)
 
-            def run():
-                abi.set_stream(torch.cuda.current_stream().cuda_stream)
-                for (w, s) in ws:
-                    rc = fn(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
-                            ctypes.c_void_p(s.data_ptr()), ctypes.c_void_p(out.data_ptr()), 6)
-                    if rc != 0:
-                        raise RuntimeError(abi.last_error())
-            g = capture(torch, run)
-            sec = time_graph(torch, g, reps, 2)
-            calls = reps * copies
-            res.setdefault(f"M{m}", {})[name] = {
-                "N": n, "K": k, "us": round(sec / calls * 1e6, 2),
-                "GBps": round(alg_bytes(m, n, k) * calls / sec / 1e9, 1),
-                "TFLOPs": round(2.0 * m * n * k * calls / sec / 1e12, 3)}
-            del g
-        del ws
-        torch.cuda.empty_cache()
+        def run():
+            abi.set_stream(torch.cuda.current_stream().cuda_stream)
+            for (w, sc) in ws:
+                rc = fn(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                        ctypes.c_void_p(sc.data_ptr()), ctypes.c_void_p(out.data_ptr()), 6)
+                if rc != 0:
+                    raise RuntimeError(abi.last_error())
+        g = capture(torch, run)
+        sec = time_graph(torch, g, reps, 2)
+        calls = reps * copies
+        res[f"M{m}"] = {"us": round(sec / calls * 1e6, 2),
+                        "GBps": round(_fmt_bytes(fmt, m, n, k) * calls / sec / 1e9, 1),
+                        "TFLOPs": round(2.0 * m * n * k * calls / sec / 1e12, 2)}
+        del g
+    del ws
+    torch.cuda.empty_cache()
     return res
+
+
+# 1.7B projections (per-row W4 uses the fused gate_up shape, as the
+# reference's SwiGLU fusion does), 8B projections (gated q, fused gate_up).
+SHAPES_1P7B_ROW = [("q_proj", 4096, 2048), ("k_proj", 1024, 2048), ("o_proj", 2048, 2048),
+                   ("gate_up_proj", 12288, 2048), ("down_proj", 2048, 6144), LM_HEAD]
+SHAPES_8B = [("q_proj", 8192, 4096), ("k_proj", 1024, 4096), ("o_proj", 4096, 4096),
+             ("gate_up_proj", 24576, 4096), ("down_proj", 4096, 12288), ("lm_head", 151936, 4096)]
+
+
+def sweep(torch, dev, sections) -> dict:
+    """Per-shape times of the measurement configurations:
+      g128   W4A16 g128 at the Qwen3-1.7B shapes, M = 1, 4, 16
+      w4row  per-row W4A16 (bundle v2) at the 1.7B shapes, M = 1, 4, 16
+      w8a32  W8A32: 4096x4096 (the single-GEMV configuration) and the 8B shapes, M = 1
+      w8a16  W8A16 at the 8B shapes, M = 1 and 5 (MTP verify of one sequence)
+      gemm   prefill / verify at the 8B shapes, W8A32 and W4A16 g128,
+             M = 64, 256, 1024, 2048 (matrix cores; TFLOP/s)
+      fused  W4 SwiGLU MLP and W8A16 lm_head argmax vs their unfused calls."""
+    res = {}
+    if "g128" in sections:
+        res["g128_1p7b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4g128", n, k, (1, 4, 16))}
+                            for name, n, k in LAYER_SHAPES + [LM_HEAD]}
+    if "w4row" in sections:
+        res["w4row_1p7b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4row", n, k, (1, 4, 16))}
+                             for name, n, k in SHAPES_1P7B_ROW}
+    if "w8a32" in sections:
+        res["w8a32"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w8a32", n, k, (1,))}
+                        for name, n, k in [("single_4096x4096", 4096, 4096)] + SHAPES_8B}
+    if "w8a16" in sections:
+        res["w8a16_8b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w8a16", n, k, (1, 5))}
+                           for name, n, k in SHAPES_8B}
+    if "gemm" in sections:
+        gm = (64, 256, 1024, 2048)
+        res["gemm_8b"] = {f"{fmt}_{name}": {"N": n, "K": k, **time_linear(torch, dev, fmt, n, k, gm, reps=5,
+                                                                         min_bytes=256 << 20)}
+                          for fmt in ("w8a32", "w4g128") for name, n, k in SHAPES_8B if name != "lm_head"}
+    if "fused" in sections:
+        res["fused"] = sweep_fused(torch, dev)
+    return res
+
+
+def sweep_fused(torch, dev, reps: int = 20) -> dict:
+    """The W4 SwiGLU MLP of one token (Qwen3-1.7B and 8B shapes) fused
+    (ekernel_swiglu_w4a16_bf16) vs gate_up GEMV + SwiGLU + down GEMV, and the
+    W8A16 lm_head with the argmax epilogue (device outputs) vs the GEMV alone."""
+    from pilm_amd import ckernel as ck
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    out = {}
+
+    def timed(fn):
+        g = capture(torch, lambda: [fn() for _ in range(reps)])
+        sec = time_graph(torch, g, 5, 1)
+        del g
+        return round(sec / (5 * reps) * 1e6, 2)
+    for name, h, i in (("qwen3_1p7b", 2048, 6144), ("qwen3_8b", 4096, 12288)):
+        x = torch.randn((1, h), device=dev, generator=gen).to(torch.bfloat16)
+        gu, gs = _fmt_weights(torch, dev, "w4row", 2 * i, h, gen)
+        dw, ds = _fmt_weights(torch, dev, "w4row", h, i, gen)
+
+        def unfused():
+            y = ck.linear_w4a16_bf16(x, gu, gs)
+            return ck.linear_w4a16_bf16(ck.swiglu_bf16(y[:, :i], y[:, i:]), dw, ds)
+        fused_us = timed(lambda: ck.swiglu_w4a16_bf16(x, gu, gs, dw, ds, i))
+        wbytes = 2 * i * (h // 2) + h * (i // 2) + 8 * i + 4 * h
+        out[f"swiglu_w4_{name}"] = {"H": h, "I": i, "fused_us": fused_us, "unfused_us": timed(unfused),
+                                    "fused_GBps": round(wbytes / fused_us / 1e3, 1)}
+        del gu, gs, dw, ds
+    for name, k in (("qwen3_1p7b", 2048), ("qwen3_8b", 4096)):
+        n = 151936
+        x = torch.randn((1, k), device=dev, generator=gen).to(torch.bfloat16)
+        w, sc = _fmt_weights(torch, dev, "w8a16", n, k, gen)
+        gemv_us = timed(lambda: ck.linear_w8a16_bf16(x, w, sc))
+        arg_us = timed(lambda: ck.linear_w8a16_bf16_argmax_device(x, w, sc))
+        out[f"lm_head_argmax_w8a16_{name}"] = {"N": n, "K": k, "gemv_us": gemv_us, "gemv_argmax_us": arg_us,
+                                               "GBps": round((n * k + 4 * n) / arg_us / 1e3, 1)}
+        del w, sc
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(budget_s: float = 12.0) -> dict | None:
@@ -349,7 +452,8 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--sweep", action="store_true", help="add the per-shape M=1,4,16 sweep")
+    ap.add_argument("--sweep", nargs="?", const="g128", default=None,
+                    help="add per-shape sweeps: comma list of g128,w4row,w8a32,w8a16,gemm,fused or 'all'")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-pass", action="store_true")
@@ -427,10 +531,12 @@ def main(argv=None) -> int:
         "roofline": roof,
     }
     if args.sweep:
-        print("[bench] shape sweep M=1,4,16", flush=True)
+        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused") if args.sweep == "all" \
+            else tuple(args.sweep.split(","))
+        print(f"[bench] sweeps: {', '.join(sections)}", flush=True)
         del calls, xs, run
         torch.cuda.empty_cache()
-        out["sweep"] = sweep(torch, dev)
+        out["sweep"] = sweep(torch, dev, sections)
     if not args.no_cpu:
         print("[bench] cpu baseline", flush=True)
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -1254,8 +1254,9 @@ int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const u
                    hipStream_t st, const char *fn) {
     const int ntiles = (int)((N + 15) / 16);
     const int ns = (int)(K / 256);
-    // four waves per tile, eight once each still gets three stripes (measured)
-    int p = ns >= 24 ? 8 : 4, d = 8;
+    // four waves per tile; eight once each still gets three stripes and at
+    // most two activation rows go through (eight-wave kernels hold two)
+    int p = (ns >= 24 && M <= 2) ? 8 : 4, d = 8;
     const int env_p = env_int("PILM_HIP_GQ_P", 0), env_d = env_int("PILM_HIP_GQ_D", 0);
     if (env_p == 1 || env_p == 2 || env_p == 4 || env_p == 8) p = env_p;
     while (p > 1 && ns < 2 * p) p /= 2;   // at least two stripes per wave
