@@ -17,10 +17,14 @@
  *     the device vtable's synchronize() makes results visible to the host.
  *   - The `isa` argument is accepted and ignored, as in the reference.
  *
- * Numerics: the linear kernels reproduce the reference CPU kernels' summation
- * order exactly (8 fp32 FMA lanes for int8 weights, 2x8 lanes per 16-element
- * chunk for int4, fresh per-group dots folded with one FMA per group), so
- * their outputs are bit-identical to the reference for every shape.
+ * Numerics: for M < 64 activation rows the linear kernels reproduce the
+ * reference CPU kernels' summation order exactly (8 fp32 FMA lanes for int8
+ * weights, 2x8 lanes per 16-element chunk for int4, fresh per-group dots
+ * folded with one FMA per group), so their outputs are bit-identical to the
+ * reference for every shape; so are the fused SwiGLU and argmax entries.
+ * For M >= 64 (environment PILM_HIP_MFMA_MIN_M, default 64; 0 disables) the
+ * linears run on the matrix cores with fp16 operands and fp32 accumulation:
+ * outputs within 1e-2 of the reference per output row.
  */
 #ifndef PILM_ECPU_HIP_H
 #define PILM_ECPU_HIP_H
