@@ -685,9 +685,10 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         const int rc = run_rows(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK) return rc;
     } else {
-        // group formats below 65536 rows: 16-row tiles, K divided among waves
+        // group formats up to 8192 rows: 16-row tiles, K divided among waves
+        // (beyond that the 64-row tiles' cheaper decode wins, measured)
         int rc = ECPU_ERR_UNSUPPORTED;
-        if (group && env_int("PILM_HIP_GQ", N <= 65536 ? 1 : 0) != 0)
+        if (group && env_int("PILM_HIP_GQ", N <= 8192 ? 1 : 0) != 0)
             rc = run_group_quad(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK && rc != ECPU_ERR_UNSUPPORTED) return rc;
         if (rc == ECPU_ERR_UNSUPPORTED) {

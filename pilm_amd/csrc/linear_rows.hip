@@ -1174,9 +1174,10 @@ int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
             return ECPU_OK;
         }
     }
-    // Below 65536 rows the 16-row quad kernel (measured faster there); above,
-    // the 64-row chain-split kernel, whose scalar activations cost less VALU.
-    if (env_int("PILM_HIP_QUAD", N < 65536 ? 1 : 0) != 0) {
+    // Below 65536 rows (16384 for fp32 activations) the 16-row quad kernel
+    // (measured faster there); above, the 64-row chain-split kernel, whose
+    // scalar activations cost less VALU (W8A32 24576x4096: 27.0 vs 40.9 us).
+    if (env_int("PILM_HIP_QUAD", N < (fmt == F_W8A32 ? 16384u : 65536u) ? 1 : 0) != 0) {
         // 16-row tiles; one wave per workgroup while there are few tiles (more
         // CUs), four beyond (fewer copies of the activations).
         const int qt = (int)((N + 15) / 16);
@@ -1254,12 +1255,14 @@ int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const u
                    hipStream_t st, const char *fn) {
     const int ntiles = (int)((N + 15) / 16);
     const int ns = (int)(K / 256);
-    // four waves per tile; eight once each still gets three stripes and at
-    // most two activation rows go through (eight-wave kernels hold two)
-    int p = (ns >= 24 && M <= 2) ? 8 : 4, d = 8;
+    // Four waves per tile; eight (at most two activation rows: the eight-wave
+    // kernels hold two) when a tile gets three stripes per wave, or when the
+    // tiles fit the CUs in one round (<= 256: one stripe per wave measured
+    // ~0.5 us faster on 1-4 MB matrices).  Every wave gets a stripe.
+    int p = (M <= 2 && (ns >= 24 || ntiles <= 256)) ? 8 : 4, d = 8;
     const int env_p = env_int("PILM_HIP_GQ_P", 0), env_d = env_int("PILM_HIP_GQ_D", 0);
     if (env_p == 1 || env_p == 2 || env_p == 4 || env_p == 8) p = env_p;
-    while (p > 1 && ns < 2 * p) p /= 2;   // at least two stripes per wave
+    while (p > 1 && ns < p) p /= 2;
     d = p == 1 ? 16 : (p == 4 && env_d == 16 ? 16 : 8);
     // activation rows per launch: the largest of 4, 2, 1 that fits LDS
     auto fits = [&](int mt) {
