@@ -23,7 +23,7 @@ Printed JSON line:
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
   sweep        per-shape times with --sweep [sections]: g128 (default),
-               w4row, w8a32, w8a16, gemm, fused, or all
+               w4row, w8a32, w8a16, gemm, fused, load (bundle -> HBM), or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -253,7 +253,8 @@ def sweep(torch, dev, sections) -> dict:
       w8a16  W8A16 at the 8B shapes, M = 1 and 5 (MTP verify of one sequence)
       gemm   prefill / verify at the 8B shapes, W8A32 and W4A16 g128,
              M = 64, 256, 1024, 2048 (matrix cores; TFLOP/s)
-      fused  W4 SwiGLU MLP and W8A16 lm_head argmax vs their unfused calls."""
+      fused  W4 SwiGLU MLP and W8A16 lm_head argmax vs their unfused calls
+      load   a 1.7B W4 bundle uploaded to HBM (GB/s)."""
     res = {}
     if "g128" in sections:
         res["g128_1p7b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4g128", n, k, (1, 4, 16))}
@@ -274,7 +275,51 @@ def sweep(torch, dev, sections) -> dict:
                           for fmt in ("w8a32", "w4g128") for name, n, k in SHAPES_8B if name != "lm_head"}
     if "fused" in sections:
         res["fused"] = sweep_fused(torch, dev)
+    if "load" in sections:
+        res["load"] = sweep_load(torch, dev)
     return res
+
+
+def sweep_load(torch, dev) -> dict:
+    """Bundle upload: a synthetic Qwen3-1.7B W4A16 per-row bundle (28 layers x
+    7 linears + lm_head, export_pilm_quant_bundle_v2 layout) written to a
+    temporary directory, then loaded into one HBM arena by pilm_amd.weights
+    (file -> pinned staging -> HBM).  The files were just written, so they
+    are read from the page cache: the rate is host memory -> HBM, not disk."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from pilm_amd import weights as Wt
+    rng = np.random.default_rng(5)
+    lin = {}
+    for layer in range(LAYERS):
+        for name, n, k in LAYER_SHAPES:
+            lin[f"model.layers.{layer}.{name}.weight"] = (
+                torch.from_numpy(rng.integers(0, 256, (n, (k + 1) // 2), dtype=np.uint8)),
+                torch.from_numpy((rng.random(n, dtype=np.float32) * 0.019 + 0.001)), k)
+    lin["lm_head.weight"] = (torch.from_numpy(rng.integers(0, 256, (LM_HEAD[1], LM_HEAD[2] // 2), dtype=np.uint8)),
+                             torch.from_numpy(rng.random(LM_HEAD[1], dtype=np.float32)), LM_HEAD[2])
+    tmp = tempfile.mkdtemp(prefix="pilm_bundle_")
+    try:
+        t0 = time.perf_counter()
+        Wt.write_bundle(tmp, "w4a16", lin)
+        write_s = time.perf_counter() - t0
+        runs = []
+        for _ in range(2):
+            b = Wt.QuantBundle(tmp, dev)
+            torch.cuda.synchronize()
+            runs.append(b.stats)
+            del b
+            torch.cuda.empty_cache()
+        best = max(runs, key=lambda r: r["GBps"])
+        return {"linears": best["linears"], "bytes": best["bytes"], "seconds": round(best["seconds"], 3),
+                "GBps": round(best["GBps"], 2), "runs_GBps": [round(r["GBps"], 2) for r in runs],
+                "write_seconds": round(write_s, 2),
+                "note": "page-cache resident files -> pinned staging -> HBM (PCIe); not part of value"}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
 
 
 def sweep_fused(torch, dev, reps: int = 20) -> dict:
@@ -453,7 +498,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sweep", nargs="?", const="g128", default=None,
-                    help="add per-shape sweeps: comma list of g128,w4row,w8a32,w8a16,gemm,fused or 'all'")
+                    help="add per-shape sweeps: comma list of g128,w4row,w8a32,w8a16,gemm,fused,load or 'all'")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-pass", action="store_true")
@@ -531,7 +576,7 @@ def main(argv=None) -> int:
         "roofline": roof,
     }
     if args.sweep:
-        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused") if args.sweep == "all" \
+        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "load") if args.sweep == "all" \
             else tuple(args.sweep.split(","))
         print(f"[bench] sweeps: {', '.join(sections)}", flush=True)
         del calls, xs, run

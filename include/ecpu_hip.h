@@ -212,7 +212,41 @@ int ekernel_swiglu_w4a16_bf16(const ekernel_w4a16_swiglu_desc_t *desc, const uin
                               const uint8_t *down_W, const float *down_scales, uint16_t *C,
                               ekernel_isa_t isa);
 
+/* ---- eram.h:12-41: weight residency ------------------------------------ */
+typedef struct eram_buffer eram_buffer_t;
+
+typedef enum {
+    ERAM_FLAG_NONE = 0,
+    ERAM_FLAG_MMAP = 1 << 0,
+    ERAM_FLAG_LOCK = 1 << 1,
+    ERAM_FLAG_HUGE_PAGES = 1 << 2,
+    ERAM_FLAG_NUMA_LOCAL = 1 << 3,
+} eram_flags_t;
+
+/* Allocate through the active device (HBM, 256-byte aligned, with EDEV_HIP
+ * active); NULL on failure.                                      eram.h:34-37 */
+eram_buffer_t *eram_buffer_alloc(size_t bytes, eram_flags_t flags);
+void eram_buffer_free(eram_buffer_t *buf);
+void *eram_buffer_data(eram_buffer_t *buf);
+size_t eram_buffer_size(eram_buffer_t *buf);
+
+/* Map a file read-only into host memory (the reference maps on Windows only
+ * and returns NULL elsewhere; this maps on Linux).               eram.h:39-41 */
+eram_buffer_t *eram_mmap(const char *path, eram_flags_t flags);
+int eram_munmap(eram_buffer_t *buf);
+int eram_advise_random(eram_buffer_t *buf);
+
 /* ---- additions (no counterpart in the reference) ----------------------- */
+
+/* Upload n byte ranges of a file into device memory: range i is bytes
+ * [file_offsets[i], file_offsets[i] + bytes[i]) and lands at dst[i] (device
+ * pointers, checked like kernel arguments).  The file is read in 16 MB chunks
+ * into two pinned staging buffers used in turn, each copied to HBM on the
+ * library's copy stream while the next is read; returns after the last copy
+ * has completed.  For the quantized-weight bundle and cache loaders: one
+ * upload per tensor, no per-call copies afterwards. */
+int eram_hip_load_file(const char *path, size_t n, const size_t *file_offsets, const size_t *bytes,
+                       void *const *dst);
 
 /* Choose the HIP stream the ekernel_* entry points enqueue on (NULL = the
  * null stream).  Callers that run on another stream (e.g. PyTorch's current

@@ -183,6 +183,22 @@ def _configure(lib):
         lib.ecpu_hip_profile_end.restype = ctypes.c_int
         lib.ecpu_hip_profile_read.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
         lib.ecpu_hip_profile_read.restype = ctypes.c_int
+    if hasattr(lib, "eram_hip_load_file"):
+        lib.eram_hip_load_file.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t),
+                                           ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_void_p)]
+        lib.eram_hip_load_file.restype = ctypes.c_int
+        lib.eram_buffer_alloc.argtypes = [ctypes.c_size_t, ctypes.c_int]
+        lib.eram_buffer_alloc.restype = ctypes.c_void_p
+        lib.eram_buffer_free.argtypes = [ctypes.c_void_p]
+        lib.eram_buffer_free.restype = None
+        lib.eram_buffer_data.argtypes = [ctypes.c_void_p]
+        lib.eram_buffer_data.restype = ctypes.c_void_p
+        lib.eram_buffer_size.argtypes = [ctypes.c_void_p]
+        lib.eram_buffer_size.restype = ctypes.c_size_t
+        lib.eram_mmap.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        lib.eram_mmap.restype = ctypes.c_void_p
+        lib.eram_munmap.argtypes = [ctypes.c_void_p]
+        lib.eram_munmap.restype = ctypes.c_int
     if hasattr(lib, "ecpu_hip_set_stream"):
         lib.ecpu_hip_set_stream.argtypes = [ctypes.c_void_p]
         lib.ecpu_hip_set_stream.restype = ctypes.c_int
@@ -388,3 +404,14 @@ def swiglu_w4a16_bf16_ptr(x_ptr: int, gate_up_w_ptr: int, gate_up_scales_ptr: in
         ctypes.byref(desc), ctypes.c_void_p(x_ptr), ctypes.c_void_p(gate_up_w_ptr),
         ctypes.c_void_p(gate_up_scales_ptr), ctypes.c_void_p(down_w_ptr), ctypes.c_void_p(down_scales_ptr),
         ctypes.c_void_p(c_ptr), int(isa))
+
+
+def eram_load_file(path: str, ranges) -> int:
+    """Upload byte ranges of a file into device memory: ranges is a list of
+    (file_offset, nbytes, device_ptr).  Returns the C rc; waits for the copies."""
+    lib = _load_lib()
+    n = len(ranges)
+    offs = (ctypes.c_size_t * max(n, 1))(*[r[0] for r in ranges])
+    sizes = (ctypes.c_size_t * max(n, 1))(*[r[1] for r in ranges])
+    dsts = (ctypes.c_void_p * max(n, 1))(*[ctypes.c_void_p(r[2]) for r in ranges])
+    return lib.eram_hip_load_file(str(path).encode(), n, offs, sizes, dsts)
