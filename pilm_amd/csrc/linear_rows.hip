@@ -643,14 +643,18 @@ struct ChainFmt {
     }
     // Position of activation k in the chain-major layout: stripe s, chain,
     // then the chain's 16 values of the stripe in the lane's word order
-    // t = 2j + qq (chunk j, dword q = parity + 2qq).
+    // t = 2j + qq (chunk j, dword q = parity + 2qq).  Blocks are kBlock = 20
+    // floats apart (16 used): the four chain groups of a wave then read
+    // different LDS banks (a 16-float pitch put two of them on the same banks).
+    static constexpr int kBlock = 20;
+    static __device__ __forceinline__ int row_floats(int K) { return K / 16 * kBlock; }
     static __device__ __forceinline__ int perm(int k) {
         if constexpr (w8) {
             const int s = k >> 7, j = (k >> 4) & 7, q = (k >> 2) & 3, b = k & 3;
-            return ((s * 8 + 4 * (q & 1) + b) << 4) + 2 * j + (q >> 1);
+            return (s * 8 + 4 * (q & 1) + b) * kBlock + 2 * j + (q >> 1);
         } else {
             const int s = k >> 8, j = (k >> 5) & 7, q = (k >> 3) & 3, p = k & 7;
-            return ((s * 16 + 8 * (q & 1) + p) << 4) + 2 * j + (q >> 1);
+            return (s * 16 + 8 * (q & 1) + p) * kBlock + 2 * j + (q >> 1);
         }
     }
 };
@@ -672,7 +676,8 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const void *__restrict_
     unsigned char *ring = lds;
     constexpr int kEbytes = FMT == F_W8A32 ? 4 : 2;   // bytes per activation
     float *act = (float *)(lds + (size_t)D * kQuadSlotBytes);
-    float *red = act + (size_t)MT * K;
+    const int arow = F::row_floats(K);   // floats per activation row in LDS
+    float *red = act + (size_t)MT * arow;
 
     // Stripe DMA: instruction i (issued by wave i, i < 2) fetches rows
     // 8i + lane/8 of the tile, chunk (lane & 7) ^ ((row >> 1) & 7).
@@ -702,7 +707,7 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const void *__restrict_
 #pragma unroll 1
         for (int m = 0; m < MT; ++m) {
             const u32x4 *asrc = (const u32x4 *)((const unsigned char *)A_ + (size_t)(m0 + m) * K * kEbytes);
-            float *dst = act + (size_t)m * K;
+            float *dst = act + (size_t)m * arow;
 #pragma unroll 1
             for (int v0 = 0; v0 < nvec; v0 += 4 * nthr) {
                 u32x4 buf[4];
@@ -761,7 +766,7 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const void *__restrict_
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int i = 0; i < F::slots; ++i) {
-                const f32x4 *ap = (const f32x4 *)(act + (size_t)m * K + ((s * F::nchain + chn[i]) << 4));
+                const f32x4 *ap = (const f32x4 *)(act + (size_t)m * arow + (s * F::nchain + chn[i]) * F::kBlock);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) av[b][m][i][v] = ap[v];
             }
@@ -847,8 +852,9 @@ __global__ __launch_bounds__(256) void gemv_chain_kernel(const void *__restrict_
 
 template <int FMT, int MT, int D, int CS>
 size_t chain_lds_bytes(int K) {
-    // ring, fp32 activations, chain sums
-    return (size_t)D * kQuadSlotBytes + (size_t)MT * K * 4 + (size_t)MT * ChainFmt<FMT, CS>::gslots * 64 * 4;
+    // ring, fp32 activations (20-float chain blocks), chain sums
+    return (size_t)D * kQuadSlotBytes + (size_t)MT * (K / 16) * ChainFmt<FMT, CS>::kBlock * 4 +
+           (size_t)MT * ChainFmt<FMT, CS>::gslots * 64 * 4;
 }
 
 template <int FMT, int MT, int D, int CS>
