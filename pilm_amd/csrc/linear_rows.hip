@@ -1139,6 +1139,9 @@ int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16
             return d == 16 ? launch_gq_mt<FMT, 16, 4>(mt, ntiles, st, A, W, S, C, N, K, m0)
                            : launch_gq_mt<FMT, 8, 4>(mt, ntiles, st, A, W, S, C, N, K, m0);
         default:   // eight waves: at most two activation rows (registers)
+            if (d == 4)
+                return mt == 1 ? launch_gq_one<FMT, 1, 4, 8>(ntiles, st, A, W, S, C, N, K, m0)
+                               : launch_gq_one<FMT, 2, 4, 8>(ntiles, st, A, W, S, C, N, K, m0);
             return mt == 1 ? launch_gq_one<FMT, 1, 8, 8>(ntiles, st, A, W, S, C, N, K, m0)
                            : launch_gq_one<FMT, 2, 8, 8>(ntiles, st, A, W, S, C, N, K, m0);
     }
@@ -1261,20 +1264,30 @@ int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const u
                    hipStream_t st, const char *fn) {
     const int ntiles = (int)((N + 15) / 16);
     const int ns = (int)(K / 256);
-    // Four waves per tile; eight (at most two activation rows: the eight-wave
-    // kernels hold two) when a tile gets three stripes per wave, or when the
-    // tiles fit the CUs in one round (<= 256: one stripe per wave measured
-    // ~0.5 us faster on 1-4 MB matrices).  Every wave gets a stripe.
-    int p = (M <= 2 && (ns >= 24 || ntiles <= 256)) ? 8 : 4, d = 8;
+    // Eight waves per tile for one or two activation rows (the eight-wave
+    // kernels hold two in registers; measured faster than four at every
+    // Qwen3 shape, e.g. 6144x2048 5.5 vs 6.1 us, 8192x4096 8.9 vs 11.0 us),
+    // four beyond.  Every wave gets a stripe.
+    int p = M <= 2 ? 8 : 4, d = 8;
     const int env_p = env_int("PILM_HIP_GQ_P", 0), env_d = env_int("PILM_HIP_GQ_D", 0);
     if (env_p == 1 || env_p == 2 || env_p == 4 || env_p == 8) p = env_p;
     while (p > 1 && ns < p) p /= 2;
-    d = p == 1 ? 16 : (p == 4 && env_d == 16 ? 16 : 8);
+    // Ring depth: 16 slots for one wave, 8 for four (16 on request), 4 for
+    // eight (the same bytes in flight per CU as four waves of 8, half the LDS,
+    // measured faster: 1.7B decode step 1.070 -> 1.058 ms; 8 on request).
+    d = p == 1 ? 16 : (p == 4 ? (env_d == 16 ? 16 : 8) : (p == 8 ? (env_d == 8 ? 8 : 4) : 8));
     // activation rows per launch: the largest of 4, 2, 1 that fits LDS
     auto fits = [&](int mt) {
         const size_t G = K / (fmt == F_W4G128 ? 128 : 32);
         return (size_t)p * d * 2048 + (size_t)mt * K * 2 + 16 * G * 4 + (size_t)mt * 16 * G * 4 <= kRowMaxLds;
     };
+    // Long rows (K = 12288 with group 32) may leave no room for the rings:
+    // fewer waves rather than the exact kernel.
+    if (p == 8 && !fits(1)) d = 4;
+    while (p > 1 && !fits(1)) {
+        p /= 2;
+        d = p == 1 ? 16 : 8;
+    }
     const int per = (p < 8 && fits(4)) ? 4 : (fits(2) ? 2 : (fits(1) ? 1 : 0));
     if (per == 0) return ECPU_ERR_UNSUPPORTED;
     for (size_t m0 = 0; m0 < M; m0 += per) {

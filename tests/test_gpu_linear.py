@@ -66,7 +66,8 @@ SPLITS = [{"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_GQ": "0", "PI
           {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "8"}, {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "2", "PILM_HIP_PG": "3"},
           {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "8", "PILM_HIP_PG": "2"},
           {"PILM_HIP_GQ_P": "1"}, {"PILM_HIP_GQ_P": "2"}, {"PILM_HIP_GQ_P": "4"},
-          {"PILM_HIP_GQ_P": "4", "PILM_HIP_GQ_D": "16"}, {"PILM_HIP_GQ_P": "8"}]
+          {"PILM_HIP_GQ_P": "4", "PILM_HIP_GQ_D": "16"}, {"PILM_HIP_GQ_P": "8"},
+          {"PILM_HIP_GQ_P": "8", "PILM_HIP_GQ_D": "8"}]
 
 
 @pytest.mark.parametrize("env", SPLITS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
@@ -133,6 +134,20 @@ def test_fresh_shapes_against_oracle(fmt, dev):
         y = run_gpu(fmt, x, w, s, dev)
         ref = gen.run(fmt, x, w, s, "oracle")
         assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n, k)
+
+
+@pytest.mark.parametrize("fmt", ["w4g32", "w4g128"])
+def test_long_rows_group_quad(fmt, dev):
+    """K = 12288 (Qwen3-8B down_proj): 24 KB of activations per tile beside
+    the rings (group 32: 48 KB of scales and block sums as well, so fewer
+    waves per tile); the bits stay the oracle's."""
+    gen = GV._gen()
+    for m, n in ((1, 200), (2, 37), (4, 64)):
+        _say(f"[gpu] long rows {fmt} M={m} N={n} K=12288")
+        x, w, s = gen.make_inputs(fmt, m, n, 12288, 4242 + m)
+        y = run_gpu(fmt, x, w, s, dev)
+        ref = gen.run(fmt, x, w, s, "oracle")
+        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n)
 
 
 def test_power_of_two_scale_full_size(dev):
