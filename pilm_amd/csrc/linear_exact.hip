@@ -396,6 +396,286 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_exact_kernel(const void *
     }
 }
 
+constexpr size_t kMaxLds = 160 * 1024;   // LDS per workgroup on gfx950
+
+// ----------------------------------------------------- small-M group GEMM
+// For a few activation rows (MTP verify, short prefills: M >= 3 below the
+// matrix-core threshold) the group formats are bound by the FMAs, M per
+// weight, not by the weight stream.  Lane = row as above, but the
+// activations reach the lanes through DPP instead of scalar loads: lane i of
+// every 16-lane row of the wave holds element i of the current 16-element
+// chunk of activation row m, and v_fmac_f32_dpp row_newbcast:l hands element l
+// to all 64 lanes inside the FMA itself (one instruction per product, the same
+// single rounding as fmaf).  The chunk's 16 weights are decoded once per lane
+// and used by the wave's MT activation rows, whose bf16 values for the
+// stripe arrive by DMA beside the weights, double-buffered in LDS.  The first
+// chunk of a group multiplies instead of adding to zero: fma(a, w, +0) and
+// a * w differ only in the sign of a zero, and a zero block sum of either
+// sign leaves the group fold fma(block, scale, acc) unchanged (acc starts at
+// +0), so the outputs keep every bit.  The m-groups of MT rows are the grid's
+// second dimension (their weight reads meet in the caches); K is divided
+// among the waves of a workgroup as in the exact kernel, parts 1.. park
+// their block sums in LDS and part 0 folds them in group order.
+
+// Eight products of one chunk half: acc[l] (op)= a of lane B + l of this
+// 16-lane row times w[l].  The s_nop covers the two wait states a DPP source
+// needs after a VALU write.
+#define PILM_BC8(OP, B0, B1, B2, B3, B4, B5, B6, B7, CONS)                                                         \
+    asm volatile("s_nop 1\n\t"                                                                                    \
+                 OP " %0, %8, %9 row_newbcast:" #B0 " row_mask:0xf bank_mask:0xf\n\t"                             \
+                 OP " %1, %8, %10 row_newbcast:" #B1 " row_mask:0xf bank_mask:0xf\n\t"                            \
+                 OP " %2, %8, %11 row_newbcast:" #B2 " row_mask:0xf bank_mask:0xf\n\t"                            \
+                 OP " %3, %8, %12 row_newbcast:" #B3 " row_mask:0xf bank_mask:0xf\n\t"                            \
+                 OP " %4, %8, %13 row_newbcast:" #B4 " row_mask:0xf bank_mask:0xf\n\t"                            \
+                 OP " %5, %8, %14 row_newbcast:" #B5 " row_mask:0xf bank_mask:0xf\n\t"                            \
+                 OP " %6, %8, %15 row_newbcast:" #B6 " row_mask:0xf bank_mask:0xf\n\t"                            \
+                 OP " %7, %8, %16 row_newbcast:" #B7 " row_mask:0xf bank_mask:0xf"                                \
+                 : CONS(acc[0]), CONS(acc[1]), CONS(acc[2]), CONS(acc[3]), CONS(acc[4]), CONS(acc[5]),           \
+                   CONS(acc[6]), CONS(acc[7])                                                                     \
+                 : "v"(a), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]))
+#define PILM_RW(x) "+v"(x)
+#define PILM_WO(x) "=&v"(x)
+
+template <int B, bool FIRST>
+__device__ __forceinline__ void bcast8(float (&acc)[8], float a, const float (&w)[8]) {
+    if constexpr (B == 0 && FIRST)
+        PILM_BC8("v_mul_f32_dpp", 0, 1, 2, 3, 4, 5, 6, 7, PILM_WO);
+    else if constexpr (B == 0)
+        PILM_BC8("v_fmac_f32_dpp", 0, 1, 2, 3, 4, 5, 6, 7, PILM_RW);
+    else if constexpr (FIRST)
+        PILM_BC8("v_mul_f32_dpp", 8, 9, 10, 11, 12, 13, 14, 15, PILM_WO);
+    else
+        PILM_BC8("v_fmac_f32_dpp", 8, 9, 10, 11, 12, 13, 14, 15, PILM_RW);
+}
+#undef PILM_BC8
+#undef PILM_RW
+#undef PILM_WO
+
+__device__ __forceinline__ float w4_block(const float (&lo)[8], const float (&hi)[8]) {
+    float s[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s[l] = lo[l] + hi[l];
+    return hsum8(s);
+}
+
+// bf16 bytes of one stripe of MT activation rows, and of its two buffers.
+template <int MT>
+constexpr int bcast_act_bytes() { return 2 * MT * 256 * 2; }
+
+// LDS: pl stripe slots, pl activation buffers, then (pl > 1) the fold area:
+// float blocks[G - G0][MT][64] and float scales[G - G0][64], G0 = groups of
+// part 0.
+template <int FMT, int MT>
+__global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16_t *__restrict__ A,
+                                                                   const uint8_t *__restrict__ W,
+                                                                   const float *__restrict__ S,
+                                                                   uint16_t *__restrict__ C, int M, int N, int K,
+                                                                   int sps) {
+    using F = StripeFmt<FMT>;
+    constexpr int GPS = F::groups_per_stripe;   // 2 (g128) or 8 (g32)
+    constexpr int CPG = 16 / GPS;               // 16-element chunks per group
+    constexpr int kAct = bcast_act_bytes<MT>();
+    constexpr int kActLoads = MT / 2;           // 1 KB DMA instructions per stripe: two rows each
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int pl = (int)(blockDim.x >> 6);
+    const int row0 = blockIdx.x * 64;
+    const int n = row0 + lane;
+    const int nc = n < N ? n : N - 1;
+    const int mb = (int)blockIdx.y * MT;        // first activation row of this workgroup
+    const int mvalid = min(MT, M - mb);
+    const int nstripes = K / 256;
+    const int G = nstripes * GPS;
+    const int s0 = min(wave * sps, nstripes);
+    const int s1 = min(s0 + sps, nstripes);
+    const int G0 = min(sps * GPS, G);
+    const size_t row_bytes = (size_t)K / 2;
+
+    const uint8_t *src[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        const int q = (lane & 7) ^ ((r >> 1) & 7);
+        src[i] = W + (size_t)min(row0 + r, N - 1) * row_bytes + q * 16;
+    }
+    const int swz = (lane >> 1) & 7;
+    u32x4 *my_slot = (u32x4 *)(lds + wave * kSlotBytes);
+    unsigned char *my_act = lds + pl * kSlotBytes + wave * kAct;   // [2][MT rows][256] bf16
+    float *fold_blocks = (float *)(lds + pl * (kSlotBytes + kAct));
+    float *fold_scales = fold_blocks + (size_t)(G - G0) * MT * 64;
+    const float *srow = S + (size_t)nc * G;
+    // Activation DMA: instruction j, lane t fetches 16 bytes of row 2j + t/32
+    // (rows past M repeat the last row; their results are not stored).
+    const uint16_t *asrc[kActLoads];
+#pragma unroll
+    for (int j = 0; j < kActLoads; ++j)
+        asrc[j] = A + (size_t)(mb + min(2 * j + (lane >> 5), mvalid - 1)) * K + 8 * (lane & 31);
+
+    auto issue = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)st * kStripe),
+                                             (lds_void *)(my_slot + 64 * i), 16, 0, kNT);
+#pragma unroll
+        for (int j = 0; j < kActLoads; ++j)
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + (size_t)st * 256),
+                                             (lds_void *)(my_act + (st & 1) * (kAct / 2) + j * 1024), 16, 0, 0);
+    };
+    if (s0 < s1) issue(s0);
+
+    float lo[MT][8], hi[MT][8], gacc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) gacc[m] = 0.0f;
+    const uint32_t magic = opaque_magic();
+
+#pragma unroll 1
+    for (int s = s0; s < s1; ++s) {
+        float sc[GPS];
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) sc[g] = srow[s * GPS + g];
+        wait_vmcnt<0>();   // stripe s and its activations landed (and the scales arrived)
+        u32x4 mine[kLoads];
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) mine[j] = my_slot[8 * lane + (j ^ swz)];
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the slot may be refilled
+        if (s + 1 < s1) issue(s + 1);
+
+        // lane i of each 16-lane row reads element i of every chunk
+        const uint16_t *abuf = (const uint16_t *)(my_act + (s & 1) * (kAct / 2)) + (lane & 15);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            float a[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) a[m] = __uint_as_float((uint32_t)abuf[m * 256 + 16 * c] << 16);
+            h2 ql[4], qh[4];
+            dequant_w4(mine[c >> 1][2 * (c & 1)], magic, ql);
+            dequant_w4(mine[c >> 1][2 * (c & 1) + 1], magic, qh);
+            float wl[8], wh[8];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                wl[l] = (float)ql[l].x;
+                wl[l + 4] = (float)ql[l].y;
+                wh[l] = (float)qh[l].x;
+                wh[l + 4] = (float)qh[l].y;
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (c % CPG == 0) {
+                    bcast8<0, true>(lo[m], a[m], wl);
+                    bcast8<8, true>(hi[m], a[m], wh);
+                } else {
+                    bcast8<0, false>(lo[m], a[m], wl);
+                    bcast8<8, false>(hi[m], a[m], wh);
+                }
+            }
+            if ((c + 1) % CPG == 0) {
+                const int gl = c / CPG;
+                const int g = GPS * s + gl;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const float block = w4_block(lo[m], hi[m]);
+                    if (wave == 0)
+                        gacc[m] = __builtin_fmaf(block, sc[gl], gacc[m]);
+                    else
+                        fold_blocks[((g - G0) * MT + m) * 64 + lane] = block;
+                }
+                if (wave != 0) fold_scales[(g - G0) * 64 + lane] = sc[gl];
+            }
+        }
+    }
+
+    if (pl > 1) {
+        __syncthreads();
+        if (wave != 0) return;
+        for (int gi = 0; gi < G - G0; ++gi) {
+            const float scg = fold_scales[gi * 64 + lane];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) gacc[m] = __builtin_fmaf(fold_blocks[(gi * MT + m) * 64 + lane], scg, gacc[m]);
+        }
+    }
+    if (n >= N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        if (m < mvalid) C[(size_t)(mb + m) * N + n] = f32_to_bf16(gacc[m]);
+}
+
+static size_t bcast_lds_bytes(int mt, int pl, int sps, int G, int gps) {
+    size_t bytes = (size_t)pl * (kSlotBytes + (size_t)2 * mt * 256 * 2);
+    if (pl > 1) bytes += (size_t)(G - std::min(sps * gps, G)) * 64 * (mt + 1) * sizeof(float);
+    return bytes;
+}
+
+template <int FMT, int MT>
+static int launch_bcast(dim3 grid, dim3 block, size_t lds, hipStream_t st, const uint16_t *A, const uint8_t *W,
+                        const float *S, uint16_t *C, int M, int N, int K, int sps) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_bcast_kernel<FMT, MT>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    gemv_bcast_kernel<FMT, MT><<<grid, block, lds, st>>>(A, W, S, C, M, N, K, sps);
+    return ECPU_OK;
+}
+
+// Small-M path of the group formats: every M rows in one launch (m-groups of
+// MT = 4 or 8 rows on the grid's y dimension), K divided among up to 8 waves
+// per tile (fewer when the parked block sums would not fit LDS).  A wave's
+// work grows with MT, so the eight-row waves are taken only where there are
+// enough of them to fill the SIMDs (>= 1536 waves; measured at M = 16:
+// 6144x2048 16.4 vs 21.0 us, 4096x2048 16.3 vs 11.2 us).  Up to four rows
+// with fewer than 768 waves stay with the group-quad kernel (returns
+// ECPU_ERR_UNSUPPORTED; 4096x2048 M=4: 8.9 vs 10.9 us).
+static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+                     hipStream_t st, const char *fn) {
+    const int nstripes = (int)(K / 256);
+    const int gps = fmt == F_W4G128 ? 2 : 8;
+    const int G = nstripes * gps;
+    const size_t ntiles = (N + 63) / 64;
+    auto plan = [&](int mt, int &pl, int &sps) {
+        pl = std::min(kMaxParts, nstripes);
+        const int env_pl = env_int("PILM_HIP_BCAST_PL", 0);
+        if (env_pl >= 1 && env_pl <= kMaxParts) pl = std::min(env_pl, nstripes);
+        sps = (nstripes + pl - 1) / pl;
+        pl = (nstripes + sps - 1) / sps;   // every part gets a stripe
+        while (pl > 1 && bcast_lds_bytes(mt, pl, sps, G, gps) > kMaxLds) {
+            pl = (pl + 1) / 2;
+            sps = (nstripes + pl - 1) / pl;
+            pl = (nstripes + sps - 1) / sps;
+        }
+    };
+    int pl8, sps8, pl4, sps4;
+    plan(8, pl8, sps8);
+    plan(4, pl4, sps4);
+    const size_t waves8 = ntiles * pl8 * ((M + 7) / 8), waves4 = ntiles * pl4 * ((M + 3) / 4);
+    int mt = (M > 4 && waves8 >= 1536) ? 8 : 4;
+    const int env_mt = env_int("PILM_HIP_BCAST_MT", 0);
+    if (env_mt == 4 || env_mt == 8)
+        mt = env_mt;
+    else if (M <= 4 && waves4 < 768)
+        return ECPU_ERR_UNSUPPORTED;
+    const int pl = mt == 8 ? pl8 : pl4, sps = mt == 8 ? sps8 : sps4;
+    const size_t lds = bcast_lds_bytes(mt, pl, sps, G, gps);
+    if (lds > kMaxLds) return fail(ECPU_ERR_DEVICE, "%s: small-M tile does not fit in LDS", fn);
+    const size_t mgroups = (M + mt - 1) / mt;
+    if (mgroups > 65535) return ECPU_ERR_UNSUPPORTED;
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)mgroups);
+    const dim3 block((unsigned)(64 * pl));
+    const uint16_t *a16 = (const uint16_t *)A;
+    uint16_t *c16 = (uint16_t *)C;
+    int rc;
+    if (fmt == F_W4G128)
+        rc = mt == 4 ? launch_bcast<F_W4G128, 4>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps)
+                     : launch_bcast<F_W4G128, 8>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps);
+    else
+        rc = mt == 4 ? launch_bcast<F_W4G32, 4>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps)
+                     : launch_bcast<F_W4G32, 8>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps);
+    if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the small-M kernel failed", fn);
+    return ECPU_OK;
+}
+
 // ----------------------------------------------------- literal fallback
 __device__ __forceinline__ float nib(const uint8_t *w, size_t k) {
     const uint8_t b = w[k >> 1];
@@ -475,7 +755,6 @@ __global__ __launch_bounds__(256) void gemv_literal_kernel(GemvArgs p, int group
 
 // --------------------------------------------------------------- launch
 
-constexpr size_t kMaxLds = 160 * 1024;   // LDS per workgroup on gfx950
 
 template <int FMT, int MT>
 static int launch_one(dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemvArgs &a, int m0) {
@@ -688,7 +967,9 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         // group formats up to 8192 rows: 16-row tiles, K divided among waves
         // (beyond that the 64-row tiles' cheaper decode wins, measured)
         int rc = ECPU_ERR_UNSUPPORTED;
-        if (group && env_int("PILM_HIP_GQ", N <= 8192 ? 1 : 0) != 0)
+        if (group && M >= 3 && env_int("PILM_HIP_BCAST", 1) != 0)
+            rc = run_bcast(fmt, M, N, K, A, W, S, C, st, fn);
+        if (rc == ECPU_ERR_UNSUPPORTED && group && env_int("PILM_HIP_GQ", N <= 8192 ? 1 : 0) != 0)
             rc = run_group_quad(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK && rc != ECPU_ERR_UNSUPPORTED) return rc;
         if (rc == ECPU_ERR_UNSUPPORTED) {
