@@ -624,7 +624,8 @@ static int launch_bcast(dim3 grid, dim3 block, size_t lds, hipStream_t st, const
 // MT = 4 or 8 rows on the grid's y dimension), K divided among up to 8 waves
 // per tile (fewer when the parked block sums would not fit LDS).  A wave's
 // work grows with MT, so the eight-row waves are taken only where there are
-// enough of them to fill the SIMDs (>= 1536 waves; measured at M = 16:
+// enough of them to fill the SIMDs (>= 1536 waves) and add no padding rows
+// over MT = 4 (measured at M = 16:
 // 6144x2048 16.4 vs 21.0 us, 4096x2048 16.3 vs 11.2 us).  Up to four rows
 // with fewer than 768 waves stay with the group-quad kernel (returns
 // ECPU_ERR_UNSUPPORTED; 4096x2048 M=4: 8.9 vs 10.9 us).
@@ -650,7 +651,8 @@ static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const
     plan(8, pl8, sps8);
     plan(4, pl4, sps4);
     const size_t waves8 = ntiles * pl8 * ((M + 7) / 8), waves4 = ntiles * pl4 * ((M + 3) / 4);
-    int mt = (M > 4 && waves8 >= 1536) ? 8 : 4;
+    const size_t pad8 = (M + 7) / 8 * 8, pad4 = (M + 3) / 4 * 4;   // rows computed, padding included
+    int mt = (pad8 <= pad4 && waves8 >= 1536) ? 8 : 4;
     const int env_mt = env_int("PILM_HIP_BCAST_MT", 0);
     if (env_mt == 4 || env_mt == 8)
         mt = env_mt;

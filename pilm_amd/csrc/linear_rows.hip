@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "gemv_device.h"
 #include "internal.h"
@@ -894,6 +895,305 @@ int chain_rows_per_launch(int K) {
     return 0;
 }
 
+// ------------------------------------------------------------------ row broadcast
+// Per-row formats with a few activation rows (MTP verify M = 1 + drafts,
+// short prefills): each weight feeds M FMAs, so the exact path is bound by
+// FMA issue, and reading every activation per lane from LDS (the chain
+// kernel) or unpacking bf16 pairs per FMA (the quad kernel) costs as much
+// again.  Here the 16-row tile keeps the quad layout's chain groups but
+// orders the lanes by group, lane = 16c + r, so each 16-lane DPP row holds
+// one chain group for 16 rows and every lane of it meets the same activation
+// at each step: lane t of the row holds step t's activation for the stripe,
+// and v_fmac_f32_dpp row_newbcast:t hands it to all sixteen inside the FMA
+// (the single rounding of fmaf).  CS waves per tile divide the chain slots
+// (one chain per lane); each weight is decoded once (bit-field extract +
+// conversion) and used by MT activation rows.  The waves share a ring of D
+// slots, each holding one stripe of the 16 rows' weights and of the MT
+// activation rows (wave 0 issues the DMA, one barrier per stripe); chain sums
+// meet in LDS and one lane per row adds them in the reference's order.  The
+// m-groups of MT rows are the grid's second dimension.
+
+// Step T of eight chains: acc[j] += a[j] of lane T of this 16-lane row times
+// w[j].  The s_nop covers the two wait states a DPP source needs after a VALU
+// write (the compiler does not see hazards inside inline asm).
+template <int T>
+__device__ __forceinline__ void rbc_step8(float (&acc)[8], const float (&a)[8], const float (&w)[8]);
+template <int T>
+__device__ __forceinline__ void rbc_step4(float (&acc)[4], const float (&a)[4], const float (&w)[4]);
+
+#define PILM_RBC_DPP(T) " row_newbcast:" #T " row_mask:0xf bank_mask:0xf\n\t"
+#define PILM_RBC_DEF(T)                                                                                           \
+    template <>                                                                                                   \
+    __device__ __forceinline__ void rbc_step8<T>(float (&acc)[8], const float (&a)[8], const float (&w)[8]) {      \
+        asm volatile("s_nop 1\n\t"                                                                                \
+                     "v_fmac_f32_dpp %0, %8, %16" PILM_RBC_DPP(T) "v_fmac_f32_dpp %1, %9, %17" PILM_RBC_DPP(T)    \
+                     "v_fmac_f32_dpp %2, %10, %18" PILM_RBC_DPP(T) "v_fmac_f32_dpp %3, %11, %19" PILM_RBC_DPP(T)  \
+                     "v_fmac_f32_dpp %4, %12, %20" PILM_RBC_DPP(T) "v_fmac_f32_dpp %5, %13, %21" PILM_RBC_DPP(T)  \
+                     "v_fmac_f32_dpp %6, %14, %22" PILM_RBC_DPP(T) "v_fmac_f32_dpp %7, %15, %23" PILM_RBC_DPP(T)  \
+                     : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),       \
+                       "+v"(acc[6]), "+v"(acc[7])                                                                 \
+                     : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),    \
+                       "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]));   \
+    }                                                                                                             \
+    template <>                                                                                                   \
+    __device__ __forceinline__ void rbc_step4<T>(float (&acc)[4], const float (&a)[4], const float (&w)[4]) {      \
+        asm volatile("s_nop 1\n\t"                                                                                \
+                     "v_fmac_f32_dpp %0, %4, %8" PILM_RBC_DPP(T) "v_fmac_f32_dpp %1, %5, %9" PILM_RBC_DPP(T)      \
+                     "v_fmac_f32_dpp %2, %6, %10" PILM_RBC_DPP(T) "v_fmac_f32_dpp %3, %7, %11" PILM_RBC_DPP(T)    \
+                     : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])                                     \
+                     : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));   \
+    }
+PILM_RBC_DEF(0) PILM_RBC_DEF(1) PILM_RBC_DEF(2) PILM_RBC_DEF(3) PILM_RBC_DEF(4) PILM_RBC_DEF(5) PILM_RBC_DEF(6)
+PILM_RBC_DEF(7) PILM_RBC_DEF(8) PILM_RBC_DEF(9) PILM_RBC_DEF(10) PILM_RBC_DEF(11) PILM_RBC_DEF(12)
+PILM_RBC_DEF(13) PILM_RBC_DEF(14) PILM_RBC_DEF(15)
+#undef PILM_RBC_DEF
+#undef PILM_RBC_DPP
+
+template <int FMT, int MT, int CS>
+struct RbcFmt {
+    using F = ChainFmt<FMT, CS>;
+    static constexpr int SL = F::slots;                        // chains per lane
+    static constexpr int NF = MT * SL;                         // FMAs per lane and step (4 or 8)
+    static_assert(NF == 4 || NF == 8, "row-broadcast step width");
+    static constexpr int ES = FMT == F_W8A32 ? 4 : 2;          // activation bytes
+    static constexpr int SPE = F::w8 ? 128 : 256;              // row elements per stripe
+    static constexpr int STEP = F::w8 ? 8 : 16;                // elements per step (a chain takes one)
+    static constexpr int RB = SPE * ES;                        // activation bytes of a row per stripe
+    static constexpr int ACT = MT * RB;                        // activation bytes per slot
+    static_assert(ACT % 1024 == 0, "activation DMA granularity");
+    static constexpr int SLOT = kQuadSlotBytes + ACT;          // weights (16 rows x 128 B) + activations
+    static constexpr int PER = 2 + ACT / 1024;                 // DMA instructions per stripe
+};
+
+template <int FMT, int MT, int CS, int D>
+__global__ __launch_bounds__(64 * CS) void gemv_rbc_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W,
+                                                          const float *__restrict__ S, void *__restrict__ C, int M,
+                                                          int N, int K) {
+    using R = RbcFmt<FMT, MT, CS>;
+    using F = typename R::F;
+    constexpr int SL = R::SL;
+    static_assert(R::PER * (D - 2) < 64, "vmcnt range");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15, c = lane >> 4, par = c >> 1, t16 = lane & 15;
+    const int row0 = blockIdx.x * 16;
+    const int mb = (int)blockIdx.y * MT;
+    const int mvalid = min(MT, M - mb);
+    const size_t row_bytes = F::w8 ? (size_t)K : (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    const unsigned char *A = (const unsigned char *)A_;
+
+    // DMA (wave 0): instructions 0, 1 fetch rows 8i + lane/8 of the tile,
+    // chunk (lane & 7) ^ ((row >> 1) & 7); instructions 2.. fetch 1 KB of the
+    // stripe's activation rows each (rows past M repeat the last row).
+    const uint8_t *wsrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rr = 8 * i + (lane >> 3);
+        wsrc[i] = W + (size_t)min(row0 + rr, N - 1) * row_bytes + (((lane & 7) ^ ((rr >> 1) & 7)) << 4);
+    }
+    const unsigned char *asrc[R::PER - 2];
+#pragma unroll
+    for (int j = 0; j < R::PER - 2; ++j) {
+        const int b = j * 1024 + 16 * lane;
+        const int m = b / R::RB;
+        asrc[j] = A + ((size_t)(mb + min(m, mvalid - 1)) * K) * R::ES + (b - m * R::RB);
+    }
+    auto issue = [&](int st) {
+        unsigned char *slot = lds + (st % D) * R::SLOT;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (size_t)st * kStripe),
+                                             (lds_void *)(slot + i * 1024), 16, 0, kNT);
+#pragma unroll
+        for (int j = 0; j < R::PER - 2; ++j)
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + (size_t)st * R::RB),
+                                             (lds_void *)(slot + kQuadSlotBytes + j * 1024), 16, 0, 0);
+    };
+    if (wave == 0) {
+#pragma unroll 1
+        for (int st = 0; st < D - 1 && st < ns; ++st) issue(st);
+    }
+
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = r * kStripe + ((j ^ swz) << 4) + 4 * par;
+    int bits[SL], aoff[SL];
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        bits[i] = F::bit(c, wave * SL + i);
+        aoff[i] = (R::STEP * t16 + F::chain(c, wave * SL + i)) * R::ES;   // lane t16 holds step t16's value
+    }
+    float acc[MT][SL];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < SL; ++i) acc[m][i] = 0.0f;
+
+#pragma unroll 1
+    for (int s = 0; s < ns; ++s) {
+        if (wave == 0) {
+            if (s + D - 2 < ns)
+                wait_vmcnt<R::PER * (D - 2)>();   // stripes s+1 .. s+D-2 may still fly
+            else
+                wait_vmcnt<0>();
+        }
+        // stripe s landed for everyone; every wave is done with slot (s-1) % D
+        asm volatile("s_barrier" ::: "memory");
+        if (wave == 0 && s + D - 1 < ns) issue(s + D - 1);
+        const unsigned char *slot = lds + (s % D) * R::SLOT;
+        uint32_t x[16];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[2 * j] = *(const uint32_t *)(slot + off[j]);
+            x[2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+        float av[R::NF];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < SL; ++i) {
+                const unsigned char *ap = slot + kQuadSlotBytes + m * R::RB + aoff[i];
+                if constexpr (FMT == F_W8A32)
+                    av[m * SL + i] = *(const float *)ap;
+                else
+                    av[m * SL + i] = __uint_as_float((uint32_t)(*(const uint16_t *)ap) << 16);
+            }
+        float fa[R::NF];
+#pragma unroll
+        for (int q = 0; q < R::NF; ++q) fa[q] = acc[q / SL][q % SL];
+        auto step = [&](auto tc) {
+            constexpr int T = decltype(tc)::value;
+            float w[R::NF];
+#pragma unroll
+            for (int i = 0; i < SL; ++i) {
+                const float wi = (float)(int)__builtin_amdgcn_sbfe((int)x[T], bits[i], F::width);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) w[m * SL + i] = wi;
+            }
+            if constexpr (R::NF == 8)
+                rbc_step8<T>(fa, av, w);
+            else
+                rbc_step4<T>(fa, av, w);
+        };
+        step(std::integral_constant<int, 0>{});
+        step(std::integral_constant<int, 1>{});
+        step(std::integral_constant<int, 2>{});
+        step(std::integral_constant<int, 3>{});
+        step(std::integral_constant<int, 4>{});
+        step(std::integral_constant<int, 5>{});
+        step(std::integral_constant<int, 6>{});
+        step(std::integral_constant<int, 7>{});
+        step(std::integral_constant<int, 8>{});
+        step(std::integral_constant<int, 9>{});
+        step(std::integral_constant<int, 10>{});
+        step(std::integral_constant<int, 11>{});
+        step(std::integral_constant<int, 12>{});
+        step(std::integral_constant<int, 13>{});
+        step(std::integral_constant<int, 14>{});
+        step(std::integral_constant<int, 15>{});
+#pragma unroll
+        for (int q = 0; q < R::NF; ++q) acc[q / SL][q % SL] = fa[q];
+    }
+
+    // Chain sums meet in LDS (over the ring, once every wave is done with it):
+    // red[m][gslot][c][r]; lane r < 16 of wave 0 adds row r's chains in the
+    // reference's order: hsum ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) of the 8
+    // lanes (int4: of lo[l] + hi[l]), times the row scale.
+    float *red = (float *)lds;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < SL; ++i) red[((m * F::gslots + wave * SL + i) * 4 + c) * 16 + r] = acc[m][i];
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int n = row0 + lane;
+    if (wave != 0 || lane >= 16 || n >= N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m >= mvalid) break;
+        const float *rm = red + m * F::gslots * 64 + lane;   // [gslot][c] at (g * 4 + c) * 16
+        float l8[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            if constexpr (F::w8) {
+                const int g = l & 1, cc = 2 * (l >> 2) + ((l >> 1) & 1);
+                l8[l] = rm[(g * 4 + cc) * 16];
+            } else {
+                const int g = ((l >> 2) & 1) + 2 * (l & 1), cl = (l >> 1) & 1;
+                l8[l] = rm[(g * 4 + cl) * 16] + rm[(g * 4 + cl + 2) * 16];
+            }
+        }
+        const float y = hsum8(l8) * S[n];
+        const size_t o = (size_t)(mb + m) * N + n;
+        if constexpr (FMT == F_W8A32)
+            ((float *)C)[o] = y;
+        else
+            ((uint16_t *)C)[o] = f32_to_bf16(y);
+    }
+}
+
+template <int FMT, int MT, int CS, int D>
+constexpr size_t rbc_lds_bytes() {
+    using R = RbcFmt<FMT, MT, CS>;
+    const size_t ring = (size_t)D * R::SLOT, red = (size_t)MT * R::F::gslots * 64 * sizeof(float);
+    return ring > red ? ring : red;
+}
+
+template <int FMT, int MT, int CS>
+int launch_rbc_one(int ntiles, int mgroups, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C,
+                   int M, int N, int K) {
+    constexpr int D = 8;
+    constexpr size_t lds = rbc_lds_bytes<FMT, MT, CS, D>();
+    static_assert(lds <= kRowMaxLds, "row-broadcast ring");
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_rbc_kernel<FMT, MT, CS, D>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    gemv_rbc_kernel<FMT, MT, CS, D><<<dim3((unsigned)ntiles, (unsigned)mgroups), 64 * CS, lds, st>>>(A, W, S, C, M, N,
+                                                                                                     K);
+    return ECPU_OK;
+}
+
+// Per-row formats, 3 <= M < 64: one chain per lane (W8 over two waves per
+// tile, W4 over four), MT = 8 activation rows per wave where that computes
+// no more padding rows than MT = 4 and still leaves >= 2048 waves, else 4
+// (measured: W8A16 8192x4096 M=5 23.1 vs 29.0 us, W4 12288x2048 M=16 25.2
+// vs 27.2 us, W4 12288x2048 M=4 10.0 vs 13.5 us).
+int run_rbc(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
+            hipStream_t st, const char *fn) {
+    const int ntiles = (int)((N + 15) / 16);
+    const int cs = fmt == F_W4ROW ? 4 : 2;
+    const size_t pad8 = (M + 7) / 8 * 8, pad4 = (M + 3) / 4 * 4;
+    int mt = pad8 <= pad4 && (size_t)ntiles * cs * (pad8 / 8) >= 2048 ? 8 : 4;
+    const int env_mt = env_int("PILM_HIP_RBC_MT", 0);
+    if (env_mt == 4 || env_mt == 8) mt = env_mt;
+    const size_t mgroups = (M + mt - 1) / mt;
+    if (mgroups > 65535) return ECPU_ERR_UNSUPPORTED;
+    const int mg = (int)mgroups;
+    int rc;
+    switch (fmt) {
+        case F_W8A32:
+            rc = mt == 8 ? launch_rbc_one<F_W8A32, 8, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                         : launch_rbc_one<F_W8A32, 4, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
+            break;
+        case F_W8A16:
+            rc = mt == 8 ? launch_rbc_one<F_W8A16, 8, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                         : launch_rbc_one<F_W8A16, 4, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
+            break;
+        default:
+            rc = mt == 8 ? launch_rbc_one<F_W4ROW, 8, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                         : launch_rbc_one<F_W4ROW, 4, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
+    }
+    if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the small-M kernel failed", fn);
+    return ECPU_OK;
+}
+
 // ------------------------------------------------------------------ group quad
 // Group formats (W4A16 g128 / g32) with the quad layout: 16-row tiles, lane
 // 4r + c serves row r with the quad kernel's int4 chains (the packing is the
@@ -1153,6 +1453,8 @@ int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16
 // or 256 int4 weights), 16-byte aligned weights and activations.
 int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn) {
+    // A few activation rows: the row-broadcast kernel, every M in one launch.
+    if (M >= 3 && env_int("PILM_HIP_RBC", 1) != 0) return run_rbc(fmt, M, N, K, A, W, S, C, st, fn);
     // Few 16-row tiles: the chain kernel (several SIMDs per tile).
     const int qt_all = (int)((N + 15) / 16);
     int cs = env_int("PILM_HIP_CS", -1);

@@ -96,15 +96,15 @@ ROW_PATHS = [{"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64"
              {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "4"},
              {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "16"},
              {"PILM_HIP_CS": "2"}, {"PILM_HIP_CS": "4"},
-             {"PILM_HIP_ROWS": "0"}]
+             {"PILM_HIP_ROWS": "0"}, {"PILM_HIP_RBC": "0"}, {"PILM_HIP_RBC_MT": "4"}]
 
 
 @pytest.mark.parametrize("env", ROW_PATHS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
 def test_row_format_paths_identical(env, dev, monkeypatch):
     """Per-row formats: every tile height and ring depth of the chain-split
     kernels (four waves per 64-row tile, four lanes per row, or two / four
-    waves per 16-row tile), and the one-wave-per-tile kernel, give the same
-    bits."""
+    waves per 16-row tile), the one-wave-per-tile kernel and the small-M
+    row-broadcast kernel (4 or 8 rows per wave, or off) give the same bits."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for case in GV.linear_cases(max_elems=1 << 24):
@@ -152,6 +152,19 @@ def test_long_rows_group_quad(fmt, dev):
         y = run_gpu(fmt, x, w, s, dev)
         ref = gen.run(fmt, x, w, s, "oracle")
         assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n)
+
+
+@pytest.mark.parametrize("fmt", ["w8a32", "w8a16", "w4"])
+def test_small_m_row_formats(fmt, dev):
+    """Per-row formats at 3 <= M < 64 (MTP verify, short prefill): the
+    row-broadcast kernel against the oracle, ragged N and partial m-groups."""
+    gen = GV._gen()
+    for m, n, k in ((3, 50, 1024), (5, 300, 2048), (8, 17, 256), (9, 64, 4096), (16, 130, 512), (33, 40, 768)):
+        _say(f"[gpu] small-M {fmt} M={m} N={n} K={k}")
+        x, w, s = gen.make_inputs(fmt, m, n, k, 9100 + m)
+        y = run_gpu(fmt, x, w, s, dev)
+        ref = gen.run(fmt, x, w, s, "oracle")
+        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n, k)
 
 
 def test_power_of_two_scale_full_size(dev):
