@@ -895,6 +895,195 @@ int chain_rows_per_launch(int K) {
     return 0;
 }
 
+// ------------------------------------------------------------------ byte waves
+// W8A32 / W8A16 decode (M = 1), a few thousand rows: the chain kernel pays
+// three VALU instructions per weight because a lane's byte position inside
+// a dword differs from lane to lane (bit-field extract + conversion + FMA).
+// Here a tile of ROWS = 16 or 32 rows has four waves and wave b owns byte b
+// of every dword: the eight chains k = 8T + 4p + b of a row are (parity p,
+// byte b), so each lane (row r = 16h + t, parity p: DPP row j = p + 2h,
+// t = lane & 15; with 16-row tiles DPP rows 2, 3 repeat rows 0..15) decodes
+// with one v_cvt_f32_i32 whose SDWA operand selects byte b (a compile-time
+// byte: one code path per wave), and the activation of step t of the
+// stripe, a[128s + 8t + 4p + b], sits in lane t of the DPP row and reaches
+// all sixteen rows through row_newbcast inside the FMA.  Two VALU
+// instructions per weight, one chain per lane.  16-row tiles spread a few
+// thousand rows over every CU (a CU streams only ~25-30 GB/s).  The four
+// waves share a ring of D slots (the tile's rows x 128 B of a stripe plus
+// its activations), in rounds of four stripes per barrier; the chain
+// sums meet in LDS and one lane per row adds them in the reference's order.
+
+// acc = fma(a of lane t of this 16-lane row, w[t], acc) for t = 0..15 in
+// order: one chain's sixteen steps of a stripe.  The s_nop covers the two
+// wait states a DPP source needs after a VALU write.
+__device__ __forceinline__ void w8b_chain16(float &acc, float a, const float (&w)[16]) {
+#define PILM_W8B(T, OP) "v_fmac_f32_dpp %0, %1, %" #OP " row_newbcast:" #T " row_mask:0xf bank_mask:0xf\n\t"
+    asm volatile("s_nop 1\n\t" PILM_W8B(0, 2) PILM_W8B(1, 3) PILM_W8B(2, 4) PILM_W8B(3, 5) PILM_W8B(4, 6)
+                     PILM_W8B(5, 7) PILM_W8B(6, 8) PILM_W8B(7, 9) PILM_W8B(8, 10) PILM_W8B(9, 11) PILM_W8B(10, 12)
+                         PILM_W8B(11, 13) PILM_W8B(12, 14) PILM_W8B(13, 15) PILM_W8B(14, 16) PILM_W8B(15, 17)
+                 : "+v"(acc)
+                 : "v"(a), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]),
+                   "v"(w[8]), "v"(w[9]), "v"(w[10]), "v"(w[11]), "v"(w[12]), "v"(w[13]), "v"(w[14]), "v"(w[15]));
+#undef PILM_W8B
+}
+
+template <int FMT, int ROWS>
+struct W8bFmt {
+    static constexpr int ES = FMT == F_W8A32 ? 4 : 2;   // activation bytes
+    static constexpr int RB = 128 * ES;                  // activation bytes per stripe
+    static constexpr int WB = ROWS * kStripe;            // weight bytes per stripe
+    static constexpr int SLOT = WB + RB;                 // the rows' stripe, then the activations
+};
+
+template <int FMT, int D, int ROWS>
+__global__ __launch_bounds__(256) void gemv_w8b_kernel(const void *__restrict__ A_, const uint8_t *__restrict__ W,
+                                                      const float *__restrict__ S, void *__restrict__ C, int N,
+                                                      int K) {
+    using B8 = W8bFmt<FMT, ROWS>;
+    static_assert(ROWS == 16 || ROWS == 32, "tile height");
+    constexpr int R = 4;   // stripes per round
+    static_assert(D % R == 0 && D >= 2 * R, "ring depth");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int t = lane & 15, j = lane >> 4, p = j & 1, r = (ROWS == 32 ? 16 * (j >> 1) : 0) + t;
+    const int row0 = blockIdx.x * ROWS;
+    const int ns = K / kStripe;
+    const unsigned char *A = (const unsigned char *)A_;
+
+    // DMA: wave w < ROWS/8 fetches rows 8w + lane/8 of the tile, chunk
+    // (lane & 7) ^ ((row >> 1) & 7); the stripe's activations are fetched by
+    // the first RB/16 lanes of wave 0.
+    constexpr int kIssuers = ROWS / 8;
+    const int dr = 8 * (wave % kIssuers) + (lane >> 3);
+    const uint8_t *wsrc = W + (size_t)min(row0 + dr, N - 1) * K + (((lane & 7) ^ ((dr >> 1) & 7)) << 4);
+    const unsigned char *asrc = A + 16 * lane;
+    const bool act_lane = wave == 0 && lane < B8::RB / 16;
+    auto issue = [&](int st) {
+        unsigned char *slot = lds + (st % D) * B8::SLOT;
+        if (wave < kIssuers)
+            __builtin_amdgcn_global_load_lds((const void *)(wsrc + (size_t)st * kStripe),
+                                             (lds_void *)(slot + wave * 1024), 16, 0, kNT);
+        if (wave == 0) {
+            if (act_lane)
+                __builtin_amdgcn_global_load_lds((const void *)(asrc + (size_t)st * B8::RB),
+                                                 (lds_void *)(slot + B8::WB), 16, 0, 0);
+        }
+    };
+#pragma unroll 1
+    for (int st = 0; st < D - R && st < ns; ++st) issue(st);
+
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) off[jj] = r * kStripe + ((jj ^ swz) << 4) + 4 * p;
+    float acc = 0.0f;
+
+    auto run = [&](auto bc) {
+        constexpr int BYTE = decltype(bc)::value;
+        // DMA instructions this wave issues per stripe: wave 0 two, the other
+        // issuers one, the rest none
+        constexpr int PERW = BYTE == 0 ? 2 : (BYTE < kIssuers ? 1 : 0);
+        const int aoff = B8::WB + (8 * t + 4 * p + BYTE) * B8::ES;
+        uint32_t xw[2][16];
+        float av[2];
+        auto load = [&](int st, int b) {
+            const unsigned char *slot = lds + (st % D) * B8::SLOT;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                xw[b][2 * jj] = *(const uint32_t *)(slot + off[jj]);
+                xw[b][2 * jj + 1] = *(const uint32_t *)(slot + off[jj] + 8);
+            }
+            if constexpr (FMT == F_W8A32)
+                av[b] = *(const float *)(slot + aoff);
+            else
+                av[b] = __uint_as_float((uint32_t)(*(const uint16_t *)(slot + aoff)) << 16);
+        };
+        auto compute = [&](int b) {
+            float w[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) w[q] = (float)(int)(int8_t)(uint8_t)(xw[b][q] >> (8 * BYTE));
+            w8b_chain16(acc, av[b], w);
+        };
+        const int nfull = ns / R * R;
+#pragma unroll 1
+        for (int s0 = 0; s0 < nfull; s0 += R) {
+            if (s0 + D - R - 1 < ns)
+                wait_vmcnt<PERW *(D - 2 * R)>();   // stripes s0+R .. s0+D-R-1 may still fly
+            else
+                wait_vmcnt<0>();
+            lds_sync();
+#pragma unroll
+            for (int u = 0; u < R; ++u)
+                if (s0 + D - R + u < ns) issue(s0 + D - R + u);
+            load(s0, 0);
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (u + 1 < R) load(s0 + u + 1, (u + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(u & 1);
+            }
+        }
+#pragma unroll 1
+        for (int s = nfull; s < ns; ++s) {
+            wait_vmcnt<0>();
+            lds_sync();
+            load(s, 0);
+            compute(0);
+        }
+    };
+    switch (wave) {
+        case 0: run(std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        default: run(std::integral_constant<int, 3>{}); break;
+    }
+
+    // red[row][chain l = 4p + b] (16-row tiles: DPP rows 2, 3 store the same
+    // values as rows 0, 1); lane r of wave 0 adds row r's chains.
+    float *red = (float *)lds;
+    lds_sync();
+    red[r * 8 + 4 * p + wave] = acc;
+    lds_sync();
+    const int n = row0 + lane;
+    if (wave != 0 || lane >= ROWS || n >= N) return;
+    float l8[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) l8[l] = red[lane * 8 + l];
+    const float y = hsum8(l8) * S[n];
+    if constexpr (FMT == F_W8A32)
+        ((float *)C)[n] = y;
+    else
+        ((uint16_t *)C)[n] = f32_to_bf16(y);
+}
+
+template <int FMT, int ROWS, int D>
+int launch_w8b_one(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int N, int K) {
+    constexpr size_t lds = (size_t)D * W8bFmt<FMT, ROWS>::SLOT;
+    static_assert(lds <= kRowMaxLds, "byte-wave ring");
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_w8b_kernel<FMT, D, ROWS>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    gemv_w8b_kernel<FMT, D, ROWS><<<(unsigned)((N + ROWS - 1) / ROWS), 256, lds, st>>>(A, W, S, C, N, K);
+    return ECPU_OK;
+}
+
+// 16-row tiles below 8192 rows (every CU gets a tile), 32 beyond.
+template <int FMT>
+int launch_w8b(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int N, int K) {
+    int rows = N < 8192 ? 16 : 32;
+    const int env_rows = env_int("PILM_HIP_W8B_ROWS", 0);
+    if (env_rows == 16 || env_rows == 32) rows = env_rows;
+    // (a 32-slot ring measured slower at every shape: 4096x4096 11.2 vs 9.8 us)
+    return rows == 16 ? launch_w8b_one<FMT, 16, 16>(st, A, W, S, C, N, K)
+                      : launch_w8b_one<FMT, 32, 16>(st, A, W, S, C, N, K);
+}
+
 // ------------------------------------------------------------------ row broadcast
 // Per-row formats with a few activation rows (MTP verify M = 1 + drafts,
 // short prefills): each weight feeds M FMAs, so the exact path is bound by
@@ -1455,6 +1644,15 @@ int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
              hipStream_t st, const char *fn) {
     // A few activation rows: the row-broadcast kernel, every M in one launch.
     if (M >= 3 && env_int("PILM_HIP_RBC", 1) != 0) return run_rbc(fmt, M, N, K, A, W, S, C, st, fn);
+    // One row of a W8 format below 16384 rows: the byte-wave kernel (measured
+    // W8A32 4096x4096 9.6 vs 10.4 us, 8192x4096 11.5 vs 13.5 us, 4096x12288
+    // 24.1 vs 26.8 us; the quad / 64-row kernels stay ahead beyond).
+    if (M == 1 && fmt != F_W4ROW && env_int("PILM_HIP_W8B", N < 16384 ? 1 : 0) != 0) {
+        const int rc = fmt == F_W8A32 ? launch_w8b<F_W8A32>(st, A, W, S, C, (int)N, (int)K)
+                                      : launch_w8b<F_W8A16>(st, A, W, S, C, (int)N, (int)K);
+        if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+        return ECPU_OK;
+    }
     // Few 16-row tiles: the chain kernel (several SIMDs per tile).
     const int qt_all = (int)((N + 15) / 16);
     int cs = env_int("PILM_HIP_CS", -1);

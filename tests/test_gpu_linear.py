@@ -96,15 +96,18 @@ ROW_PATHS = [{"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64"
              {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "4"},
              {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "16"},
              {"PILM_HIP_CS": "2"}, {"PILM_HIP_CS": "4"},
-             {"PILM_HIP_ROWS": "0"}, {"PILM_HIP_RBC": "0"}, {"PILM_HIP_RBC_MT": "4"}]
+             {"PILM_HIP_ROWS": "0"}, {"PILM_HIP_RBC": "0"}, {"PILM_HIP_RBC_MT": "4"},
+             {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "16"}, {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "32"},
+             {"PILM_HIP_W8B": "0"}]
 
 
 @pytest.mark.parametrize("env", ROW_PATHS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
 def test_row_format_paths_identical(env, dev, monkeypatch):
     """Per-row formats: every tile height and ring depth of the chain-split
     kernels (four waves per 64-row tile, four lanes per row, or two / four
-    waves per 16-row tile), the one-wave-per-tile kernel and the small-M
-    row-broadcast kernel (4 or 8 rows per wave, or off) give the same bits."""
+    waves per 16-row tile), the one-wave-per-tile kernel, the byte-wave W8
+    kernel (16- or 32-row tiles, or off) and the small-M row-broadcast
+    kernel (4 or 8 rows per wave, or off) give the same bits."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for case in GV.linear_cases(max_elems=1 << 24):
