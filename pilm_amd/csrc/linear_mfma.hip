@@ -53,6 +53,8 @@ struct MF {
     static constexpr int group = FMT == F_W4G128 ? 128 : (FMT == F_W4G32 ? 32 : 0);
     static constexpr int wrow = w8 ? kBK : kBK / 2;   // weight bytes per row per stage
     static constexpr int planes = a32 ? 2 : 1;        // fp16 parts per activation
+    // chunk swizzle of weight row r in the LDS tile (wrow / 16 chunks per row)
+    static __device__ __forceinline__ int wswz(int r) { return w8 ? (r >> 2) & 3 : (r >> 3) & 1; }
 };
 
 // fp16 pair of two bf16 values (exact in the fp16 normal range), packed lo/hi.
@@ -176,13 +178,17 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
                                                  16, 0, 0);
             }
     };
-    // Weight tile: row-major, wrow bytes per row, by DMA (16 B per lane).
+    // Weight tile: wrow bytes per row, by DMA (16 B per lane); the row's
+    // 16-byte chunks sit at positions ch ^ wswz(row), so that the 32 rows a
+    // wave reads at one k fall on different LDS banks (rows 8 apart for int4,
+    // 4 apart for int8 would otherwise share them).
     auto load_w = [&](int t, int b) {
         unsigned char *ws = lds + b * STAGE + A_BYTES;
 #pragma unroll
         for (int i = 0; i < W_LOADS; ++i) {
-            const int idx = tid + i * kMfmaThreads;            // 16-byte chunk of the tile
-            const int row = idx / (F::wrow / 16), ch = idx % (F::wrow / 16);
+            const int idx = tid + i * kMfmaThreads;            // 16-byte position in the tile
+            const int row = idx / (F::wrow / 16), pos = idx % (F::wrow / 16);
+            const int ch = pos ^ F::wswz(row);
             const int n = min(n0 + row, N - 1);
             const uint8_t *src = W + (size_t)n * row_bytes + (size_t)(t0 + t) * F::wrow + ch * 16;
             __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(ws + (i * kMfmaThreads + wave * 64) * 16),
@@ -246,8 +252,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
                 const int nl = ncol_base + j * 32 + (lane & 31);
                 u32x4 q;
                 if constexpr (F::w8) {
-                    // bytes k..k+7 of row nl: k = 16 kk + 8 (lane >> 5)
-                    const uint32_t *pw = (const uint32_t *)(ws + nl * F::wrow + 16 * kk + 8 * (lane >> 5));
+                    // bytes k..k+7 of row nl: k = 16 kk + 8 (lane >> 5), chunk kk
+                    const uint32_t *pw =
+                        (const uint32_t *)(ws + nl * F::wrow + ((kk ^ F::wswz(nl)) << 4) + 8 * (lane >> 5));
                     const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
                     for (int d = 0; d < 2; ++d) {
@@ -258,7 +265,9 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
                         q[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
                     }
                 } else {
-                    const uint32_t x = *(const uint32_t *)(ws + nl * F::wrow + 8 * kk + 4 * (lane >> 5));
+                    // nibbles k..k+7 of row nl: byte 8 kk + 4 (lane >> 5), chunk kk / 2
+                    const uint32_t x = *(const uint32_t *)(ws + nl * F::wrow + (((kk >> 1) ^ F::wswz(nl)) << 4) +
+                                                           8 * (kk & 1) + 4 * (lane >> 5));
                     h2 qq[4];
                     dequant_w4(x, magic, qq);
                     if constexpr (F::group > 0) {
