@@ -170,6 +170,21 @@ def test_small_m_row_formats(fmt, dev):
         assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n, k)
 
 
+@pytest.mark.parametrize("fmt", ["w8a32", "w8a16", "w4", "w4g32", "w4g128"])
+def test_m_boundaries(fmt, dev):
+    """M around the kernel switches: 2 / 3 (group-quad or quad -> small-M
+    kernels), 4 / 5 and 8 / 9 (m-groups of 4 and 8), 63 (the last exact M
+    below the matrix cores); bit-exact against the oracle."""
+    gen = GV._gen()
+    for m in (2, 3, 4, 5, 8, 9, 63):
+        n, k = 70, 512
+        _say(f"[gpu] M boundary {fmt} M={m} N={n} K={k}")
+        x, w, s = gen.make_inputs(fmt, m, n, k, 7300 + m)
+        y = run_gpu(fmt, x, w, s, dev)
+        ref = gen.run(fmt, x, w, s, "oracle")
+        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n, k)
+
+
 def test_power_of_two_scale_full_size(dev):
     """Size-independent property at the lm_head shape: doubling the scales doubles every output."""
     n, k = 151936, 2048
