@@ -1618,6 +1618,207 @@ int launch_gq_mt(int mt, int ntiles, hipStream_t st, const uint16_t *A, const ui
     }
 }
 
+// 8-row tiles for one activation row (k/v, o, down at 1.7B: 64-128 16-row
+// tiles would leave CUs idle, and dividing a tile across workgroups costs a
+// global round trip).  Lane 8r + c serves row r: c < 4 the lo half of each
+// 16-element chunk, c >= 4 the hi half, chains (c & 3) and (c & 3) + 4 --
+// two int4 chains per lane instead of four.  The block sums of a group meet
+// in the reference's order: lo + hi (lane c reads lane c + 4 of its 16-lane
+// row by DPP row_ror:12), then ((l0+l4)+(l1+l5)) + ((l2+l6)+(l3+l7)) by quad
+// permutes.
+// Otherwise as gemv_gq_kernel (per-wave rings, activations and scales by DMA,
+// blocks folded in group order by lane 8r of wave 0).
+// Value of lane i + 4 (mod 16) of the 16-lane row: row_ror:12 (lane i reads
+// lane i - 12).
+__device__ __forceinline__ float dpp_up4(float x) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x12C, 0xF, 0xF, false));
+}
+
+template <int FMT, int D, int P>
+__global__ __launch_bounds__(64 * P) void gemv_gq8_kernel(const uint16_t *__restrict__ A, const uint8_t *__restrict__ W,
+                                                      const float *__restrict__ S, uint16_t *__restrict__ C, int N,
+                                                      int K) {
+    constexpr int GS = FMT == F_W4G128 ? 128 : 32;   // group size
+    constexpr int GPS = 256 / GS;                    // groups per stripe: 2 or 8
+    constexpr int WPG = 16 / GPS;                    // lane words per group: 8 or 2
+    constexpr int SLOT = 8 * kStripe;                // one stripe of the tile: 8 rows x 128 B
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 3, c = lane & 7, par = c >> 2, nb = c & 3;
+    const int row0 = blockIdx.x * 8;
+    const size_t row_bytes = (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    const int G = K / GS;
+    const int rdw = K / 2;                          // activation dwords
+    const int sps = (ns + P - 1) / P;
+    const int sb = min(ns, wave * sps);
+    const int nsw = min(ns, sb + sps) - sb;         // this wave's stripes (may be 0)
+    unsigned char *act = lds + (size_t)P * D * SLOT;
+    float *scl = (float *)(act + (size_t)rdw * 4);  // [8][G]
+    float *blk = scl + 8 * G;                       // [8][G]
+
+    // Activation row (16-byte DMA, 256 dwords per instruction) and the
+    // tile's scales (4-byte DMA, 64 per instruction), dealt round-robin.
+    {
+        int issued = 0;
+        const uint32_t *a = (const uint32_t *)A;
+#pragma unroll 1
+        for (int q = wave; q * 256 < rdw; q += P) {
+            const int g = q * 256 + 4 * lane;
+            if (g < rdw)
+                __builtin_amdgcn_global_load_lds((const void *)(a + g), (lds_void *)(act + (size_t)q * 1024), 16, 0,
+                                                 0);
+            if ((++issued & 15) == 0) wait_vmcnt<16>();
+        }
+        const int nscl = 8 * G;
+#pragma unroll 1
+        for (int q = wave; q * 64 < nscl; q += P) {
+            const int i = q * 64 + lane;
+            if (i < nscl) {
+                const int rr = i / G, g = i - rr * G;
+                __builtin_amdgcn_global_load_lds((const void *)(S + (size_t)min(row0 + rr, N - 1) * G + g),
+                                                 (lds_void *)(scl + q * 64), 4, 0, 0);
+            }
+            if ((++issued & 15) == 0) wait_vmcnt<16>();
+        }
+    }
+
+    // This wave's stripes through its own ring of D slots: lane t fetches
+    // row t/8, chunk (t & 7) ^ ((row >> 1) & 7).
+    const int rr = lane >> 3;
+    const uint8_t *src = W + (size_t)min(row0 + rr, N - 1) * row_bytes + (((lane & 7) ^ ((rr >> 1) & 7)) << 4);
+    unsigned char *ring = lds + (size_t)wave * D * SLOT;
+    auto issue = [&](int t) {
+        __builtin_amdgcn_global_load_lds((const void *)(src + (size_t)(sb + t) * kStripe),
+                                         (lds_void *)(ring + (t % D) * SLOT), 16, 0, kNT);
+    };
+#pragma unroll
+    for (int t = 0; t < D - 2; ++t)
+        if (t < nsw) issue(t);
+    if (nsw >= D - 2)
+        wait_vmcnt<D - 2>();   // activation and scale copies, older than the stripes
+    else
+        wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");
+
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = r * kStripe + ((j ^ swz) << 4) + 4 * par;
+    // activation dwords of chunk T hold elements 16T + 8 par + nb (and + 4)
+    // in half nb & 1
+    const uint32_t *my_act = (const uint32_t *)act + 4 * par + (nb >> 1);
+    const uint32_t sel = (nb & 1) ? 0x03020C0Cu : 0x01000C0Cu;   // v_perm: that half -> fp32 bits
+    const uint32_t shift = 4u * nb;
+    const uint32_t magic = opaque_magic();
+
+    float acc0 = 0.0f, acc1 = 0.0f;   // chains nb and nb + 4 of the lane's half
+    auto load = [&](int t, uint32_t (&x)[16], uint32_t (&av)[32]) {
+        const unsigned char *slot = ring + (t % D) * SLOT;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[2 * j] = *(const uint32_t *)(slot + off[j]);
+            x[2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+        const int st = sb + t;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t *ap = my_act + 8 * (16 * st + u);
+            av[2 * u] = ap[0];
+            av[2 * u + 1] = ap[2];
+        }
+    };
+    auto compute = [&](int t, const uint32_t (&x)[16], const uint32_t (&av)[32]) {
+        const int g0 = (sb + t) * GPS;
+#pragma unroll
+        for (int gi = 0; gi < GPS; ++gi) {
+#pragma unroll
+            for (int u = gi * WPG; u < (gi + 1) * WPG; ++u) {
+                const uint32_t v = (x[u] ^ 0x88888888u) >> shift;
+                const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+                const h2 q = __builtin_bit_cast(h2, (v & 0x000F000Fu) | magic) + bias;
+                const float a0 = __uint_as_float(__builtin_amdgcn_perm(0u, av[2 * u], sel));
+                const float a1 = __uint_as_float(__builtin_amdgcn_perm(0u, av[2 * u + 1], sel));
+                acc0 = __builtin_fmaf(a0, (float)q.x, acc0);
+                acc1 = __builtin_fmaf(a1, (float)q.y, acc1);
+            }
+            // lo + hi (lanes c < 4 read lane c + 4), then the quad sums in
+            // the reference's order
+            const float s0 = acc0 + dpp_up4(acc0);   // s_nb
+            const float s4 = acc1 + dpp_up4(acc1);   // s_{nb+4}
+            const float h = dpp_quad_add(dpp_quad_add(s0 + s4, 0), 1);
+            if (c == 0) blk[r * G + g0 + gi] = h;
+            acc0 = 0.0f;
+            acc1 = 0.0f;
+        }
+    };
+    uint32_t xa[16], xb[16];
+    uint32_t aa[32], ab[32];
+    if (nsw > 0) {
+        if (nsw >= D - 2)
+            wait_vmcnt<D - 3>();
+        else
+            wait_vmcnt<0>();
+        load(0, xa, aa);
+    }
+    int t = 0;
+#pragma unroll 1
+    for (; t + 1 < nsw; t += 2) {
+        if (t + D - 2 < nsw) issue(t + D - 2);
+        if (t + D - 1 < nsw) issue(t + D - 1);
+        if (t + D <= nsw)
+            wait_vmcnt<D - 2>();
+        else
+            wait_vmcnt<0>();
+        load(t + 1, xb, ab);
+        compute(t, xa, aa);
+        if (t + 2 < nsw) {
+            if (t + D <= nsw)
+                wait_vmcnt<D - 3>();
+            else
+                wait_vmcnt<0>();
+            load(t + 2, xa, aa);
+        }
+        compute(t + 1, xb, ab);
+    }
+    if (t < nsw) compute(t, xa, aa);
+
+    // Fold: row r's blocks in group order (kernels.c:1141-1150), by lane 8r of wave 0.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int n = row0 + r;
+    if (wave != 0 || c != 0 || n >= N) return;
+    const float *sr = scl + r * G;
+    const float *br = blk + r * G;
+    float a = 0.0f;
+#pragma unroll 8
+    for (int g = 0; g < G; ++g) a = __builtin_fmaf(br[g], sr[g], a);
+    C[n] = f32_to_bf16(a);
+}
+
+template <int FMT, int D, int P>
+size_t gq8_lds_bytes(int K) {
+    const size_t G = (size_t)K / (FMT == F_W4G128 ? 128 : 32);
+    return (size_t)P * D * 8 * kStripe + (size_t)K * 2 + 8 * G * 4 + 8 * G * 4;
+}
+
+template <int FMT, int D, int P>
+int launch_gq8(int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *C, int N,
+               int K) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_gq8_kernel<FMT, D, P>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = gq8_lds_bytes<FMT, D, P>(K);
+    if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
+    gemv_gq8_kernel<FMT, D, P><<<ntiles, 64 * P, lds, st>>>(A, W, S, C, N, K);
+    return ECPU_OK;
+}
+
 template <int FMT>
 int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W,
                   const float *S, uint16_t *C, int N, int K, int m0) {
@@ -1764,6 +1965,26 @@ int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const u
                    hipStream_t st, const char *fn) {
     const int ntiles = (int)((N + 15) / 16);
     const int ns = (int)(K / 256);
+    // One activation row and fewer 16-row tiles than CUs: 8-row tiles.
+    if (M == 1 && env_int("PILM_HIP_GQ8", ntiles < 256 ? 1 : 0) != 0) {
+        int p = 8;
+        while (p > 1 && ns < p) p /= 2;
+        const int nt8 = (int)((N + 7) / 8);
+        int rc;
+        if (fmt == F_W4G128)
+            rc = p == 8 ? launch_gq8<F_W4G128, 4, 8>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
+                 : p == 4 ? launch_gq8<F_W4G128, 8, 4>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
+                 : p == 2 ? launch_gq8<F_W4G128, 8, 2>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
+                          : launch_gq8<F_W4G128, 16, 1>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K);
+        else
+            rc = p == 8 ? launch_gq8<F_W4G32, 4, 8>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
+                 : p == 4 ? launch_gq8<F_W4G32, 8, 4>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
+                 : p == 2 ? launch_gq8<F_W4G32, 8, 2>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
+                          : launch_gq8<F_W4G32, 16, 1>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K);
+        if (rc == ECPU_ERR_DEVICE) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+        if (rc == ECPU_OK) return ECPU_OK;
+        // (rows too long for LDS: the 16-row kernel below)
+    }
     // Eight waves per tile for one or two activation rows (the eight-wave
     // kernels hold two in registers; measured faster than four at every
     // Qwen3 shape, e.g. 6144x2048 5.5 vs 6.1 us, 8192x4096 8.9 vs 11.0 us),

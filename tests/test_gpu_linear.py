@@ -67,7 +67,7 @@ SPLITS = [{"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_GQ": "0", "PI
           {"PILM_HIP_GQ": "0", "PILM_HIP_PL": "8", "PILM_HIP_PG": "2"},
           {"PILM_HIP_GQ_P": "1"}, {"PILM_HIP_GQ_P": "2"}, {"PILM_HIP_GQ_P": "4"},
           {"PILM_HIP_GQ_P": "4", "PILM_HIP_GQ_D": "16"}, {"PILM_HIP_GQ_P": "8"},
-          {"PILM_HIP_GQ_P": "8", "PILM_HIP_GQ_D": "8"},
+          {"PILM_HIP_GQ_P": "8", "PILM_HIP_GQ_D": "8"}, {"PILM_HIP_GQ8": "0"}, {"PILM_HIP_GQ8": "1"},
           {"PILM_HIP_BCAST_PL": "1"}, {"PILM_HIP_BCAST_PL": "3"}, {"PILM_HIP_BCAST_MT": "8"},
           {"PILM_HIP_BCAST_MT": "8", "PILM_HIP_BCAST_PL": "2"}, {"PILM_HIP_BCAST": "0"},
           {"PILM_HIP_BCAST": "0", "PILM_HIP_GQ": "0"}]
@@ -76,8 +76,8 @@ SPLITS = [{"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_GQ": "0", "PI
 @pytest.mark.parametrize("env", SPLITS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
 def test_group_split_variants_identical(env, dev, monkeypatch):
     """Splitting K across waves (in LDS or in global memory; 64-row tiles,
-    the 16-row group-quad tiles, or the small-M broadcast kernel) must not
-    change a single bit."""
+    the 16- or 8-row group-quad tiles, or the small-M broadcast kernel) must
+    not change a single bit."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for prefix in ("config2_w4g128_M1", "config2_w4g128_M4", "w4g32_cancel", "w4g128_cancel"):
