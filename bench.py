@@ -16,7 +16,8 @@ Printed JSON line:
   value        algorithmic GB/s of the whole step (weights + scales +
                activations + outputs, each counted once) / wall time
   roofline     the g128 GEMV kernels' algorithmic GB/s per launch (the
-               group-quad kernel for the 196 projections, the 64-row exact
+               group-quad kernels for the 196 projections, 8-row tiles for
+               k/v/o/down and 16-row tiles for q/gate/up, the 64-row exact
                kernel for lm_head; they are the step's only kernels): HIP
                events on the replay stream around the timed replays, divided
                by the launches, against 8 TB/s
@@ -50,9 +51,10 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 KERNEL_SRCS = [ROOT / "pilm_amd" / "csrc" / f for f in ("linear_exact.hip", "linear_rows.hip", "gemv_device.h")]
 # The kernels of the W4A16 group-128 GEMV path at M=1: the group-quad kernel
-# for the projections (N <= 65536), the 64-row exact kernel for lm_head.
-GEMV_KERNELS = ("gemv_gq_kernel<3, 1,", "gemv_exact_kernel<3, 1>")
-GEMV_KERNEL = "gemv_gq_kernel<3, 1, *> + gemv_exact_kernel<3, 1>"
+# for the projections (8-row tiles below 4096 rows, 16-row tiles up to 8192),
+# the 64-row exact kernel for lm_head.
+GEMV_KERNELS = ("gemv_gq_kernel<3, 1,", "gemv_gq8_kernel<3,", "gemv_exact_kernel<3, 1>")
+GEMV_KERNEL = "gemv_gq_kernel<3, 1, *> + gemv_gq8_kernel<3, *> + gemv_exact_kernel<3, 1>"
 TRAFFIC_FILE = ROOT / "profiles" / "gemv_w4a16g128_m1_qwen3_1p7b_decode.traffic.txt"
 CALIB_BYTES = 1 << 30                              # copy kernel: reads and writes 1 GiB
 LAYERS = 28
