@@ -895,6 +895,167 @@ int chain_rows_per_launch(int K) {
     return 0;
 }
 
+// ------------------------------------------------------------------ chain, 8 rows
+// W4 per-row (bundle v2), one activation row, a few thousand rows: the chain
+// kernel's 16-row tiles leave CUs idle below 4096 rows (k/v 1024: 64 tiles).
+// Here a tile has 8 rows, lane 8r + c serves row r with chain group c (lo
+// half for c < 4, hi for c >= 4; nibbles c & 3 and (c & 3) + 4) and the two
+// waves of the workgroup take one of those two chains each, so every lane
+// runs one chain: chain 8h + l, l = (c & 3) + 4w.  Activations are staged in
+// LDS chain-major as in the chain kernel (a lane reads its chain's sixteen
+// values of a stripe with four 16-byte loads shared by the eight rows); the
+// waves share a ring of D one-stripe slots (wave 0 issues the DMA, one
+// barrier per round of four stripes); chain sums meet in LDS and lane r of
+// wave 0 adds lo[l] + hi[l], then the reference's hsum, times the scale.
+template <int D>
+__global__ __launch_bounds__(128) void gemv_w4c8_kernel(const uint16_t *__restrict__ A, const uint8_t *__restrict__ W,
+                                                       const float *__restrict__ S, uint16_t *__restrict__ C, int N,
+                                                       int K) {
+    using F = ChainFmt<F_W4ROW, 4>;   // activation layout (perm, row_floats) only
+    constexpr int R = 4;
+    constexpr int SLOT = 8 * kStripe;
+    static_assert(D % R == 0 && D >= 2 * R, "ring depth");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 3, c = lane & 7, par = c >> 2;
+    const int l = (c & 3) + 4 * wave;      // the lane's chain within its half
+    const int chain = 8 * par + l;
+    const int row0 = blockIdx.x * 8;
+    const size_t row_bytes = (size_t)K / 2;
+    const int ns = (int)(row_bytes / kStripe);
+    unsigned char *ring = lds;
+    float *act = (float *)(lds + (size_t)D * SLOT);
+    float *red = act + F::row_floats(K);   // [2 waves][64 lanes]
+
+    // Stripe DMA (wave 0): lane t fetches row t/8, chunk (t & 7) ^ ((row >> 1) & 7).
+    const int dr = lane >> 3;
+    const uint8_t *src = W + (size_t)min(row0 + dr, N - 1) * row_bytes + (((lane & 7) ^ ((dr >> 1) & 7)) << 4);
+    auto issue = [&](int st) {
+        __builtin_amdgcn_global_load_lds((const void *)(src + (size_t)st * kStripe),
+                                         (lds_void *)(ring + (st % D) * SLOT), 16, 0, kNT);
+    };
+    // Activations -> fp32, chain-major (16-byte loads, four per lane in flight).
+    {
+        const int nvec = K / 8, nthr = 128;
+#pragma unroll 1
+        for (int v0 = 0; v0 < nvec; v0 += 4 * nthr) {
+            u32x4 buf[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int v = v0 + u * nthr + (int)threadIdx.x;
+                if (v < nvec) buf[u] = ((const u32x4 *)A)[v];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int v = v0 + u * nthr + (int)threadIdx.x;
+                if (v >= nvec) continue;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t word = buf[u][e >> 1];
+                    act[F::perm(v * 8 + e)] = (e & 1) ? bf16_hi(word) : bf16_lo(word);
+                }
+            }
+        }
+    }
+    if (wave == 0) {
+#pragma unroll 1
+        for (int t = 0; t < D - R; ++t)
+            if (t < ns) issue(t);
+    }
+    // (the first round's barrier orders the activation writes before any read)
+
+    const int swz = (r >> 1) & 7;
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = r * kStripe + ((j ^ swz) << 4) + 4 * par;
+    const int bit = 4 * l;
+    float acc = 0.0f;
+    uint32_t xw[2][16];
+    f32x4 av[2][4];
+    auto load = [&](int st, int b) {
+        const unsigned char *slot = ring + (st % D) * SLOT;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            xw[b][2 * j] = *(const uint32_t *)(slot + off[j]);
+            xw[b][2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
+        }
+        const f32x4 *ap = (const f32x4 *)(act + (st * 16 + chain) * F::kBlock);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) av[b][v] = ap[v];
+    };
+    auto compute = [&](int b) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float w = (float)(int)__builtin_amdgcn_sbfe((int)xw[b][t], bit, 4);
+            acc = __builtin_fmaf(av[b][t >> 2][t & 3], w, acc);
+        }
+    };
+    const int nfull = ns / R * R;
+#pragma unroll 1
+    for (int s0 = 0; s0 < nfull; s0 += R) {
+        if (wave == 0) {
+            if (s0 + D - R - 1 < ns)
+                wait_vmcnt<D - 2 * R>();   // stripes s0+R .. s0+D-R-1 may still fly
+            else
+                wait_vmcnt<0>();
+        }
+        lds_sync();
+        if (wave == 0) {
+#pragma unroll
+            for (int u = 0; u < R; ++u)
+                if (s0 + D - R + u < ns) issue(s0 + D - R + u);
+        }
+        load(s0, 0);
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 1 < R) load(s0 + u + 1, (u + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(u & 1);
+        }
+    }
+#pragma unroll 1
+    for (int s = nfull; s < ns; ++s) {
+        if (wave == 0) wait_vmcnt<0>();
+        lds_sync();
+        load(s, 0);
+        compute(0);
+    }
+
+    red[wave * 64 + lane] = acc;
+    lds_sync();
+    const int n = row0 + r;
+    if (wave != 0 || c != 0 || n >= N) return;
+    float l8[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const float *rw = red + (q >> 2) * 64 + 8 * r + (q & 3);   // wave q/4, lanes c = q & 3 (lo), + 4 (hi)
+        l8[q] = rw[0] + rw[4];
+    }
+    C[n] = f32_to_bf16(hsum8(l8) * S[n]);
+}
+
+template <int D>
+size_t w4c8_lds_bytes(int K) {
+    return (size_t)D * 8 * kStripe + (size_t)(K / 16) * ChainFmt<F_W4ROW, 4>::kBlock * 4 + 2 * 64 * 4;
+}
+
+template <int D>
+int launch_w4c8(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int N, int K) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_w4c8_kernel<D>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = w4c8_lds_bytes<D>(K);
+    if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
+    gemv_w4c8_kernel<D><<<(unsigned)((N + 7) / 8), 128, lds, st>>>((const uint16_t *)A, W, S, (uint16_t *)C, N, K);
+    return ECPU_OK;
+}
+
 // ------------------------------------------------------------------ byte waves
 // W8A32 / W8A16 decode (M = 1), a few thousand rows: the chain kernel pays
 // three VALU instructions per weight because a lane's byte position inside
@@ -1845,6 +2006,14 @@ int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
              hipStream_t st, const char *fn) {
     // A few activation rows: the row-broadcast kernel, every M in one launch.
     if (M >= 3 && env_int("PILM_HIP_RBC", 1) != 0) return run_rbc(fmt, M, N, K, A, W, S, C, st, fn);
+    // One row of W4 per-row below 4096 rows: 8-row chain tiles (measured
+    // 1024x2048 4.49 -> 4.02 us, 2048x6144 8.59 -> 7.79 us; slower from 4096
+    // rows on, where the 16-row tiles already cover every CU).
+    if (M == 1 && fmt == F_W4ROW && env_int("PILM_HIP_W4C8", N < 4096 ? 1 : 0) != 0) {
+        const int rc = launch_w4c8<16>(st, A, W, S, C, (int)N, (int)K);
+        if (rc == ECPU_ERR_DEVICE) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+        if (rc == ECPU_OK) return ECPU_OK;
+    }
     // One row of a W8 format below 16384 rows: the byte-wave kernel (measured
     // W8A32 4096x4096 9.6 vs 10.4 us, 8192x4096 11.5 vs 13.5 us, 4096x12288
     // 24.1 vs 26.8 us; the quad / 64-row kernels stay ahead beyond).

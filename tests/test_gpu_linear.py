@@ -98,7 +98,7 @@ ROW_PATHS = [{"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64"
              {"PILM_HIP_CS": "2"}, {"PILM_HIP_CS": "4"},
              {"PILM_HIP_ROWS": "0"}, {"PILM_HIP_RBC": "0"}, {"PILM_HIP_RBC_MT": "4"},
              {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "16"}, {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "32"},
-             {"PILM_HIP_W8B": "0"}]
+             {"PILM_HIP_W8B": "0"}, {"PILM_HIP_W4C8": "1"}, {"PILM_HIP_W4C8": "0"}]
 
 
 @pytest.mark.parametrize("env", ROW_PATHS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
