@@ -523,8 +523,9 @@ def main(argv=None) -> int:
         print(stats_summary(args.stats_summary))
         return 0
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the decode GEMV would shard by output rows, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py measures one GPU: there is no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the decode GEMV would shard by output rows, each GPU holding W[N/G, K] and its scales",
+              file=sys.stderr)
         return 2
 
     import torch
