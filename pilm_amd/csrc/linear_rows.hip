@@ -1101,13 +1101,16 @@ __global__ __launch_bounds__(256) void gemv_w8b_kernel(const void *__restrict__ 
                                                       const float *__restrict__ S, void *__restrict__ C, int N,
                                                       int K) {
     using B8 = W8bFmt<FMT, ROWS>;
-    static_assert(ROWS == 16 || ROWS == 32, "tile height");
+    static_assert(ROWS == 8 || ROWS == 16 || ROWS == 32, "tile height");
     constexpr int R = 4;   // stripes per round
     static_assert(D % R == 0 && D >= 2 * R, "ring depth");
     extern __shared__ __align__(16) unsigned char lds[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int t = lane & 15, j = lane >> 4, p = j & 1, r = (ROWS == 32 ? 16 * (j >> 1) : 0) + t;
+    // (8-row tiles: lanes t >= 8 repeat rows t - 8, each DPP row still
+    // carrying the stripe's sixteen steps)
+    const int t = lane & 15, j = lane >> 4, p = j & 1;
+    const int r = ROWS == 32 ? 16 * (j >> 1) + t : (ROWS == 16 ? t : (t & 7));
     const int row0 = blockIdx.x * ROWS;
     const int ns = K / kStripe;
     const unsigned char *A = (const unsigned char *)A_;
@@ -1202,7 +1205,8 @@ __global__ __launch_bounds__(256) void gemv_w8b_kernel(const void *__restrict__ 
     }
 
     // red[row][chain l = 4p + b] (16-row tiles: DPP rows 2, 3 store the same
-    // values as rows 0, 1); lane r of wave 0 adds row r's chains.
+    // values as rows 0, 1; 8-row tiles: lanes t >= 8 the same as t - 8); lane
+    // r of wave 0 adds row r's chains.
     float *red = (float *)lds;
     lds_sync();
     red[r * 8 + 4 * p + wave] = acc;
@@ -1234,13 +1238,15 @@ int launch_w8b_one(hipStream_t st, const void *A, const uint8_t *W, const float 
     return ECPU_OK;
 }
 
-// 16-row tiles below 8192 rows (every CU gets a tile), 32 beyond.
 template <int FMT>
 int launch_w8b(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int N, int K) {
-    int rows = N < 8192 ? 16 : 32;
+    // 8-row tiles up to 1024 rows (k/v: 1024x4096 W8A16 9.6 -> 8.9 us; the
+    // repeated lanes cost more than the extra CUs gain beyond), 16 below 8192.
+    int rows = N <= 1024 ? 8 : (N < 8192 ? 16 : 32);
     const int env_rows = env_int("PILM_HIP_W8B_ROWS", 0);
-    if (env_rows == 16 || env_rows == 32) rows = env_rows;
+    if (env_rows == 8 || env_rows == 16 || env_rows == 32) rows = env_rows;
     // (a 32-slot ring measured slower at every shape: 4096x4096 11.2 vs 9.8 us)
+    if (rows == 8) return launch_w8b_one<FMT, 8, 16>(st, A, W, S, C, N, K);
     return rows == 16 ? launch_w8b_one<FMT, 16, 16>(st, A, W, S, C, N, K)
                       : launch_w8b_one<FMT, 32, 16>(st, A, W, S, C, N, K);
 }
