@@ -2010,8 +2010,13 @@ int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16
 // or 256 int4 weights), 16-byte aligned weights and activations.
 int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn) {
-    // A few activation rows: the row-broadcast kernel, every M in one launch.
-    if (M >= 3 && env_int("PILM_HIP_RBC", 1) != 0) return run_rbc(fmt, M, N, K, A, W, S, C, st, fn);
+    // A few activation rows: the row-broadcast kernel, every M in one launch;
+    // at M = 2 only where the quad kernel would run (more than 512 16-row
+    // tiles, below 65536 rows: W8A16 24576x4096 37.1 vs 52.7 us; the chain
+    // kernel stays ahead below, e.g. 8192x4096 15.2 vs 19.5 us).
+    const size_t qt16 = (N + 15) / 16;
+    const bool rbc2 = M == 2 && qt16 > 512 && N < 65536;
+    if ((M >= 3 || rbc2) && env_int("PILM_HIP_RBC", 1) != 0) return run_rbc(fmt, M, N, K, A, W, S, C, st, fn);
     // One row of W4 per-row below 4096 rows: 8-row chain tiles (measured
     // 1024x2048 4.49 -> 4.02 us, 2048x6144 8.59 -> 7.79 us; slower from 4096
     // rows on, where the 16-row tiles already cover every CU).

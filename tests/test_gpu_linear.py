@@ -160,10 +160,12 @@ def test_long_rows_group_quad(fmt, dev):
 
 @pytest.mark.parametrize("fmt", ["w8a32", "w8a16", "w4"])
 def test_small_m_row_formats(fmt, dev):
-    """Per-row formats at 3 <= M < 64 (MTP verify, short prefill): the
-    row-broadcast kernel against the oracle, ragged N and partial m-groups."""
+    """Per-row formats at 3 <= M < 64 (MTP verify, short prefill), and M = 2
+    beyond 8192 rows: the row-broadcast kernel against the oracle, ragged N
+    and partial m-groups."""
     gen = GV._gen()
-    for m, n, k in ((3, 50, 1024), (5, 300, 2048), (8, 17, 256), (9, 64, 4096), (16, 130, 512), (33, 40, 768)):
+    for m, n, k in ((3, 50, 1024), (5, 300, 2048), (8, 17, 256), (9, 64, 4096), (16, 130, 512), (33, 40, 768),
+                    (2, 8200, 256)):
         _say(f"[gpu] small-M {fmt} M={m} N={n} K={k}")
         x, w, s = gen.make_inputs(fmt, m, n, k, 9100 + m)
         y = run_gpu(fmt, x, w, s, dev)
