@@ -626,15 +626,20 @@ static int launch_bcast(dim3 grid, dim3 block, size_t lds, hipStream_t st, const
 // work grows with MT, so the eight-row waves are taken only where there are
 // enough of them to fill the SIMDs (>= 1536 waves) and add no padding rows
 // over MT = 4 (measured at M = 16:
-// 6144x2048 16.4 vs 21.0 us, 4096x2048 16.3 vs 11.2 us).  Up to four rows
-// with fewer than 768 waves stay with the group-quad kernel (returns
-// ECPU_ERR_UNSUPPORTED; 4096x2048 M=4: 8.9 vs 10.9 us).
+// 6144x2048 16.4 vs 21.0 us, 4096x2048 16.3 vs 11.2 us).  The group-quad
+// kernels take (returns ECPU_ERR_UNSUPPORTED): up to four rows with fewer
+// than 768 waves or at most 6144 rows (g128 4096x4096 M=4: 13.0 vs 16.1 us,
+// 6144x2048 M=3: 9.8 vs 11.0 us), and up to eight rows when LDS leaves two
+// waves per tile or fewer (group 32, long K: 1024x4096 M=5 22 vs 50 us,
+// 4096x12288 113 vs 266 us) or takes any beyond 8192 rows (those go to the
+// 64-row tiles: g32 12288x2048 M=5 22.6 vs 29.8 us).
 static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
                      hipStream_t st, const char *fn) {
     const int nstripes = (int)(K / 256);
     const int gps = fmt == F_W4G128 ? 2 : 8;
     const int G = nstripes * gps;
     const size_t ntiles = (N + 63) / 64;
+    bool reduced = false;   // LDS took waves from the four-row plan
     auto plan = [&](int mt, int &pl, int &sps) {
         pl = std::min(kMaxParts, nstripes);
         const int env_pl = env_int("PILM_HIP_BCAST_PL", 0);
@@ -645,18 +650,20 @@ static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const
             pl = (pl + 1) / 2;
             sps = (nstripes + pl - 1) / pl;
             pl = (nstripes + sps - 1) / sps;
+            if (mt == 4) reduced = true;
         }
     };
     int pl8, sps8, pl4, sps4;
     plan(8, pl8, sps8);
     plan(4, pl4, sps4);
+    const bool cramped = reduced && (pl4 <= 2 || N > 8192);
     const size_t waves8 = ntiles * pl8 * ((M + 7) / 8), waves4 = ntiles * pl4 * ((M + 3) / 4);
     const size_t pad8 = (M + 7) / 8 * 8, pad4 = (M + 3) / 4 * 4;   // rows computed, padding included
     int mt = (pad8 <= pad4 && waves8 >= 1536) ? 8 : 4;
     const int env_mt = env_int("PILM_HIP_BCAST_MT", 0);
     if (env_mt == 4 || env_mt == 8)
         mt = env_mt;
-    else if (M <= 4 && waves4 < 768)
+    else if ((M <= 4 && (waves4 < 768 || N <= 6144)) || (M <= 8 && cramped))
         return ECPU_ERR_UNSUPPORTED;
     const int pl = mt == 8 ? pl8 : pl4, sps = mt == 8 ? sps8 : sps4;
     const size_t lds = bcast_lds_bytes(mt, pl, sps, G, gps);
@@ -971,7 +978,8 @@ int run_linear(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8
         int rc = ECPU_ERR_UNSUPPORTED;
         if (group && M >= 3 && env_int("PILM_HIP_BCAST", 1) != 0)
             rc = run_bcast(fmt, M, N, K, A, W, S, C, st, fn);
-        if (rc == ECPU_ERR_UNSUPPORTED && group && env_int("PILM_HIP_GQ", N <= 8192 ? 1 : 0) != 0)
+        // (two rows: the 64-row tiles from 6144 rows, 6144x2048 8.4 vs 10.0 us)
+        if (rc == ECPU_ERR_UNSUPPORTED && group && env_int("PILM_HIP_GQ", N <= (M == 2 ? 4096u : 8192u) ? 1 : 0) != 0)
             rc = run_group_quad(fmt, M, N, K, A, W, S, C, st, fn);
         if (rc != ECPU_OK && rc != ECPU_ERR_UNSUPPORTED) return rc;
         if (rc == ECPU_ERR_UNSUPPORTED) {

@@ -1785,9 +1785,9 @@ int launch_gq_mt(int mt, int ntiles, hipStream_t st, const uint16_t *A, const ui
     }
 }
 
-// 8-row tiles for one activation row (k/v, o, down at 1.7B: 64-128 16-row
-// tiles would leave CUs idle, and dividing a tile across workgroups costs a
-// global round trip).  Lane 8r + c serves row r: c < 4 the lo half of each
+// 8-row tiles for up to four activation rows (k/v, o, down at 1.7B: 64-128
+// 16-row tiles would leave CUs idle, and dividing a tile across workgroups
+// costs a global round trip).  Lane 8r + c serves row r: c < 4 the lo half of each
 // 16-element chunk, c >= 4 the hi half, chains (c & 3) and (c & 3) + 4 --
 // two int4 chains per lane instead of four.  The block sums of a group meet
 // in the reference's order: lo + hi (lane c reads lane c + 4 of its 16-lane
@@ -1802,10 +1802,10 @@ __device__ __forceinline__ float dpp_up4(float x) {
                               __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x12C, 0xF, 0xF, false));
 }
 
-template <int FMT, int D, int P>
+template <int FMT, int MT, int D, int P>
 __global__ __launch_bounds__(64 * P) void gemv_gq8_kernel(const uint16_t *__restrict__ A, const uint8_t *__restrict__ W,
                                                       const float *__restrict__ S, uint16_t *__restrict__ C, int N,
-                                                      int K) {
+                                                      int K, int m0) {
     constexpr int GS = FMT == F_W4G128 ? 128 : 32;   // group size
     constexpr int GPS = 256 / GS;                    // groups per stripe: 2 or 8
     constexpr int WPG = 16 / GPS;                    // lane words per group: 8 or 2
@@ -1823,18 +1823,19 @@ __global__ __launch_bounds__(64 * P) void gemv_gq8_kernel(const uint16_t *__rest
     const int sb = min(ns, wave * sps);
     const int nsw = min(ns, sb + sps) - sb;         // this wave's stripes (may be 0)
     unsigned char *act = lds + (size_t)P * D * SLOT;
-    float *scl = (float *)(act + (size_t)rdw * 4);  // [8][G]
-    float *blk = scl + 8 * G;                       // [8][G]
+    float *scl = (float *)(act + (size_t)MT * rdw * 4);   // [8][G]
+    float *blk = scl + 8 * G;                              // [MT][8][G]
 
-    // Activation row (16-byte DMA, 256 dwords per instruction) and the
+    // Activation rows m0.. (16-byte DMA, 256 dwords per instruction) and the
     // tile's scales (4-byte DMA, 64 per instruction), dealt round-robin.
     {
         int issued = 0;
-        const uint32_t *a = (const uint32_t *)A;
+        const int total = MT * rdw;
+        const uint32_t *a = (const uint32_t *)A + (size_t)m0 * rdw;
 #pragma unroll 1
-        for (int q = wave; q * 256 < rdw; q += P) {
+        for (int q = wave; q * 256 < total; q += P) {
             const int g = q * 256 + 4 * lane;
-            if (g < rdw)
+            if (g < total)
                 __builtin_amdgcn_global_load_lds((const void *)(a + g), (lds_void *)(act + (size_t)q * 1024), 16, 0,
                                                  0);
             if ((++issued & 15) == 0) wait_vmcnt<16>();
@@ -1881,24 +1882,36 @@ __global__ __launch_bounds__(64 * P) void gemv_gq8_kernel(const uint16_t *__rest
     const uint32_t shift = 4u * nb;
     const uint32_t magic = opaque_magic();
 
-    float acc0 = 0.0f, acc1 = 0.0f;   // chains nb and nb + 4 of the lane's half
-    auto load = [&](int t, uint32_t (&x)[16], uint32_t (&av)[32]) {
+    // One or two activation rows: a stripe's activation words are read with
+    // its weights, one stripe ahead; three or four: when used (the prefetched
+    // words would not fit in registers).
+    constexpr bool kPre = MT <= 2;
+    constexpr int AB = kPre ? MT : 1;
+    float acc0[MT], acc1[MT];   // chains nb and nb + 4 of the lane's half, per activation row
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
+    auto load = [&](int t, uint32_t (&x)[16], uint32_t (&av)[AB][32]) {
         const unsigned char *slot = ring + (t % D) * SLOT;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             x[2 * j] = *(const uint32_t *)(slot + off[j]);
             x[2 * j + 1] = *(const uint32_t *)(slot + off[j] + 8);
         }
-        const int st = sb + t;
+        if constexpr (kPre) {
+            const int st = sb + t;
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const uint32_t *ap = my_act + 8 * (16 * st + u);
-            av[2 * u] = ap[0];
-            av[2 * u + 1] = ap[2];
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const uint32_t *ap = my_act + (size_t)m * rdw + 8 * (16 * st + u);
+                    av[m][2 * u] = ap[0];
+                    av[m][2 * u + 1] = ap[2];
+                }
         }
     };
-    auto compute = [&](int t, const uint32_t (&x)[16], const uint32_t (&av)[32]) {
-        const int g0 = (sb + t) * GPS;
+    auto compute = [&](int t, const uint32_t (&x)[16], const uint32_t (&av)[AB][32]) {
+        const int st = sb + t;
+        const int g0 = st * GPS;
 #pragma unroll
         for (int gi = 0; gi < GPS; ++gi) {
 #pragma unroll
@@ -1906,23 +1919,38 @@ __global__ __launch_bounds__(64 * P) void gemv_gq8_kernel(const uint16_t *__rest
                 const uint32_t v = (x[u] ^ 0x88888888u) >> shift;
                 const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
                 const h2 q = __builtin_bit_cast(h2, (v & 0x000F000Fu) | magic) + bias;
-                const float a0 = __uint_as_float(__builtin_amdgcn_perm(0u, av[2 * u], sel));
-                const float a1 = __uint_as_float(__builtin_amdgcn_perm(0u, av[2 * u + 1], sel));
-                acc0 = __builtin_fmaf(a0, (float)q.x, acc0);
-                acc1 = __builtin_fmaf(a1, (float)q.y, acc1);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    uint32_t w0, w1;
+                    if constexpr (kPre) {
+                        w0 = av[m][2 * u];
+                        w1 = av[m][2 * u + 1];
+                    } else {
+                        const uint32_t *ap = my_act + (size_t)m * rdw + 8 * (16 * st + u);
+                        w0 = ap[0];
+                        w1 = ap[2];
+                    }
+                    const float a0 = __uint_as_float(__builtin_amdgcn_perm(0u, w0, sel));
+                    const float a1 = __uint_as_float(__builtin_amdgcn_perm(0u, w1, sel));
+                    acc0[m] = __builtin_fmaf(a0, (float)q.x, acc0[m]);
+                    acc1[m] = __builtin_fmaf(a1, (float)q.y, acc1[m]);
+                }
             }
             // lo + hi (lanes c < 4 read lane c + 4), then the quad sums in
             // the reference's order
-            const float s0 = acc0 + dpp_up4(acc0);   // s_nb
-            const float s4 = acc1 + dpp_up4(acc1);   // s_{nb+4}
-            const float h = dpp_quad_add(dpp_quad_add(s0 + s4, 0), 1);
-            if (c == 0) blk[r * G + g0 + gi] = h;
-            acc0 = 0.0f;
-            acc1 = 0.0f;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const float s0 = acc0[m] + dpp_up4(acc0[m]);   // s_nb
+                const float s4 = acc1[m] + dpp_up4(acc1[m]);   // s_{nb+4}
+                const float h = dpp_quad_add(dpp_quad_add(s0 + s4, 0), 1);
+                if (c == 0) blk[(m * 8 + r) * G + g0 + gi] = h;
+                acc0[m] = 0.0f;
+                acc1[m] = 0.0f;
+            }
         }
     };
     uint32_t xa[16], xb[16];
-    uint32_t aa[32], ab[32];
+    uint32_t aa[AB][32], ab[AB][32];
     if (nsw > 0) {
         if (nsw >= D - 2)
             wait_vmcnt<D - 3>();
@@ -1957,33 +1985,59 @@ __global__ __launch_bounds__(64 * P) void gemv_gq8_kernel(const uint16_t *__rest
     const int n = row0 + r;
     if (wave != 0 || c != 0 || n >= N) return;
     const float *sr = scl + r * G;
-    const float *br = blk + r * G;
-    float a = 0.0f;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const float *br = blk + (m * 8 + r) * G;
+        float a = 0.0f;
 #pragma unroll 8
-    for (int g = 0; g < G; ++g) a = __builtin_fmaf(br[g], sr[g], a);
-    C[n] = f32_to_bf16(a);
+        for (int g = 0; g < G; ++g) a = __builtin_fmaf(br[g], sr[g], a);
+        C[(size_t)(m0 + m) * N + n] = f32_to_bf16(a);
+    }
 }
 
-template <int FMT, int D, int P>
+template <int FMT, int MT, int D, int P>
 size_t gq8_lds_bytes(int K) {
     const size_t G = (size_t)K / (FMT == F_W4G128 ? 128 : 32);
-    return (size_t)P * D * 8 * kStripe + (size_t)K * 2 + 8 * G * 4 + 8 * G * 4;
+    return (size_t)P * D * 8 * kStripe + (size_t)MT * K * 2 + 8 * G * 4 + (size_t)MT * 8 * G * 4;
 }
 
-template <int FMT, int D, int P>
-int launch_gq8(int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *C, int N,
-               int K) {
+template <int FMT, int MT, int D, int P>
+int launch_gq8_one(int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *C,
+                   int N, int K, int m0) {
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     std::call_once(once, [] {
-        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_gq8_kernel<FMT, D, P>),
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_gq8_kernel<FMT, MT, D, P>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
     });
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
-    const size_t lds = gq8_lds_bytes<FMT, D, P>(K);
+    const size_t lds = gq8_lds_bytes<FMT, MT, D, P>(K);
     if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
-    gemv_gq8_kernel<FMT, D, P><<<ntiles, 64 * P, lds, st>>>(A, W, S, C, N, K);
+    gemv_gq8_kernel<FMT, MT, D, P><<<ntiles, 64 * P, lds, st>>>(A, W, S, C, N, K, m0);
     return ECPU_OK;
+}
+
+// Eight waves with four-slot rings, or fewer waves for short rows.
+template <int FMT, int MT>
+int launch_gq8(int p, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *C,
+               int N, int K, int m0) {
+    switch (p) {
+        case 8: return launch_gq8_one<FMT, MT, 4, 8>(ntiles, st, A, W, S, C, N, K, m0);
+        case 4: return launch_gq8_one<FMT, MT, 8, 4>(ntiles, st, A, W, S, C, N, K, m0);
+        case 2: return launch_gq8_one<FMT, MT, 8, 2>(ntiles, st, A, W, S, C, N, K, m0);
+        default: return launch_gq8_one<FMT, MT, 16, 1>(ntiles, st, A, W, S, C, N, K, m0);
+    }
+}
+
+template <int FMT>
+int launch_gq8_mt(int mt, int p, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S,
+                  uint16_t *C, int N, int K, int m0) {
+    switch (mt) {
+        case 1: return launch_gq8<FMT, 1>(p, ntiles, st, A, W, S, C, N, K, m0);
+        case 2: return launch_gq8<FMT, 2>(p, ntiles, st, A, W, S, C, N, K, m0);
+        case 3: return launch_gq8<FMT, 3>(p, ntiles, st, A, W, S, C, N, K, m0);
+        default: return launch_gq8<FMT, 4>(p, ntiles, st, A, W, S, C, N, K, m0);
+    }
 }
 
 template <int FMT>
@@ -2145,24 +2199,30 @@ int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const u
                    hipStream_t st, const char *fn) {
     const int ntiles = (int)((N + 15) / 16);
     const int ns = (int)(K / 256);
-    // One activation row and fewer 16-row tiles than CUs: 8-row tiles.
-    if (M == 1 && env_int("PILM_HIP_GQ8", ntiles < 256 ? 1 : 0) != 0) {
+    // 8-row tiles: one or two activation rows with fewer 16-row tiles than
+    // CUs, more rows up to 6144 output rows (g128 4096x2048 M=4 7.8 vs 8.9
+    // us; M=2 7.8 vs 5.8, so not there), in launches of up to four rows
+    // (as many as LDS holds).
+    if (env_int("PILM_HIP_GQ8", (M <= 2 ? ntiles < 256 : ntiles <= 384) ? 1 : 0) != 0) {
         int p = 8;
         while (p > 1 && ns < p) p /= 2;
+        const size_t G = K / (fmt == F_W4G128 ? 128 : 32);
+        const int d = p == 8 ? 4 : (p == 1 ? 16 : 8);
+        int per = 4;
+        while (per > 0 && (size_t)p * d * 8 * kStripe + (size_t)per * K * 2 + 8 * G * 4 + (size_t)per * 8 * G * 4 > kRowMaxLds)
+            --per;
         const int nt8 = (int)((N + 7) / 8);
-        int rc;
-        if (fmt == F_W4G128)
-            rc = p == 8 ? launch_gq8<F_W4G128, 4, 8>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
-                 : p == 4 ? launch_gq8<F_W4G128, 8, 4>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
-                 : p == 2 ? launch_gq8<F_W4G128, 8, 2>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
-                          : launch_gq8<F_W4G128, 16, 1>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K);
-        else
-            rc = p == 8 ? launch_gq8<F_W4G32, 4, 8>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
-                 : p == 4 ? launch_gq8<F_W4G32, 8, 4>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
-                 : p == 2 ? launch_gq8<F_W4G32, 8, 2>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K)
-                          : launch_gq8<F_W4G32, 16, 1>(nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C, (int)N, (int)K);
-        if (rc == ECPU_ERR_DEVICE) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
-        if (rc == ECPU_OK) return ECPU_OK;
+        for (size_t m0 = 0; per > 0 && m0 < M; m0 += per) {
+            const int mt = (int)std::min<size_t>(per, M - m0);
+            const int rc = fmt == F_W4G128
+                               ? launch_gq8_mt<F_W4G128>(mt, p, nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C,
+                                                         (int)N, (int)K, (int)m0)
+                               : launch_gq8_mt<F_W4G32>(mt, p, nt8, st, (const uint16_t *)A, W, S, (uint16_t *)C,
+                                                        (int)N, (int)K, (int)m0);
+            if (rc == ECPU_ERR_DEVICE) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+            if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: 8-row group-quad launch does not fit in LDS", fn);
+        }
+        if (per > 0) return ECPU_OK;
         // (rows too long for LDS: the 16-row kernel below)
     }
     // Eight waves per tile for one or two activation rows (the eight-wave

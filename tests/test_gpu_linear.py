@@ -148,14 +148,17 @@ def test_fresh_shapes_against_oracle(fmt, dev):
 def test_long_rows_group_quad(fmt, dev):
     """K = 12288 (Qwen3-8B down_proj): 24 KB of activations per tile beside
     the rings (group 32: 48 KB of scales and block sums as well, so fewer
-    waves per tile); the bits stay the oracle's."""
+    waves per tile, and launches of fewer activation rows); up to eight rows
+    where the small-M kernel's LDS would hold too few waves (group 32,
+    K = 4096 and 12288); the bits stay the oracle's."""
     gen = GV._gen()
-    for m, n in ((1, 200), (2, 37), (4, 64)):
-        _say(f"[gpu] long rows {fmt} M={m} N={n} K=12288")
-        x, w, s = gen.make_inputs(fmt, m, n, 12288, 4242 + m)
+    for m, n, k in ((1, 200, 12288), (2, 37, 12288), (4, 64, 12288), (5, 300, 12288), (8, 24, 12288),
+                    (5, 1024, 4096), (7, 90, 4096)):
+        _say(f"[gpu] long rows {fmt} M={m} N={n} K={k}")
+        x, w, s = gen.make_inputs(fmt, m, n, k, 4242 + m)
         y = run_gpu(fmt, x, w, s, dev)
         ref = gen.run(fmt, x, w, s, "oracle")
-        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n)
+        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), (fmt, m, n, k)
 
 
 @pytest.mark.parametrize("fmt", ["w8a32", "w8a16", "w4"])
