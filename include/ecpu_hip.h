@@ -264,6 +264,41 @@ int ecpu_hip_profile_begin(void);
 int ecpu_hip_profile_end(void);
 int ecpu_hip_profile_read(char *buf, size_t len);
 
+/* ---- paged attention on device (no C counterpart: the reference runs this
+ * step in torch, src/models/qwen3/attention.py:95-139, over the paged cache
+ * of src/runtime/kvcache/physical_kv.py:11-81) ----------------------------- */
+typedef struct {
+    size_t S;            /* query rows (tokens) of this step */
+    size_t n_heads;      /* query heads; head h reads kv head h / (n_heads / n_kv_heads) */
+    size_t n_kv_heads;
+    size_t head_dim;     /* 64, 128 or 256 */
+    size_t cache_len;    /* tokens once this step's S rows are in: positions 0 .. cache_len-1,
+                            the new rows at cache_len-S .. cache_len-1 */
+    size_t block_size;   /* tokens per cache block */
+    size_t num_blocks;   /* blocks in each cache tensor */
+    size_t n_block_ids;  /* entries of the block table */
+    size_t gate_stride;  /* elements between the gates of consecutive (s, h); 0 = no gate */
+} ekernel_paged_attention_desc_t;
+
+/* out[s, h*D + d] = bf16(sum_j p[s,h,j] * V[j, h/rep, d]) (times bf16(sigmoid(gate[s,h,d]))
+ * when gate is not NULL), with p the bf16 softmax (fp32) of the bf16 scores
+ * bf16(bf16(q[s,h,:] . K[j, h/rep, :]) * (1/sqrt(D))) over positions
+ * j <= cache_len - S + s (the causal mask), as attention.py:95-139 computes
+ * them.  q [S, H, D], k_new / v_new [S, Hkv, D] (after k_norm / rope), caches
+ * [num_blocks, block_size, Hkv, D], all bf16; position j lives in block
+ * block_ids[j / block_size], slot j % block_size.  The new rows are written
+ * into the caches (attention.py:95-97) and attended from k_new / v_new.
+ * k_cache = v_cache = NULL attends over the new rows only (cache_len == S,
+ * attention.py:115-116).  Gate (s, h, d) is gate[(s*H + h)*gate_stride + d]
+ * (the q_proj output's second half: gate = qg + D, gate_stride = 2D).
+ * Outputs within one bf16 ulp of the reference except where a score or
+ * weight lands on the other side of a rounding boundary (the fp32 sums and
+ * the exp differ in their last bits). */
+int ekernel_paged_attention_bf16(const ekernel_paged_attention_desc_t *desc, const uint16_t *q,
+                                 const uint16_t *k_new, const uint16_t *v_new, uint16_t *k_cache,
+                                 uint16_t *v_cache, const int32_t *block_ids, const uint16_t *gate,
+                                 uint16_t *out);
+
 #ifdef __cplusplus
 }
 #endif

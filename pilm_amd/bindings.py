@@ -42,6 +42,7 @@ _OPTIONAL_KERNEL_SYMBOLS = [
     "ekernel_swiglu_w4a16_bf16",
     "ekernel_rmsnorm_bf16",
     "ekernel_gated_delta_recurrent_f32",
+    "ekernel_paged_attention_bf16",
 ]
 
 DEFAULT_LIB = Path(__file__).resolve().parent / "lib" / "libecpu.so"
@@ -136,6 +137,21 @@ class EkernelW4A16SwiGLUDesc(ctypes.Structure):
     ]
 
 
+class EkernelPagedAttentionDesc(ctypes.Structure):
+    """ekernel_paged_attention_desc_t (no C counterpart: attention.py:95-139)."""
+    _fields_ = [
+        ("S", ctypes.c_size_t),
+        ("n_heads", ctypes.c_size_t),
+        ("n_kv_heads", ctypes.c_size_t),
+        ("head_dim", ctypes.c_size_t),
+        ("cache_len", ctypes.c_size_t),
+        ("block_size", ctypes.c_size_t),
+        ("num_blocks", ctypes.c_size_t),
+        ("n_block_ids", ctypes.c_size_t),
+        ("gate_stride", ctypes.c_size_t),
+    ]
+
+
 _LINEAR_ARGTYPES = [ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p,
                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
 
@@ -199,6 +215,10 @@ def _configure(lib):
         lib.eram_mmap.restype = ctypes.c_void_p
         lib.eram_munmap.argtypes = [ctypes.c_void_p]
         lib.eram_munmap.restype = ctypes.c_int
+    if hasattr(lib, "ekernel_paged_attention_bf16"):
+        lib.ekernel_paged_attention_bf16.argtypes = [ctypes.POINTER(EkernelPagedAttentionDesc)] + \
+            [ctypes.c_void_p] * 8
+        lib.ekernel_paged_attention_bf16.restype = ctypes.c_int
     if hasattr(lib, "ecpu_hip_set_stream"):
         lib.ecpu_hip_set_stream.argtypes = [ctypes.c_void_p]
         lib.ecpu_hip_set_stream.restype = ctypes.c_int
@@ -404,6 +424,21 @@ def swiglu_w4a16_bf16_ptr(x_ptr: int, gate_up_w_ptr: int, gate_up_scales_ptr: in
         ctypes.byref(desc), ctypes.c_void_p(x_ptr), ctypes.c_void_p(gate_up_w_ptr),
         ctypes.c_void_p(gate_up_scales_ptr), ctypes.c_void_p(down_w_ptr), ctypes.c_void_p(down_scales_ptr),
         ctypes.c_void_p(c_ptr), int(isa))
+
+
+def paged_attention_bf16_ptr(q_ptr: int, k_new_ptr: int, v_new_ptr: int, k_cache_ptr: int, v_cache_ptr: int,
+                             block_ids_ptr: int, gate_ptr: int, out_ptr: int, s: int, n_heads: int,
+                             n_kv_heads: int, head_dim: int, cache_len: int, block_size: int, num_blocks: int,
+                             n_block_ids: int, gate_stride: int) -> int:
+    """Paged attention of one sequence (ekernel_paged_attention_bf16); 0 for
+    k_cache_ptr / v_cache_ptr / gate_ptr means none.  Returns the C rc."""
+    lib = _load_lib()
+    if not hasattr(lib, "ekernel_paged_attention_bf16"):
+        raise RuntimeError("loaded eCPU library does not expose ekernel_paged_attention_bf16")
+    desc = EkernelPagedAttentionDesc(s, n_heads, n_kv_heads, head_dim, cache_len, block_size, num_blocks,
+                                     n_block_ids, gate_stride)
+    ptrs = [q_ptr, k_new_ptr, v_new_ptr, k_cache_ptr, v_cache_ptr, block_ids_ptr, gate_ptr, out_ptr]
+    return lib.ekernel_paged_attention_bf16(ctypes.byref(desc), *[ctypes.c_void_p(p or None) for p in ptrs])
 
 
 def eram_load_file(path: str, ranges) -> int:

@@ -1,0 +1,476 @@
+// Paged attention of one sequence on the GPU: the step FullAttention.forward
+// takes after q_norm / k_norm / rope (src/models/qwen3/attention.py:95-139)
+// over the block-paged cache of src/runtime/kvcache/physical_kv.py:11-81,
+// with the reference's roundings: bf16 scores of an fp32 dot product, a bf16
+// product with 1/sqrt(D), softmax in fp32, weights rounded to bf16, a bf16
+// P.V of fp32 sums, and the bf16 sigmoid gate.
+//
+// Two launches per group of query rows:
+//   attn_scores_kernel  grid (chunks of 256 positions, kv heads): lane =
+//       position; the position's key row (from the cache through the block
+//       table, or the step's own new rows, which it also writes into the
+//       cache) is dotted with every query row that reads this kv head (the
+//       heads of the GQA group x the step's tokens, held in LDS and read as
+//       broadcasts).  Scores go to scratch as bf16; each chunk also leaves
+//       its (max, sum of exp(score - max)) per row.
+//   attn_pv_kernel      same grid: every workgroup folds the chunk
+//       statistics into the row's max and sum (the same order in each, so
+//       the same values), forms the bf16 weights of its chunk, and
+//       accumulates P.V with lane = head-dim column (a wave reads one value
+//       row per instruction); waves meet in LDS in wave order, chunks in a
+//       global fold in chunk order by the last workgroup of the kv head (a
+//       ticket), which rounds, applies the gate and stores.
+// K and V are read once from HBM per kv head; that is the kernel's roofline.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <mutex>
+
+#include "gemv_device.h"
+#include "internal.h"
+
+namespace pilm {
+namespace {
+
+constexpr int kChunk = 256;    // positions per workgroup (one per thread of the score pass)
+constexpr int kMaxRows = 32;   // query rows per kv head and launch (heads of the group x tokens)
+
+struct AttnArgs {
+    const uint16_t *q;       // [S_total, H, D]
+    const uint16_t *k_new;   // [S_total, Hkv, D]
+    const uint16_t *v_new;
+    uint16_t *k_cache;       // [NB, BS, Hkv, D] or null
+    uint16_t *v_cache;
+    const int32_t *block_ids;
+    const uint16_t *gate;    // (s, h, d) at gate[(s * H + h) * gate_stride + d], or null
+    uint16_t *out;           // [S_total, H * D]
+    uint16_t *scores;        // [Hkv][RB][Lp] bf16
+    float *stats;            // [nchunk][Hkv][RB][2]: chunk max, chunk sum
+    float *part;             // [nchunk][Hkv][RB][D]: chunk P.V sums
+    int *tickets;            // [Hkv], zero between launches
+    int S;                   // query rows of this launch (R = S * rep)
+    int s0;                  // first of them within the step
+    int H, Hkv, rep;
+    int new0;                // position of the step's first new row: cache_len - S_total
+    int L;                   // positions this launch reads: new0 + s0 + S
+    int Lp;                  // L rounded up to whole chunks
+    int nchunk;
+    int BS, NB;
+    int write_cache;         // store this launch's rows (positions new0 + s0 ..) into the caches
+    int gate_stride;
+    float scale;             // (float)(1 / sqrt(D)), as the reference's Python float meets bf16
+};
+
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); }
+__device__ __forceinline__ float bf16_bits(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+
+// Row of position j of kv head kvh: the step's new rows come from its own K / V.
+template <int D>
+__device__ __forceinline__ const uint16_t *kv_row(const AttnArgs &a, const uint16_t *cache, const uint16_t *fresh,
+                                                  int j, int kvh) {
+    if (j >= a.new0) return fresh + ((size_t)(j - a.new0) * a.Hkv + kvh) * D;
+    const int b = min(max(a.block_ids[j / a.BS], 0), a.NB - 1);
+    return cache + (((size_t)b * a.BS + j % a.BS) * a.Hkv + kvh) * D;
+}
+
+template <int D>
+__device__ __forceinline__ uint16_t *cache_row(const AttnArgs &a, uint16_t *cache, int j, int kvh) {
+    const int b = min(max(a.block_ids[j / a.BS], 0), a.NB - 1);
+    return cache + (((size_t)b * a.BS + j % a.BS) * a.Hkv + kvh) * D;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+template <int D, int RB>
+__global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
+    __shared__ float qs[RB * D];
+    __shared__ float wmax[4][RB], wsum[4][RB], cmax[RB];
+    const int chunk = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int R = a.S * a.rep;
+    // query rows r = s * rep + i (head kvh * rep + i, token s0 + s) as fp32
+    for (int e = tid; e < RB * D; e += 256) {
+        const int r = e / D, d = e - r * D;
+        float v = 0.0f;
+        if (r < R) {
+            const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+            v = bf16_bits(a.q[((size_t)(a.s0 + s) * a.H + h) * D + d]);
+        }
+        qs[e] = v;
+    }
+    __syncthreads();
+
+    const int j = chunk * kChunk + tid;
+    const bool valid = j < a.L;
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
+    if (valid) {
+        const uint4 *kp = (const uint4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh);
+        uint4 *dst = (a.write_cache && j >= a.new0 + a.s0) ? (uint4 *)cache_row<D>(a, a.k_cache, j, kvh) : nullptr;
+#pragma unroll 2
+        for (int c = 0; c < D / 8; ++c) {
+            const uint4 kv = kp[c];
+            if (dst) dst[c] = kv;
+            const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float k0 = bf16_lo(w[t]), k1 = bf16_hi(w[t]);
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t], k0, acc[r]);
+                    acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t + 1], k1, acc[r]);
+                }
+            }
+        }
+    }
+    // attention.py:128-134: bf16 bmm output, times the scale in bf16, causal mask
+    float sc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const bool seen = valid && r < R && j <= a.new0 + a.s0 + r / a.rep;
+        sc[r] = seen ? bf16_round(bf16_round(acc[r]) * a.scale) : -__builtin_inff();
+        if (r < R) a.scores[((size_t)kvh * RB + r) * a.Lp + j] = f32_to_bf16(sc[r]);
+    }
+    // chunk statistics: max, then sum of exp(score - max)
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const float m = wave_max(sc[r]);
+        if (lane == 0) wmax[wave][r] = m;
+    }
+    __syncthreads();
+    if (tid < RB) cmax[tid] = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const float m = cmax[r];
+        const float e = sc[r] == -__builtin_inff() ? 0.0f : ref_expf(sc[r] - m);
+        const float l = wave_sum(e);
+        if (lane == 0) wsum[wave][r] = l;
+    }
+    __syncthreads();
+    if (tid < R) {
+        float *st = a.stats + (((size_t)chunk * a.Hkv + kvh) * RB + tid) * 2;
+        st[0] = cmax[tid];
+        st[1] = ((wsum[0][tid] + wsum[1][tid]) + wsum[2][tid]) + wsum[3][tid];
+    }
+}
+
+template <int D, int RB>
+constexpr size_t pv_lds_bytes() {
+    return ((size_t)RB * kChunk + 3 * (size_t)RB * D + 2 * RB) * sizeof(float);
+}
+
+template <int D, int RB>
+__global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
+    constexpr int E = D / 64;   // head-dim columns per lane
+    extern __shared__ float lds[];
+    float *p = lds;                       // [RB][kChunk] bf16 weights as fp32
+    float *red = p + RB * kChunk;         // [3][RB][D] sums of waves 1..3
+    float *gm = red + 3 * RB * D;         // [RB] row max
+    float *ginv = gm + RB;                // [RB] 1 / row sum
+    const int chunk = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int R = a.S * a.rep;
+    const float ninf = -__builtin_inff();
+
+    // The row's max and sum over every chunk, folded in chunk order.
+    if (tid < R) {
+        const float *st = a.stats + ((size_t)kvh * RB + tid) * 2;
+        const size_t cstride = (size_t)a.Hkv * RB * 2;
+        float m = ninf;
+        for (int c = 0; c < a.nchunk; ++c) m = fmaxf(m, st[c * cstride]);
+        float l = 0.0f;
+        for (int c = 0; c < a.nchunk; ++c) {
+            const float mc = st[c * cstride], lc = st[c * cstride + 1];
+            if (mc != ninf) l = l + lc * ref_expf(mc - m);
+        }
+        gm[tid] = m;
+        ginv[tid] = 1.0f / l;
+    }
+    __syncthreads();
+    // attention.py:136: softmax in fp32 (exp(x - max) * (1 / sum)), weights to bf16
+    for (int e = tid; e < RB * kChunk; e += 256) {
+        const int r = e / kChunk, t = e - r * kChunk;
+        float w = 0.0f;
+        if (r < R) {
+            const float s = bf16_bits(a.scores[((size_t)kvh * RB + r) * a.Lp + chunk * kChunk + t]);
+            if (s != ninf) w = bf16_round(ref_expf(s - gm[r]) * ginv[r]);
+        }
+        p[e] = w;
+    }
+    __syncthreads();
+
+    // attention.py:137: P.V, wave w over positions 64w .. 64w + 63 of the chunk
+    float acc[RB][E];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[r][e] = 0.0f;
+    const int t0 = wave * 64;
+    const int jn = min(64, a.L - (chunk * kChunk + t0));
+#pragma unroll 4
+    for (int t = 0; t < jn; ++t) {
+        const int j = chunk * kChunk + t0 + t;
+        const uint16_t *vr = kv_row<D>(a, a.v_cache, a.v_new, j, kvh) + E * lane;
+        float v[E];
+        if constexpr (E == 1) {
+            const uint16_t x = *vr;
+            v[0] = bf16_bits(x);
+            if (a.write_cache && j >= a.new0 + a.s0) cache_row<D>(a, a.v_cache, j, kvh)[lane] = x;
+        } else if constexpr (E == 2) {
+            const uint32_t x = *(const uint32_t *)vr;
+            v[0] = bf16_lo(x);
+            v[1] = bf16_hi(x);
+            if (a.write_cache && j >= a.new0 + a.s0) ((uint32_t *)cache_row<D>(a, a.v_cache, j, kvh))[lane] = x;
+        } else {
+            const uint2 x = *(const uint2 *)vr;
+            v[0] = bf16_lo(x.x);
+            v[1] = bf16_hi(x.x);
+            v[2] = bf16_lo(x.y);
+            v[3] = bf16_hi(x.y);
+            if (a.write_cache && j >= a.new0 + a.s0) ((uint2 *)cache_row<D>(a, a.v_cache, j, kvh))[lane] = x;
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const float w = p[r * kChunk + t0 + t];
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[r][e] = __builtin_fmaf(w, v[e], acc[r][e]);
+        }
+    }
+    if (wave != 0) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int e = 0; e < E; ++e) red[((wave - 1) * RB + r) * D + E * lane + e] = acc[r][e];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int d = E * lane + e;
+            acc[r][e] = ((acc[r][e] + red[r * D + d]) + red[(RB + r) * D + d]) + red[(2 * RB + r) * D + d];
+        }
+
+    auto store = [&](int r, int d, float x) {
+        // attention.py:137-139: bf16 P.V, rows (s, h), bf16(out * bf16(sigmoid(gate)))
+        const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+        const size_t row = (size_t)(a.s0 + s) * a.H + h;
+        uint16_t o = f32_to_bf16(x);
+        if (a.gate) {
+            const float g = bf16_bits(a.gate[row * a.gate_stride + d]);
+            const float sig = bf16_round(1.0f / (1.0f + ref_expf(-g)));
+            o = f32_to_bf16(bf16_bits(o) * sig);
+        }
+        a.out[row * D + d] = o;
+    };
+    if (a.nchunk == 1) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+            if (r < R)
+#pragma unroll
+                for (int e = 0; e < E; ++e) store(r, E * lane + e, acc[r][e]);
+        return;
+    }
+    // Chunk sums leave as agent-scope stores; once they have completed the
+    // wave takes the kv head's ticket, and the last chunk folds them all in
+    // chunk order with agent-scope loads.
+    float *mine = a.part + ((size_t)chunk * a.Hkv + kvh) * RB * D;
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+        if (r < R)
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                __hip_atomic_store(mine + r * D + E * lane + e, acc[r][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vmcnt<0>();
+    int ticket = 0;
+    if (lane == 0) ticket = __hip_atomic_fetch_add(a.tickets + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __builtin_amdgcn_readfirstlane(ticket);
+    if (ticket != a.nchunk - 1) return;
+    const size_t cstride = (size_t)a.Hkv * RB * D;
+    const float *base = a.part + (size_t)kvh * RB * D;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int d = E * lane + e;
+            float x = 0.0f;
+            for (int c = 0; c < a.nchunk; ++c)
+                x += __hip_atomic_load(base + c * cstride + r * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            store(r, d, x);
+        }
+    if (lane == 0) __hip_atomic_store(a.tickets + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int RB>
+int launch_attn(const AttnArgs &a, hipStream_t st) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_pv_kernel<D, RB>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)pv_lds_bytes<D, RB>());
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const dim3 grid((unsigned)a.nchunk, (unsigned)a.Hkv);
+    attn_scores_kernel<D, RB><<<grid, 256, 0, st>>>(a);
+    attn_pv_kernel<D, RB><<<grid, 256, pv_lds_bytes<D, RB>(), st>>>(a);
+    return ECPU_OK;
+}
+
+template <int D>
+int launch_attn_rb(int rb, const AttnArgs &a, hipStream_t st) {
+    switch (rb) {
+        case 1: return launch_attn<D, 1>(a, st);
+        case 2: return launch_attn<D, 2>(a, st);
+        case 4: return launch_attn<D, 4>(a, st);
+        case 8: return launch_attn<D, 8>(a, st);
+        case 16: return launch_attn<D, 16>(a, st);
+        default: return launch_attn<D, 32>(a, st);
+    }
+}
+
+}  // namespace
+
+int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t *q, const uint16_t *k_new,
+                        const uint16_t *v_new, uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids,
+                        const uint16_t *gate, uint16_t *out, hipStream_t st, const char *fn) {
+    const int S = (int)d->S, H = (int)d->n_heads, Hkv = (int)d->n_kv_heads, D = (int)d->head_dim;
+    const int rep = H / Hkv;
+    const int L_total = (int)d->cache_len;
+    // query rows per launch: the most tokens whose heads fit kMaxRows rows
+    const int per = std::max(1, std::min(S, kMaxRows / rep));
+    const int rb_full = per * rep <= 1 ? 1 : (per * rep <= 2 ? 2 : (per * rep <= 4 ? 4 : (per * rep <= 8 ? 8 : (per * rep <= 16 ? 16 : 32))));
+    const int Lp_max = (L_total + kChunk - 1) / kChunk * kChunk;
+    const int nchunk_max = Lp_max / kChunk;
+    const size_t score_floats = ((size_t)Hkv * rb_full * Lp_max * sizeof(uint16_t) + 3) / 4;
+    const size_t stat_floats = (size_t)nchunk_max * Hkv * rb_full * 2;
+    const size_t part_floats = (size_t)nchunk_max * Hkv * rb_full * D;
+    float *P = nullptr;
+    int *T = nullptr;
+    const size_t pad = 64;   // keep each region 256-byte aligned
+    const size_t off_stat = (score_floats + pad - 1) / pad * pad;
+    const size_t off_part = off_stat + (stat_floats + pad - 1) / pad * pad;
+    int rc = split_scratch(st, off_part + part_floats, (size_t)Hkv, &P, &T, fn);
+    if (rc != ECPU_OK) return rc;
+
+    AttnArgs a;
+    a.q = q;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.block_ids = block_ids;
+    a.gate = gate;
+    a.out = out;
+    a.scores = (uint16_t *)P;
+    a.stats = P + off_stat;
+    a.part = P + off_part;
+    a.tickets = T;
+    a.H = H;
+    a.Hkv = Hkv;
+    a.rep = rep;
+    a.new0 = L_total - S;
+    a.BS = k_cache ? (int)d->block_size : 1;
+    a.NB = k_cache ? (int)d->num_blocks : 1;
+    a.gate_stride = (int)d->gate_stride;
+    a.scale = (float)(1.0 / std::sqrt((double)D));
+    for (int s0 = 0; s0 < S; s0 += per) {
+        a.s0 = s0;
+        a.S = std::min(per, S - s0);
+        const int R = a.S * rep;
+        const int rb = R <= 1 ? 1 : (R <= 2 ? 2 : (R <= 4 ? 4 : (R <= 8 ? 8 : (R <= 16 ? 16 : 32))));
+        a.L = a.new0 + s0 + a.S;
+        a.Lp = (a.L + kChunk - 1) / kChunk * kChunk;
+        a.nchunk = a.Lp / kChunk;
+        a.write_cache = k_cache != nullptr ? 1 : 0;
+        // scores keep the first launch's row stride so the regions stay in bounds
+        if (rb > rb_full) return fail(ECPU_ERR_DEVICE, "%s: internal row bucket", fn);
+        switch (D) {
+            case 64: rc = launch_attn_rb<64>(rb, a, st); break;
+            case 128: rc = launch_attn_rb<128>(rb, a, st); break;
+            default: rc = launch_attn_rb<256>(rb, a, st); break;
+        }
+        if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the attention kernel failed", fn);
+        rc = check_launch(fn);
+        if (rc != ECPU_OK) return rc;
+    }
+    return ECPU_OK;
+}
+
+}  // namespace pilm
+
+using namespace pilm;
+
+namespace {
+
+int check_buf(const void *p, size_t bytes, const char *what, const char *fn) {
+    if (!p) return fail(ECPU_ERR_PARAM, "%s: %s is NULL", fn, what);
+    return check_device_buffer(p, bytes, what, fn);
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int ekernel_paged_attention_bf16(const ekernel_paged_attention_desc_t *desc, const uint16_t *q,
+                                            const uint16_t *k_new, const uint16_t *v_new, uint16_t *k_cache,
+                                            uint16_t *v_cache, const int32_t *block_ids, const uint16_t *gate,
+                                            uint16_t *out) {
+    static const char *fn = "ekernel_paged_attention_bf16";
+    if (!desc) return fail(ECPU_ERR_PARAM, "%s: desc is NULL", fn);
+    const size_t S = desc->S, H = desc->n_heads, Hkv = desc->n_kv_heads, D = desc->head_dim;
+    if (S == 0) return ECPU_OK;
+    if (H == 0 || Hkv == 0 || H % Hkv != 0)
+        return fail(ECPU_ERR_PARAM, "%s: n_heads (%zu) must be a positive multiple of n_kv_heads (%zu)", fn, H, Hkv);
+    if (H / Hkv > (size_t)kMaxRows)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: more than %d query heads per kv head", fn, kMaxRows);
+    if (D != 64 && D != 128 && D != 256) return fail(ECPU_ERR_UNSUPPORTED, "%s: head_dim %zu (64, 128 or 256)", fn, D);
+    const size_t L = desc->cache_len;
+    if (L < S) return fail(ECPU_ERR_PARAM, "%s: cache_len (%zu) is smaller than S (%zu)", fn, L, S);
+    if (L > (size_t)INT_MAX / 2 || S * H * D > (size_t)INT_MAX)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: sequence too long", fn);
+    if ((k_cache == nullptr) != (v_cache == nullptr))
+        return fail(ECPU_ERR_PARAM, "%s: k_cache and v_cache must both be given or both be NULL", fn);
+    int rc;
+    if ((rc = check_buf(q, S * H * D * 2, "q", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(k_new, S * Hkv * D * 2, "k_new", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(v_new, S * Hkv * D * 2, "v_new", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(out, S * H * D * 2, "out", fn)) != ECPU_OK) return rc;
+    if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new))
+        return fail(ECPU_ERR_PARAM, "%s: q, k_new and v_new must be 16-byte aligned", fn);
+    if (k_cache) {
+        const size_t BS = desc->block_size, NB = desc->num_blocks, nids = desc->n_block_ids;
+        if (BS == 0 || NB == 0) return fail(ECPU_ERR_PARAM, "%s: block_size and num_blocks must be positive", fn);
+        if (nids < (L + BS - 1) / BS)
+            return fail(ECPU_ERR_PARAM, "%s: %zu block ids cannot hold %zu positions of %zu per block", fn, nids, L, BS);
+        if (NB > (size_t)INT_MAX || BS > (size_t)INT_MAX) return fail(ECPU_ERR_UNSUPPORTED, "%s: cache too large", fn);
+        const size_t cache_bytes = NB * BS * Hkv * D * 2;
+        if ((rc = check_buf(k_cache, cache_bytes, "k_cache", fn)) != ECPU_OK) return rc;
+        if ((rc = check_buf(v_cache, cache_bytes, "v_cache", fn)) != ECPU_OK) return rc;
+        if ((rc = check_buf(block_ids, nids * 4, "block_ids", fn)) != ECPU_OK) return rc;
+        if (!aligned16(k_cache) || !aligned16(v_cache))
+            return fail(ECPU_ERR_PARAM, "%s: k_cache and v_cache must be 16-byte aligned", fn);
+    } else if (L != S) {
+        return fail(ECPU_ERR_PARAM, "%s: without a cache, cache_len (%zu) must equal S (%zu)", fn, L, S);
+    }
+    if (gate) {
+        const size_t gs = desc->gate_stride;
+        if (gs < D || gs > (size_t)INT_MAX) return fail(ECPU_ERR_PARAM, "%s: gate_stride %zu is below head_dim", fn, gs);
+        if ((rc = check_buf(gate, ((S * H - 1) * gs + D) * 2, "gate", fn)) != ECPU_OK) return rc;
+    }
+    return run_paged_attention(desc, q, k_new, v_new, k_cache, v_cache, block_ids, gate, out, current_stream(), fn);
+}

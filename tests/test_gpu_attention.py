@@ -1,0 +1,159 @@
+"""GPU parity of the paged attention kernels against the attention oracle.
+
+Calls go through the C ABI (pilm_amd.attention -> ctypes ->
+ekernel_paged_attention_bf16).  The oracle runs the reference's torch CPU
+operations; the kernels reproduce its roundings (bf16 scores, bf16 scaled
+scores, fp32 softmax, bf16 weights, bf16 P.V, bf16 gate) but not its fp32
+summation orders or its exp, so a score or weight that falls next to a bf16
+rounding boundary can land one bf16 step away.  Tolerance, per call: at
+least 97 % of the outputs bit-identical, and every output within 2e-2 of
+the oracle's largest output magnitude (a wrong mask, scale, head mapping or
+block lookup moves outputs by far more).  The caches after the call must
+hold the oracle's rows exactly (the new rows are copies).
+"""
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from oracle import attention as OA
+from pilm_amd import attention as A
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _bf(x) -> torch.Tensor:
+    return torch.as_tensor(x, dtype=torch.float32).to(torch.bfloat16)
+
+
+def _inputs(seed, S, H, Hkv, D, L, BS, cache=True, gate="none"):
+    g = torch.Generator().manual_seed(seed)
+    q = _bf(torch.randn(S, H, D, generator=g))
+    k_new = _bf(torch.randn(S, Hkv, D, generator=g))
+    v_new = _bf(torch.randn(S, Hkv, D, generator=g))
+    kc = vc = ids = None
+    if cache:
+        nblk = (L + BS - 1) // BS
+        NB = nblk + 5
+        kc = _bf(torch.randn(NB, BS, Hkv, D, generator=g))
+        vc = _bf(torch.randn(NB, BS, Hkv, D, generator=g))
+        ids = torch.randperm(NB, generator=g)[:nblk].tolist()
+    qg = None
+    if gate != "none":
+        qg = _bf(torch.randn(S, H, 2 * D, generator=g))   # q_proj's output: query | gate per head
+    return q, k_new, v_new, kc, vc, ids, qg
+
+
+def _run_both(dev, S, H, Hkv, D, L, BS=16, cache=True, gate="none", seed=0):
+    q, k_new, v_new, kc, vc, ids, qg = _inputs(seed, S, H, Hkv, D, L, BS, cache, gate)
+    gate_cpu = qg[:, :, D:] if qg is not None else None
+    ref_kc = kc.clone() if kc is not None else None
+    ref_vc = vc.clone() if vc is not None else None
+    ref = OA.paged_attention(q, k_new, v_new, ref_kc, ref_vc, ids, L if cache else None, gate_cpu)
+    gk = kc.to(dev) if kc is not None else None
+    gv = vc.to(dev) if vc is not None else None
+    g_gate = None
+    if qg is not None:
+        qg_dev = qg.to(dev)
+        g_gate = qg_dev[:, :, D:] if gate == "strided" else qg_dev[:, :, D:].contiguous()
+    out = A.paged_attention(q.to(dev), k_new.to(dev), v_new.to(dev), gk, gv, ids, L if cache else None, g_gate)
+    torch.cuda.synchronize()
+    if cache:
+        assert torch.equal(gk.cpu(), ref_kc), "k_cache differs from the oracle's after the call"
+        assert torch.equal(gv.cpu(), ref_vc), "v_cache differs from the oracle's after the call"
+    return out.cpu(), ref
+
+
+def _check(out, ref, what):
+    assert out.shape == ref.shape, what
+    o, r = out.float(), ref.float()
+    same = (out.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
+    err = (o - r).abs().max().item()
+    bound = 2e-2 * r.abs().max().item()
+    assert err <= bound, f"{what}: max error {err} above {bound} (identical {same:.4f})"
+    assert same >= 0.97, f"{what}: only {same:.4f} of the outputs bit-identical (max error {err})"
+
+
+# (S, H, Hkv, D, L, block_size, gate): decode at the Qwen3-1.7B / 8B head
+# layouts and around the 256-position chunks, MTP verify rows, more rows
+# than one launch holds, other head sizes and GQA ratios.
+CASES = [
+    (1, 16, 8, 128, 1, 16, "none"), (1, 16, 8, 128, 2, 16, "strided"), (1, 16, 8, 128, 255, 16, "none"),
+    (1, 16, 8, 128, 256, 16, "contiguous"), (1, 16, 8, 128, 257, 16, "strided"),
+    (1, 16, 8, 128, 384, 16, "strided"), (1, 32, 8, 128, 1000, 16, "strided"),
+    (1, 32, 8, 128, 4097, 64, "none"), (4, 16, 8, 128, 517, 16, "strided"), (5, 32, 8, 128, 600, 16, "strided"),
+    (20, 16, 8, 128, 300, 16, "strided"), (9, 32, 8, 128, 40, 16, "none"), (3, 8, 1, 128, 77, 8, "contiguous"),
+    (2, 4, 4, 64, 129, 1, "strided"), (3, 8, 2, 256, 270, 32, "strided"), (1, 64, 2, 128, 33, 16, "none"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "S{}_H{}_kv{}_D{}_L{}_bs{}_{}".format(*c))
+def test_paged_attention_against_oracle(case, dev):
+    S, H, Hkv, D, L, BS, gate = case
+    _say(f"[gpu] attention {case}")
+    out, ref = _run_both(dev, S, H, Hkv, D, L, BS, True, gate, seed=S * 100003 + L)
+    _check(out, ref, str(case))
+
+
+@pytest.mark.parametrize("S,H,Hkv,D", [(1, 16, 8, 128), (33, 16, 8, 128), (7, 32, 8, 64)])
+def test_no_cache_prefill(S, H, Hkv, D, dev):
+    """attention.py:115-116: the rows attend to each other only (causal)."""
+    _say(f"[gpu] attention no cache S={S} H={H} kv={Hkv} D={D}")
+    out, ref = _run_both(dev, S, H, Hkv, D, S, cache=False, gate="strided", seed=S)
+    _check(out, ref, f"no cache S={S}")
+
+
+def test_long_context_8b_heads(dev):
+    """32768 positions (128 chunks per kv head, the ticket fold over all of
+    them) at the Qwen3-8B head layout."""
+    _say("[gpu] attention L=32768")
+    out, ref = _run_both(dev, 1, 32, 8, 128, 32768, 16, True, "strided", seed=11)
+    _check(out, ref, "L=32768")
+
+
+def test_repeat_calls_identical(dev):
+    """Tickets are reset by the last workgroup: the same call twice gives the same bits."""
+    q, k_new, v_new, kc, vc, ids, qg = _inputs(3, 4, 16, 8, 128, 1500, 16, True, "strided")
+    args = [t.to(dev) for t in (q, k_new, v_new, kc, vc)]
+    gate = qg.to(dev)[:, :, 128:]
+    o1 = A.paged_attention(*args, ids, 1500, gate)
+    o2 = A.paged_attention(*args, ids, 1500, gate)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+def test_paged_kv_cache_class(dev):
+    """PagedKVCache.write / read_seq / attend against the oracle's cache."""
+    S, H, Hkv, D, L, BS = 2, 16, 8, 128, 50, 16
+    q, k_new, v_new, kc, vc, ids, _ = _inputs(5, S, H, Hkv, D, L, BS)
+    cache = A.PagedKVCache(1, kc.shape[0], BS, Hkv, D, device=dev)
+    cache.k_cache[0].copy_(kc.to(dev))
+    cache.v_cache[0].copy_(vc.to(dev))
+    out = cache.attend(0, ids, L, q.to(dev), k_new.to(dev), v_new.to(dev))
+    ref = OA.paged_attention(q, k_new, v_new, kc, vc, ids, L)
+    _check(out.cpu(), ref, "PagedKVCache.attend")
+    k, v = cache.read_seq(0, ids[: (L + BS - 1) // BS], L)
+    rk, rv = OA.read_seq(kc, vc, ids[: (L + BS - 1) // BS], L)
+    assert torch.equal(k.cpu(), rk) and torch.equal(v.cpu(), rv)
+    cache.write(0, [ids[0]], [3], k_new[:1].to(dev), v_new[:1].to(dev))
+    assert torch.equal(cache.k_cache[0][ids[0], 3].cpu(), k_new[0])
+
+
+def test_rejected_arguments(dev):
+    q, k_new, v_new, kc, vc, ids, _ = _inputs(1, 2, 16, 8, 128, 40, 16)
+    gq, gk, gv, gkc, gvc = (t.to(dev) for t in (q, k_new, v_new, kc, vc))
+    with pytest.raises(ValueError):
+        A.paged_attention(q, k_new, v_new)                      # host tensors
+    with pytest.raises(RuntimeError):
+        A.paged_attention(gq, gk, gv, gkc, gvc, ids, 1)         # cache_len < S
+    with pytest.raises(RuntimeError):
+        A.paged_attention(gq, gk, gv, gkc, gvc, ids[:1], 40)    # too few block ids
+    with pytest.raises(RuntimeError):
+        A.paged_attention(gq, gk, gv, None, None, None, 40)     # no cache needs cache_len == S
