@@ -28,6 +28,7 @@
 #include <cmath>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "gemv_device.h"
 #include "internal.h"
@@ -49,8 +50,9 @@ struct AttnArgs {
     uint16_t *out;           // [S_total, H * D]
     uint16_t *scores;        // [Hkv][RB][Lp] bf16
     float *stats;            // [nchunk][Hkv][RB][2]: chunk max, chunk sum
-    float *part;             // [nchunk][Hkv][RB][D]: chunk P.V sums
-    int *tickets;            // [Hkv], zero between launches
+    float *gstat;            // [Hkv][RB][2]: row max, 1 / row sum
+    float *part;             // [ngroups][Hkv][RB][D]: P.V sums of each group of chunks
+    int *tickets;            // [2 * Hkv], zero between launches (P.V fold, statistics fold)
     int S;                   // query rows of this launch (R = S * rep)
     int s0;                  // first of them within the step
     int H, Hkv, rep;
@@ -58,11 +60,28 @@ struct AttnArgs {
     int L;                   // positions this launch reads: new0 + s0 + S
     int Lp;                  // L rounded up to whole chunks
     int nchunk;
+    int fold_in_pv;          // few chunks: every P.V wave folds the chunk statistics itself
+    int cpw;                 // chunks per P.V workgroup
+    int ngroups;             // P.V workgroups per kv head: ceil(nchunk / cpw)
     int BS, NB;
     int write_cache;         // store this launch's rows (positions new0 + s0 ..) into the caches
     int gate_stride;
     float scale;             // (float)(1 / sqrt(D)), as the reference's Python float meets bf16
 };
+
+// Global-memory views of the row pointers: loads through them are global_load
+// (vector memory counter only), not flat loads, which would also hold up
+// every LDS wait behind them.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *gbl(const T *p) {
+    return (const __attribute__((address_space(1))) T *)p;
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *gbl_w(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
 
 __device__ __forceinline__ float bf16_round(float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); }
 __device__ __forceinline__ float bf16_bits(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
@@ -82,6 +101,12 @@ __device__ __forceinline__ uint16_t *cache_row(const AttnArgs &a, uint16_t *cach
     return cache + (((size_t)b * a.BS + j % a.BS) * a.Hkv + kvh) * D;
 }
 
+// exp for the softmax and the gate: the device library's single-precision
+// exp (ALU only, within 1 ulp).  The reference's is torch's vectorized CPU
+// exp, not a correctly rounded one either; either way the weights are then
+// rounded to bf16.
+__device__ __forceinline__ float att_exp(float x) { return expf(x); }
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
@@ -98,6 +123,7 @@ template <int D, int RB>
 __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     __shared__ float qs[RB * D];
     __shared__ float wmax[4][RB], wsum[4][RB], cmax[RB];
+    __shared__ int last;
     const int chunk = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int R = a.S * a.rep;
@@ -119,11 +145,11 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
     if (valid) {
-        const uint4 *kp = (const uint4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh);
-        uint4 *dst = (a.write_cache && j >= a.new0 + a.s0) ? (uint4 *)cache_row<D>(a, a.k_cache, j, kvh) : nullptr;
+        const auto *kp = gbl((const u32x4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh));
+        auto *dst = (a.write_cache && j >= a.new0 + a.s0) ? gbl_w((u32x4 *)cache_row<D>(a, a.k_cache, j, kvh)) : nullptr;
 #pragma unroll 2
         for (int c = 0; c < D / 8; ++c) {
-            const uint4 kv = kp[c];
+            const u32x4 kv = kp[c];
             if (dst) dst[c] = kv;
             const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
@@ -157,99 +183,188 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
         const float m = cmax[r];
-        const float e = sc[r] == -__builtin_inff() ? 0.0f : ref_expf(sc[r] - m);
+        const float e = sc[r] == -__builtin_inff() ? 0.0f : att_exp(sc[r] - m);
         const float l = wave_sum(e);
         if (lane == 0) wsum[wave][r] = l;
     }
     __syncthreads();
+    if (a.fold_in_pv) {
+        if (tid < R) {
+            float *st = a.stats + (((size_t)chunk * a.Hkv + kvh) * RB + tid) * 2;
+            st[0] = cmax[tid];
+            st[1] = ((wsum[0][tid] + wsum[1][tid]) + wsum[2][tid]) + wsum[3][tid];
+        }
+        return;
+    }
+    // The chunk statistics leave as agent-scope stores; the last chunk of
+    // the kv head (ticket) folds them into the row's max and 1 / sum: wave w
+    // takes rows w, w + 4, ..; lane c chunks c, c + 64, .. in order, then the
+    // lanes meet in a fixed butterfly.
     if (tid < R) {
         float *st = a.stats + (((size_t)chunk * a.Hkv + kvh) * RB + tid) * 2;
-        st[0] = cmax[tid];
-        st[1] = ((wsum[0][tid] + wsum[1][tid]) + wsum[2][tid]) + wsum[3][tid];
+        __hip_atomic_store(st, cmax[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(st + 1, ((wsum[0][tid] + wsum[1][tid]) + wsum[2][tid]) + wsum[3][tid], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(a.tickets + a.Hkv + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               a.nchunk - 1;
+    __syncthreads();
+    if (!last) return;
+    const size_t cstride = (size_t)a.Hkv * RB * 2;
+    for (int r = wave; r < R; r += 4) {
+        const float *st = a.stats + ((size_t)kvh * RB + r) * 2;
+        float m = -__builtin_inff();
+        for (int c = lane; c < a.nchunk; c += 64)
+            m = fmaxf(m, __hip_atomic_load(st + c * cstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int c = lane; c < a.nchunk; c += 64) {
+            const float mc = __hip_atomic_load(st + c * cstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float lc = __hip_atomic_load(st + c * cstride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (mc != -__builtin_inff()) l = l + lc * att_exp(mc - m);
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            float *gs = a.gstat + ((size_t)kvh * RB + r) * 2;
+            gs[0] = m;
+            gs[1] = 1.0f / l;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(a.tickets + a.Hkv + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int RB>
 constexpr size_t pv_lds_bytes() {
-    return ((size_t)RB * kChunk + 3 * (size_t)RB * D + 2 * RB) * sizeof(float);
+    return ((size_t)RB * kChunk + 3 * (size_t)RB * D + 4 * 2 * RB) * sizeof(float);
 }
 
 template <int D, int RB>
 __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
-    constexpr int E = D / 64;   // head-dim columns per lane
+    constexpr int E = D / 64;                 // head-dim columns per lane
+    constexpr int kBatch = E == 4 ? 32 : 64;  // value rows in flight per wave
     extern __shared__ float lds[];
-    float *p = lds;                       // [RB][kChunk] bf16 weights as fp32
-    float *red = p + RB * kChunk;         // [3][RB][D] sums of waves 1..3
-    float *gm = red + 3 * RB * D;         // [RB] row max
-    float *ginv = gm + RB;                // [RB] 1 / row sum
-    const int chunk = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    float *p = lds;                           // [RB][kChunk] bf16 weights as fp32 (wave w: columns 64w..)
+    float *red = p + RB * kChunk;             // [3][RB][D] sums of waves 1..3
+    const int grp = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    float *gm = red + 3 * RB * D + wave * 2 * RB;   // [RB] row max, then [RB] 1 / row sum (per wave)
+    float *ginv = gm + RB;
     const int R = a.S * a.rep;
     const float ninf = -__builtin_inff();
-
-    // The row's max and sum over every chunk, folded in chunk order.
-    if (tid < R) {
-        const float *st = a.stats + ((size_t)kvh * RB + tid) * 2;
-        const size_t cstride = (size_t)a.Hkv * RB * 2;
-        float m = ninf;
-        for (int c = 0; c < a.nchunk; ++c) m = fmaxf(m, st[c * cstride]);
-        float l = 0.0f;
-        for (int c = 0; c < a.nchunk; ++c) {
-            const float mc = st[c * cstride], lc = st[c * cstride + 1];
-            if (mc != ninf) l = l + lc * ref_expf(mc - m);
+    const int t0 = wave * 64;
+    if (lane < R) {
+        if (a.fold_in_pv) {
+            // (up to 8 chunks: the row's max and sum folded here, in chunk order)
+            const float *st = a.stats + ((size_t)kvh * RB + lane) * 2;
+            const size_t cstride = (size_t)a.Hkv * RB * 2;
+            float mc[8], lc[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                mc[c] = c < a.nchunk ? st[c * cstride] : ninf;
+                lc[c] = c < a.nchunk ? st[c * cstride + 1] : 0.0f;
+            }
+            float m = ninf;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) m = fmaxf(m, mc[c]);
+            float l = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                if (mc[c] != ninf) l = l + lc[c] * att_exp(mc[c] - m);
+            gm[lane] = m;
+            ginv[lane] = 1.0f / l;
+        } else {
+            const float *gs = a.gstat + ((size_t)kvh * RB + lane) * 2;
+            gm[lane] = gs[0];
+            ginv[lane] = gs[1];
         }
-        gm[tid] = m;
-        ginv[tid] = 1.0f / l;
     }
-    __syncthreads();
-    // attention.py:136: softmax in fp32 (exp(x - max) * (1 / sum)), weights to bf16
-    for (int e = tid; e < RB * kChunk; e += 256) {
-        const int r = e / kChunk, t = e - r * kChunk;
-        float w = 0.0f;
-        if (r < R) {
-            const float s = bf16_bits(a.scores[((size_t)kvh * RB + r) * a.Lp + chunk * kChunk + t]);
-            if (s != ninf) w = bf16_round(ref_expf(s - gm[r]) * ginv[r]);
-        }
-        p[e] = w;
-    }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();   // (LDS is in order within the wave; keep the compiler from reordering)
 
-    // attention.py:137: P.V, wave w over positions 64w .. 64w + 63 of the chunk
+    // Each wave works alone until the waves' sums meet.  Per chunk of the
+    // group: lane l looks up the value row of position t0 + l (storing this
+    // launch's new rows into the cache), the wave's value loads go out, lane
+    // l forms that position's weights, then the FMAs run in position order.
     float acc[RB][E];
 #pragma unroll
     for (int r = 0; r < RB; ++r)
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[r][e] = 0.0f;
-    const int t0 = wave * 64;
-    const int jn = min(64, a.L - (chunk * kChunk + t0));
-#pragma unroll 4
-    for (int t = 0; t < jn; ++t) {
-        const int j = chunk * kChunk + t0 + t;
-        const uint16_t *vr = kv_row<D>(a, a.v_cache, a.v_new, j, kvh) + E * lane;
-        float v[E];
-        if constexpr (E == 1) {
-            const uint16_t x = *vr;
-            v[0] = bf16_bits(x);
-            if (a.write_cache && j >= a.new0 + a.s0) cache_row<D>(a, a.v_cache, j, kvh)[lane] = x;
-        } else if constexpr (E == 2) {
-            const uint32_t x = *(const uint32_t *)vr;
-            v[0] = bf16_lo(x);
-            v[1] = bf16_hi(x);
-            if (a.write_cache && j >= a.new0 + a.s0) ((uint32_t *)cache_row<D>(a, a.v_cache, j, kvh))[lane] = x;
-        } else {
-            const uint2 x = *(const uint2 *)vr;
-            v[0] = bf16_lo(x.x);
-            v[1] = bf16_hi(x.x);
-            v[2] = bf16_lo(x.y);
-            v[3] = bf16_hi(x.y);
-            if (a.write_cache && j >= a.new0 + a.s0) ((uint2 *)cache_row<D>(a, a.v_cache, j, kvh))[lane] = x;
+    uint64_t myrow_bits = 0;
+    int jn = 0;
+    // lane t's row pointer as a wave-uniform value (v_readlane: no LDS trip)
+    auto row_of = [&](int t) -> const uint16_t * {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)myrow_bits, t);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(myrow_bits >> 32), t);
+        return (const uint16_t *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+    };
+    // raw value words, unpacked at their FMAs (unpacking at the load would
+    // make the compiler wait for each load in turn)
+    typedef std::conditional_t<E == 1, uint16_t, std::conditional_t<E == 2, uint32_t, u32x2>> Raw;
+    Raw raw[kBatch];
+    auto load_batch = [&](int tb) {
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            // every lane's row is a valid one (positions past the end read
+            // the last position's); their weights are zero and their values dropped
+            raw[u] = *gbl((const Raw *)(row_of(tb + u) + E * lane));
         }
+    };
+    auto value = [&](int tb, int u, float (&v)[E]) {
+        const bool in = tb + u < jn;
+        if constexpr (E == 1) {
+            v[0] = in ? bf16_bits(raw[u]) : 0.0f;
+        } else if constexpr (E == 2) {
+            v[0] = in ? bf16_lo(raw[u]) : 0.0f;
+            v[1] = in ? bf16_hi(raw[u]) : 0.0f;
+        } else {
+            v[0] = in ? bf16_lo(raw[u].x) : 0.0f;
+            v[1] = in ? bf16_hi(raw[u].x) : 0.0f;
+            v[2] = in ? bf16_lo(raw[u].y) : 0.0f;
+            v[3] = in ? bf16_hi(raw[u].y) : 0.0f;
+        }
+    };
+    const int c_end = min(a.nchunk, (grp + 1) * a.cpw);
+    for (int chunk = grp * a.cpw; chunk < c_end; ++chunk) {
+        jn = min(64, a.L - (chunk * kChunk + t0));   // this wave's positions (may be <= 0)
+        const int jl = chunk * kChunk + t0 + lane;
+        const uint16_t *myrow = kv_row<D>(a, a.v_cache, a.v_new, min(jl, a.L - 1), kvh);
+        if (jl < a.L && a.write_cache && jl >= a.new0 + a.s0) {
+            auto *dst = gbl_w((u32x4 *)cache_row<D>(a, a.v_cache, jl, kvh));
+#pragma unroll 4
+            for (int c = 0; c < D / 8; ++c) dst[c] = gbl((const u32x4 *)myrow)[c];
+        }
+        myrow_bits = (uint64_t)(uintptr_t)myrow;
+        if (jn > 0) load_batch(0);
+        // attention.py:136: softmax in fp32 (exp(x - max) * (1 / sum)), weights to bf16
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const float w = p[r * kChunk + t0 + t];
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[r][e] = __builtin_fmaf(w, v[e], acc[r][e]);
+            float w = 0.0f;
+            if (r < R) {
+                const float sc = bf16_bits(a.scores[((size_t)kvh * RB + r) * a.Lp + chunk * kChunk + t0 + lane]);
+                if (sc != ninf) w = bf16_round(att_exp(sc - gm[r]) * ginv[r]);
+            }
+            p[r * kChunk + t0 + lane] = w;
         }
+        __builtin_amdgcn_wave_barrier();
+        // attention.py:137: P.V over the wave's positions in order
+        for (int tb = 0; tb < jn; tb += kBatch) {
+            if (tb > 0) load_batch(tb);
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                float v[E];
+                value(tb, u, v);
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const float w = p[r * kChunk + t0 + tb + u];
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[r][e] = __builtin_fmaf(w, v[e], acc[r][e]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();   // (the next chunk's weights reuse the wave's columns)
     }
     if (wave != 0) {
 #pragma unroll
@@ -274,12 +389,12 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
         uint16_t o = f32_to_bf16(x);
         if (a.gate) {
             const float g = bf16_bits(a.gate[row * a.gate_stride + d]);
-            const float sig = bf16_round(1.0f / (1.0f + ref_expf(-g)));
+            const float sig = bf16_round(1.0f / (1.0f + att_exp(-g)));
             o = f32_to_bf16(bf16_bits(o) * sig);
         }
         a.out[row * D + d] = o;
     };
-    if (a.nchunk == 1) {
+    if (a.ngroups == 1) {
 #pragma unroll
         for (int r = 0; r < RB; ++r)
             if (r < R)
@@ -287,10 +402,10 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
                 for (int e = 0; e < E; ++e) store(r, E * lane + e, acc[r][e]);
         return;
     }
-    // Chunk sums leave as agent-scope stores; once they have completed the
-    // wave takes the kv head's ticket, and the last chunk folds them all in
-    // chunk order with agent-scope loads.
-    float *mine = a.part + ((size_t)chunk * a.Hkv + kvh) * RB * D;
+    // Group sums leave as agent-scope stores; once they have completed the
+    // wave takes the kv head's ticket, and the last group folds them all in
+    // group order with agent-scope loads.
+    float *mine = a.part + ((size_t)grp * a.Hkv + kvh) * RB * D;
 #pragma unroll
     for (int r = 0; r < RB; ++r)
         if (r < R)
@@ -301,16 +416,26 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     int ticket = 0;
     if (lane == 0) ticket = __hip_atomic_fetch_add(a.tickets + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ticket = __builtin_amdgcn_readfirstlane(ticket);
-    if (ticket != a.nchunk - 1) return;
-    const size_t cstride = (size_t)a.Hkv * RB * D;
+    if (ticket != a.ngroups - 1) return;
+    const size_t gstride = (size_t)a.Hkv * RB * D;
     const float *base = a.part + (size_t)kvh * RB * D;
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int d = E * lane + e;
+            // group sums in group order, loaded 16 at a time
             float x = 0.0f;
-            for (int c = 0; c < a.nchunk; ++c)
-                x += __hip_atomic_load(base + c * cstride + r * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int g0 = 0; g0 < a.ngroups; g0 += 16) {
+                float y[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    y[u] = g0 + u < a.ngroups ? __hip_atomic_load(base + (g0 + u) * gstride + r * D + d,
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                              : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (g0 + u < a.ngroups) x += y[u];
+            }
             store(r, d, x);
         }
     if (lane == 0) __hip_atomic_store(a.tickets + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -325,9 +450,8 @@ int launch_attn(const AttnArgs &a, hipStream_t st) {
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)pv_lds_bytes<D, RB>());
     });
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
-    const dim3 grid((unsigned)a.nchunk, (unsigned)a.Hkv);
-    attn_scores_kernel<D, RB><<<grid, 256, 0, st>>>(a);
-    attn_pv_kernel<D, RB><<<grid, 256, pv_lds_bytes<D, RB>(), st>>>(a);
+    attn_scores_kernel<D, RB><<<dim3((unsigned)a.nchunk, (unsigned)a.Hkv), 256, 0, st>>>(a);
+    attn_pv_kernel<D, RB><<<dim3((unsigned)a.ngroups, (unsigned)a.Hkv), 256, pv_lds_bytes<D, RB>(), st>>>(a);
     return ECPU_OK;
 }
 
@@ -363,8 +487,9 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
     int *T = nullptr;
     const size_t pad = 64;   // keep each region 256-byte aligned
     const size_t off_stat = (score_floats + pad - 1) / pad * pad;
-    const size_t off_part = off_stat + (stat_floats + pad - 1) / pad * pad;
-    int rc = split_scratch(st, off_part + part_floats, (size_t)Hkv, &P, &T, fn);
+    const size_t off_gstat = off_stat + (stat_floats + pad - 1) / pad * pad;
+    const size_t off_part = off_gstat + ((size_t)Hkv * rb_full * 2 + pad - 1) / pad * pad;
+    int rc = split_scratch(st, off_part + part_floats, 2 * (size_t)Hkv, &P, &T, fn);
     if (rc != ECPU_OK) return rc;
 
     AttnArgs a;
@@ -378,6 +503,7 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
     a.out = out;
     a.scores = (uint16_t *)P;
     a.stats = P + off_stat;
+    a.gstat = P + off_gstat;
     a.part = P + off_part;
     a.tickets = T;
     a.H = H;
@@ -396,6 +522,13 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
         a.L = a.new0 + s0 + a.S;
         a.Lp = (a.L + kChunk - 1) / kChunk * kChunk;
         a.nchunk = a.Lp / kChunk;
+        // The score pass folds the chunk statistics once beyond 8 chunks (a
+        // ticket); below, each P.V wave reads them all.  At most 64 P.V
+        // workgroups per kv head keep the final fold short; up to 3 chunks
+        // go to one workgroup, which needs no fold at all.
+        a.fold_in_pv = a.nchunk <= 8 ? 1 : 0;
+        a.cpw = a.nchunk <= 3 ? a.nchunk : (a.nchunk + 63) / 64;
+        a.ngroups = (a.nchunk + a.cpw - 1) / a.cpw;
         a.write_cache = k_cache != nullptr ? 1 : 0;
         // scores keep the first launch's row stride so the regions stay in bounds
         if (rb > rb_full) return fail(ECPU_ERR_DEVICE, "%s: internal row bucket", fn);

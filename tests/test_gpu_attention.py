@@ -6,9 +6,10 @@ operations; the kernels reproduce its roundings (bf16 scores, bf16 scaled
 scores, fp32 softmax, bf16 weights, bf16 P.V, bf16 gate) but not its fp32
 summation orders or its exp, so a score or weight that falls next to a bf16
 rounding boundary can land one bf16 step away.  Tolerance, per call: at
-least 97 % of the outputs bit-identical, and every output within 2e-2 of
-the oracle's largest output magnitude (a wrong mask, scale, head mapping or
-block lookup moves outputs by far more).  The caches after the call must
+least 98 % of the outputs bit-identical, and every output within 1e-2 of
+the oracle's largest output magnitude (measured: >= 99 % identical, largest
+error 0.23 % of it; a wrong mask, scale, head mapping or block lookup moves
+outputs by far more).  The caches after the call must
 hold the oracle's rows exactly (the new rows are copies).
 """
 from __future__ import annotations
@@ -76,9 +77,9 @@ def _check(out, ref, what):
     o, r = out.float(), ref.float()
     same = (out.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
     err = (o - r).abs().max().item()
-    bound = 2e-2 * r.abs().max().item()
+    bound = 1e-2 * r.abs().max().item()
     assert err <= bound, f"{what}: max error {err} above {bound} (identical {same:.4f})"
-    assert same >= 0.97, f"{what}: only {same:.4f} of the outputs bit-identical (max error {err})"
+    assert same >= 0.98, f"{what}: only {same:.4f} of the outputs bit-identical (max error {err})"
 
 
 # (S, H, Hkv, D, L, block_size, gate): decode at the Qwen3-1.7B / 8B head
