@@ -24,7 +24,8 @@ Printed JSON line:
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
   sweep        per-shape times with --sweep [sections]: g128 (default),
-               w4row, w8a32, w8a16, gemm, fused, load (bundle -> HBM), or all
+               w4row, w8a32, w8a16, gemm, fused, attention, load (bundle ->
+               HBM), or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -256,6 +257,8 @@ def sweep(torch, dev, sections) -> dict:
       gemm   prefill / verify at the 8B shapes, W8A32 and W4A16 g128,
              M = 64, 256, 1024, 2048 (matrix cores; TFLOP/s)
       fused  W4 SwiGLU MLP and W8A16 lm_head argmax vs their unfused calls
+      attention  paged attention of one sequence (decode and MTP verify) at
+             the 1.7B and 8B head layouts, 384 .. 131072 positions (K+V GB/s)
       load   a 1.7B W4 bundle uploaded to HBM (GB/s)."""
     res = {}
     if "g128" in sections:
@@ -277,6 +280,8 @@ def sweep(torch, dev, sections) -> dict:
                           for fmt in ("w8a32", "w4g128") for name, n, k in SHAPES_8B if name != "lm_head"}
     if "fused" in sections:
         res["fused"] = sweep_fused(torch, dev)
+    if "attention" in sections:
+        res["attention"] = sweep_attention(torch, dev)
     if "load" in sections:
         res["load"] = sweep_load(torch, dev)
     return res
@@ -322,6 +327,51 @@ def sweep_load(torch, dev) -> dict:
                 "note": "page-cache resident files -> pinned staging -> HBM (PCIe); not part of value"}
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
+
+
+def sweep_attention(torch, dev) -> dict:
+    """ekernel_paged_attention_bf16 for one sequence: S new rows (1 = decode,
+    5 / 4 = MTP verify with 4 / 3 drafts) over L cached positions in 16-token
+    blocks, gate from q_proj's output.  Enough distinct caches (>= 512 MB)
+    that K and V stream from HBM; GB/s counts K and V once (the kernels'
+    bound: 2 * L * n_kv_heads * head_dim * 2 bytes)."""
+    from pilm_amd import bindings as abi
+    out = {}
+    bs, d = 16, 128
+    cases = [("qwen3_1p7b", 16, 8, 1, L) for L in (384, 4096, 32768)] + \
+            [("qwen3_8b", 32, 8, 1, L) for L in (384, 4096, 32768, 131072)] + \
+            [("qwen3_1p7b", 16, 8, 4, 4096), ("qwen3_8b", 32, 8, 5, 4096)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    for model, h, hkv, s_rows, L in cases:
+        nblk = (L + bs - 1) // bs
+        per = 2 * nblk * bs * hkv * d * 2
+        copies = max(2, min(64, (512 << 20) // per))
+        caches = [(torch.randn(nblk, bs, hkv, d, device=dev, generator=gen).to(torch.bfloat16),
+                   torch.randn(nblk, bs, hkv, d, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(copies)]
+        ids = torch.randperm(nblk, device=dev, generator=gen).to(torch.int32)
+        q = torch.randn(s_rows, h, d, device=dev, generator=gen).to(torch.bfloat16)
+        kn = torch.randn(s_rows, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+        vn = torch.randn(s_rows, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+        qg = torch.randn(s_rows, h, 2 * d, device=dev, generator=gen).to(torch.bfloat16)
+        o = torch.empty(s_rows, h * d, device=dev, dtype=torch.bfloat16)
+
+        def run():
+            abi.set_stream(torch.cuda.current_stream().cuda_stream)
+            for kc, vc in caches:
+                rc = abi.paged_attention_bf16_ptr(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(),
+                                                  vc.data_ptr(), ids.data_ptr(), qg.data_ptr() + 2 * d, o.data_ptr(),
+                                                  s_rows, h, hkv, d, L, bs, nblk, nblk, 2 * d)
+                if rc != 0:
+                    raise RuntimeError(f"ekernel_paged_attention_bf16 failed: rc={rc} ({abi.last_error()})")
+        g = capture(torch, run)
+        us = time_graph(torch, g, 5, 1) / (5 * copies) * 1e6
+        del g, caches
+        kv = 2 * L * hkv * d * 2
+        out[f"{model}_S{s_rows}_L{L}"] = {"H": h, "Hkv": hkv, "D": d, "S": s_rows, "L": L, "us": round(us, 2),
+                                           "kv_GBps": round(kv / us / 1e3, 1)}
+    torch.cuda.empty_cache()
+    return out
 
 
 def sweep_fused(torch, dev, reps: int = 20) -> dict:
@@ -500,7 +550,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sweep", nargs="?", const="g128", default=None,
-                    help="add per-shape sweeps: comma list of g128,w4row,w8a32,w8a16,gemm,fused,load or 'all'")
+                    help="add per-shape sweeps: comma list of g128,w4row,w8a32,w8a16,gemm,fused,attention,load or 'all'")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-pass", action="store_true")
@@ -579,7 +629,7 @@ def main(argv=None) -> int:
         "roofline": roof,
     }
     if args.sweep:
-        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "load") if args.sweep == "all" \
+        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "attention", "load") if args.sweep == "all" \
             else tuple(args.sweep.split(","))
         print(f"[bench] sweeps: {', '.join(sections)}", flush=True)
         del calls, xs, run
