@@ -107,16 +107,31 @@ __device__ __forceinline__ uint16_t *cache_row(const AttnArgs &a, uint16_t *cach
 // rounded to bf16.
 __device__ __forceinline__ float att_exp(float x) { return expf(x); }
 
+// Wave reductions in a fixed order with DPP inside each 16-lane row (quad
+// swaps, then rotations by 4 and 8) and the four row results by v_readlane:
+// ALU operations only, no LDS round trip.  The result is wave-uniform.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float x, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-    return x;
+    x = fmaxf(x, dpp_f<0xB1>(x));    // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp_f<0x4E>(x));    // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp_f<0x124>(x));   // row_ror:4
+    x = fmaxf(x, dpp_f<0x128>(x));   // row_ror:8
+    return fmaxf(fmaxf(lane_f(x, 0), lane_f(x, 16)), fmaxf(lane_f(x, 32), lane_f(x, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    return x;
+    x = x + dpp_f<0xB1>(x);
+    x = x + dpp_f<0x4E>(x);
+    x = x + dpp_f<0x124>(x);
+    x = x + dpp_f<0x128>(x);
+    return (lane_f(x, 0) + lane_f(x, 16)) + (lane_f(x, 32) + lane_f(x, 48));
 }
 
 template <int D, int RB>
@@ -441,6 +456,181 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     if (lane == 0) __hip_atomic_store(a.tickets + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Short contexts (L <= 512 positions, RB x D <= 1024): the whole step in
+// one workgroup of eight waves per kv head and one launch.  Thread t owns
+// position t: it forms its scores (as the score pass) and keeps its softmax
+// weights and value-row pointer in registers; wave w then runs P.V over
+// exactly the 64 positions its lanes own (weights and row pointers by
+// v_readlane), so no scratch, ticket or second launch is needed.  Row max and
+// sum meet through LDS in a fixed order.
+constexpr int kSmallL = 512;
+constexpr int kSmallWaves = kSmallL / 64;
+
+template <int D, int RB>
+__global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
+    constexpr int E = D / 64;
+    constexpr int W = kSmallWaves;
+    typedef std::conditional_t<E == 1, uint16_t, std::conditional_t<E == 2, uint32_t, u32x2>> Raw;
+    __shared__ float qs[RB * D];
+    __shared__ float wred[W][RB], rmax[RB], rinv[RB];
+    __shared__ float red[(W - 1) * RB * D];
+    const int kvh = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int R = a.S * a.rep;
+    const float ninf = -__builtin_inff();
+    for (int e = tid; e < RB * D; e += kSmallL) {
+        const int r = e / D, d = e - r * D;
+        float v = 0.0f;
+        if (r < R) {
+            const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+            v = bf16_bits(a.q[((size_t)(a.s0 + s) * a.H + h) * D + d]);
+        }
+        qs[e] = v;
+    }
+    __syncthreads();
+
+    // scores of position tid (attention.py:128-134)
+    const int j = tid;
+    const bool valid = j < a.L;
+    const uint64_t vrow = (uint64_t)(uintptr_t)kv_row<D>(a, a.v_cache, a.v_new, min(j, a.L - 1), kvh);
+    float sc[RB];
+    {
+        float acc[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
+        if (valid) {
+            const auto *kp = gbl((const u32x4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh));
+            const bool fresh = a.write_cache && j >= a.new0 + a.s0;
+            auto *kdst = fresh ? gbl_w((u32x4 *)cache_row<D>(a, a.k_cache, j, kvh)) : nullptr;
+            if (fresh) {
+                auto *vdst = gbl_w((u32x4 *)cache_row<D>(a, a.v_cache, j, kvh));
+                const auto *vsrc = gbl((const u32x4 *)(uintptr_t)vrow);
+#pragma unroll 4
+                for (int c = 0; c < D / 8; ++c) vdst[c] = vsrc[c];
+            }
+#pragma unroll 2
+            for (int c = 0; c < D / 8; ++c) {
+                const u32x4 kv = kp[c];
+                if (kdst) kdst[c] = kv;
+                const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float k0 = bf16_lo(w[t]), k1 = bf16_hi(w[t]);
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t], k0, acc[r]);
+                        acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t + 1], k1, acc[r]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const bool seen = valid && r < R && j <= a.new0 + a.s0 + r / a.rep;
+            sc[r] = seen ? bf16_round(bf16_round(acc[r]) * a.scale) : ninf;
+        }
+    }
+    // row max, then sum of exp(s - max) (lanes by butterfly, waves in wave
+    // order), then the bf16 weights (:136)
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const float m = wave_max(sc[r]);
+        if (lane == 0) wred[wave][r] = m;
+    }
+    __syncthreads();
+    if (tid < RB) {
+        float m = wred[0][tid];
+#pragma unroll
+        for (int w = 1; w < W; ++w) m = fmaxf(m, wred[w][tid]);
+        rmax[tid] = m;
+    }
+    __syncthreads();
+    float pw[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        pw[r] = sc[r] == ninf ? 0.0f : att_exp(sc[r] - rmax[r]);
+        const float l = wave_sum(pw[r]);
+        if (lane == 0) wred[wave][r] = l;
+    }
+    __syncthreads();
+    if (tid < RB) {
+        float l = wred[0][tid];
+#pragma unroll
+        for (int w = 1; w < W; ++w) l = l + wred[w][tid];
+        rinv[tid] = 1.0f / l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RB; ++r) pw[r] = r < R ? bf16_round(pw[r] * rinv[r]) : 0.0f;
+
+    // P.V (:137): wave w over its lanes' positions, value rows in flight
+    float acc[RB][E];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[r][e] = 0.0f;
+    if (wave * 64 < a.L) {
+        Raw raw[64];
+#pragma unroll
+        for (int u = 0; u < 64; ++u) {
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)vrow, u);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(vrow >> 32), u);
+            const uint16_t *vr = (const uint16_t *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+            raw[u] = *gbl((const Raw *)(vr + E * lane));
+        }
+#pragma unroll
+        for (int u = 0; u < 64; ++u) {
+            // (positions past the end read the last row with weight 0)
+            float v[E];
+            if constexpr (E == 1) {
+                v[0] = bf16_bits(raw[u]);
+            } else if constexpr (E == 2) {
+                v[0] = bf16_lo(raw[u]);
+                v[1] = bf16_hi(raw[u]);
+            } else {
+                v[0] = bf16_lo(raw[u].x);
+                v[1] = bf16_hi(raw[u].x);
+                v[2] = bf16_lo(raw[u].y);
+                v[3] = bf16_hi(raw[u].y);
+            }
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[r]), u));
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[r][e] = __builtin_fmaf(w, v[e], acc[r][e]);
+            }
+        }
+    }
+    if (wave != 0) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int e = 0; e < E; ++e) red[((wave - 1) * RB + r) * D + E * lane + e] = acc[r][e];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        if (r >= R) continue;
+        const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+        const size_t row = (size_t)(a.s0 + s) * a.H + h;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int d = E * lane + e;
+            float x = acc[r][e];
+#pragma unroll
+            for (int w = 0; w < W - 1; ++w) x = x + red[(w * RB + r) * D + d];
+            uint16_t o = f32_to_bf16(x);
+            if (a.gate) {   // :139
+                const float g = bf16_bits(a.gate[row * a.gate_stride + d]);
+                const float sig = bf16_round(1.0f / (1.0f + att_exp(-g)));
+                o = f32_to_bf16(bf16_bits(o) * sig);
+            }
+            a.out[row * D + d] = o;
+        }
+    }
+}
+
 template <int D, int RB>
 int launch_attn(const AttnArgs &a, hipStream_t st) {
     static std::once_flag once;
@@ -450,6 +640,12 @@ int launch_attn(const AttnArgs &a, hipStream_t st) {
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)pv_lds_bytes<D, RB>());
     });
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    if constexpr (RB * D <= 1024) {
+        if (a.L <= kSmallL && env_int("PILM_HIP_ATTN_SMALL", 1) != 0) {
+            attn_small_kernel<D, RB><<<dim3((unsigned)a.Hkv), kSmallL, 0, st>>>(a);
+            return ECPU_OK;
+        }
+    }
     attn_scores_kernel<D, RB><<<dim3((unsigned)a.nchunk, (unsigned)a.Hkv), 256, 0, st>>>(a);
     attn_pv_kernel<D, RB><<<dim3((unsigned)a.ngroups, (unsigned)a.Hkv), 256, pv_lds_bytes<D, RB>(), st>>>(a);
     return ECPU_OK;

@@ -92,6 +92,8 @@ CASES = [
     (1, 32, 8, 128, 4097, 64, "none"), (4, 16, 8, 128, 517, 16, "strided"), (5, 32, 8, 128, 600, 16, "strided"),
     (20, 16, 8, 128, 300, 16, "strided"), (9, 32, 8, 128, 40, 16, "none"), (3, 8, 1, 128, 77, 8, "contiguous"),
     (2, 4, 4, 64, 129, 1, "strided"), (3, 8, 2, 256, 270, 32, "strided"), (1, 64, 2, 128, 33, 16, "none"),
+    (4, 16, 8, 128, 512, 16, "strided"), (4, 16, 8, 128, 513, 16, "strided"), (2, 16, 4, 256, 300, 16, "strided"),
+    (1, 8, 8, 64, 500, 4, "contiguous"), (1, 8, 2, 256, 300, 16, "strided"), (16, 16, 16, 64, 200, 16, "strided"),
 ]
 
 
@@ -99,6 +101,17 @@ CASES = [
 def test_paged_attention_against_oracle(case, dev):
     S, H, Hkv, D, L, BS, gate = case
     _say(f"[gpu] attention {case}")
+    out, ref = _run_both(dev, S, H, Hkv, D, L, BS, True, gate, seed=S * 100003 + L)
+    _check(out, ref, str(case))
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[4] <= 512], ids=lambda c: "S{}_H{}_kv{}_D{}_L{}".format(*c))
+def test_short_context_two_launch_path(case, dev, monkeypatch):
+    """Up to 512 positions and 8 rows per kv head run as one launch; the
+    two-launch path (scores, then P.V) must give the same results there."""
+    monkeypatch.setenv("PILM_HIP_ATTN_SMALL", "0")
+    S, H, Hkv, D, L, BS, gate = case
+    _say(f"[gpu] attention two-launch {case}")
     out, ref = _run_both(dev, S, H, Hkv, D, L, BS, True, gate, seed=S * 100003 + L)
     _check(out, ref, str(case))
 
