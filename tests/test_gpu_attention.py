@@ -171,3 +171,41 @@ def test_rejected_arguments(dev):
         A.paged_attention(gq, gk, gv, gkc, gvc, ids[:1], 40)    # too few block ids
     with pytest.raises(RuntimeError):
         A.paged_attention(gq, gk, gv, None, None, None, 40)     # no cache needs cache_len == S
+
+
+@pytest.mark.parametrize("L", [300, 1000, 5000])
+def test_graph_replays_match_eager(L, dev):
+    """The call captured in a HIP graph (one launch at 300 positions; two
+    launches with the P.V ticket at 1000; with the statistics ticket too at
+    5000) and replayed three times with eager work in between: every replay
+    gives the eager call's bits (tickets are reset by the kernels, no memset
+    is captured)."""
+    _say(f"[gpu] attention graph L={L}")
+    S, H, Hkv, D, BS = 1, 16, 8, 128, 16
+    q, k_new, v_new, kc, vc, ids, qg = _inputs(21, S, H, Hkv, D, L, BS, True, "strided")
+    args = [t.to(dev) for t in (q, k_new, v_new, kc, vc)]
+    table = torch.tensor(ids, dtype=torch.int32, device=dev)
+    gate = qg.to(dev)[:, :, D:]
+    eager = A.paged_attention(*args, table, L, gate)        # also sizes the scratch before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        A.paged_attention(*args, table, L, gate)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        out = A.paged_attention(*args, table, L, gate)
+    # eager work between replays, on caches of its own (a call stores its new
+    # rows, which would change what the captured call reads)
+    other = [args[0], args[1], args[2], args[3].clone(), args[4].clone()]
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        junk = A.paged_attention(*other, table, L // 2 + 1, gate)
+        torch.cuda.synchronize()
+        del junk
