@@ -651,6 +651,12 @@ int launch_attn(const AttnArgs &a, hipStream_t st) {
     return ECPU_OK;
 }
 
+// Query rows per kv head are computed in buckets of 1, 2, 4, 8, 16, 24 or 32
+// (24: MTP verify with 5 tokens of a 4-head GQA group, 20 rows).
+int row_bucket(int R) {
+    return R <= 1 ? 1 : (R <= 2 ? 2 : (R <= 4 ? 4 : (R <= 8 ? 8 : (R <= 16 ? 16 : (R <= 24 ? 24 : 32)))));
+}
+
 template <int D>
 int launch_attn_rb(int rb, const AttnArgs &a, hipStream_t st) {
     switch (rb) {
@@ -659,6 +665,7 @@ int launch_attn_rb(int rb, const AttnArgs &a, hipStream_t st) {
         case 4: return launch_attn<D, 4>(a, st);
         case 8: return launch_attn<D, 8>(a, st);
         case 16: return launch_attn<D, 16>(a, st);
+        case 24: return launch_attn<D, 24>(a, st);
         default: return launch_attn<D, 32>(a, st);
     }
 }
@@ -673,7 +680,7 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
     const int L_total = (int)d->cache_len;
     // query rows per launch: the most tokens whose heads fit kMaxRows rows
     const int per = std::max(1, std::min(S, kMaxRows / rep));
-    const int rb_full = per * rep <= 1 ? 1 : (per * rep <= 2 ? 2 : (per * rep <= 4 ? 4 : (per * rep <= 8 ? 8 : (per * rep <= 16 ? 16 : 32))));
+    const int rb_full = row_bucket(per * rep);
     const int Lp_max = (L_total + kChunk - 1) / kChunk * kChunk;
     const int nchunk_max = Lp_max / kChunk;
     const size_t score_floats = ((size_t)Hkv * rb_full * Lp_max * sizeof(uint16_t) + 3) / 4;
@@ -714,7 +721,7 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
         a.s0 = s0;
         a.S = std::min(per, S - s0);
         const int R = a.S * rep;
-        const int rb = R <= 1 ? 1 : (R <= 2 ? 2 : (R <= 4 ? 4 : (R <= 8 ? 8 : (R <= 16 ? 16 : 32))));
+        const int rb = row_bucket(R);
         a.L = a.new0 + s0 + a.S;
         a.Lp = (a.L + kChunk - 1) / kChunk * kChunk;
         a.nchunk = a.Lp / kChunk;
