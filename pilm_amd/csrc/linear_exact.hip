@@ -465,7 +465,14 @@ constexpr int bcast_act_bytes() { return 2 * MT * 256 * 2; }
 // LDS: pl stripe slots, pl activation buffers, then (pl > 1) the fold area:
 // float blocks[G - G0][MT][64] and float scales[G - G0][64], G0 = groups of
 // part 0.
-template <int FMT, int MT>
+// WIN (windowed fold, for long rows whose parked block sums would not fit):
+// the waves take stripes in rounds, wave w stripe t * pl + w of round t, and
+// park each round's block sums in one of two buffers,
+// float blocks[2][pl][GPS][MT][64] and scales[2][pl][GPS][64]; after the
+// round's barrier wave 0 folds them in stripe and group order while the
+// others go on to the next round in the other buffer (a buffer is written
+// again only after the next barrier, which wave 0 reaches after its fold).
+template <int FMT, int MT, bool WIN = false>
 __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16_t *__restrict__ A,
                                                                    const uint8_t *__restrict__ W,
                                                                    const float *__restrict__ S,
@@ -487,8 +494,10 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16
     const int mvalid = min(MT, M - mb);
     const int nstripes = K / 256;
     const int G = nstripes * GPS;
-    const int s0 = min(wave * sps, nstripes);
-    const int s1 = min(s0 + sps, nstripes);
+    const int s0 = WIN ? min(wave, nstripes) : min(wave * sps, nstripes);
+    const int s1 = WIN ? nstripes : min(s0 + sps, nstripes);
+    const int sstep = WIN ? pl : 1;                 // a wave's next stripe
+    const int nrounds = (nstripes + pl - 1) / pl;   // (WIN)
     const int G0 = min(sps * GPS, G);
     const size_t row_bytes = (size_t)K / 2;
 
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16
     u32x4 *my_slot = (u32x4 *)(lds + wave * kSlotBytes);
     unsigned char *my_act = lds + pl * kSlotBytes + wave * kAct;   // [2][MT rows][256] bf16
     float *fold_blocks = (float *)(lds + pl * (kSlotBytes + kAct));
-    float *fold_scales = fold_blocks + (size_t)(G - G0) * MT * 64;
+    float *fold_scales = fold_blocks + (WIN ? (size_t)2 * pl * GPS * MT * 64 : (size_t)(G - G0) * MT * 64);
     const float *srow = S + (size_t)nc * G;
     // Activation DMA: instruction j, lane t fetches 16 bytes of row 2j + t/32
     // (rows past M repeat the last row; their results are not stored).
@@ -520,7 +529,8 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16
 #pragma unroll
         for (int j = 0; j < kActLoads; ++j)
             __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + (size_t)st * 256),
-                                             (lds_void *)(my_act + (st & 1) * (kAct / 2) + j * 1024), 16, 0, 0);
+                                             (lds_void *)(my_act + (((st - s0) / sstep) & 1) * (kAct / 2) + j * 1024), 16, 0,
+                                             0);
     };
     if (s0 < s1) issue(s0);
 
@@ -529,8 +539,25 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16
     for (int m = 0; m < MT; ++m) gacc[m] = 0.0f;
     const uint32_t magic = opaque_magic();
 
+    auto fold_round = [&](int t) {   // (WIN) wave 0: round t's block sums, stripe then group order
+        const float *pb = fold_blocks + (size_t)(t & 1) * pl * GPS * MT * 64;
+        const float *ps = fold_scales + (size_t)(t & 1) * pl * GPS * 64;
+        for (int w = 0; w < pl && t * pl + w < nstripes; ++w)
+#pragma unroll
+            for (int gl = 0; gl < GPS; ++gl) {
+                const float scg = ps[(w * GPS + gl) * 64 + lane];
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    gacc[m] = __builtin_fmaf(pb[((w * GPS + gl) * MT + m) * 64 + lane], scg, gacc[m]);
+            }
+    };
 #pragma unroll 1
-    for (int s = s0; s < s1; ++s) {
+    for (int it = 0, s = s0; WIN ? it < nrounds : s < s1; ++it, s += sstep) {
+        if (WIN && s >= s1) {   // no stripe for this wave in the last round
+            __syncthreads();
+            if (wave == 0) fold_round(it);
+            continue;
+        }
         float sc[GPS];
 #pragma unroll
         for (int g = 0; g < GPS; ++g) sc[g] = srow[s * GPS + g];
@@ -539,10 +566,10 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) mine[j] = my_slot[8 * lane + (j ^ swz)];
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the slot may be refilled
-        if (s + 1 < s1) issue(s + 1);
+        if (s + sstep < s1) issue(s + sstep);
 
         // lane i of each 16-lane row reads element i of every chunk
-        const uint16_t *abuf = (const uint16_t *)(my_act + (s & 1) * (kAct / 2)) + (lane & 15);
+        const uint16_t *abuf = (const uint16_t *)(my_act + (it & 1) * (kAct / 2)) + (lane & 15);
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
             float a[MT];
@@ -572,20 +599,33 @@ __global__ __launch_bounds__(64 * kMaxParts) void gemv_bcast_kernel(const uint16
             if ((c + 1) % CPG == 0) {
                 const int gl = c / CPG;
                 const int g = GPS * s + gl;
+                if constexpr (WIN) {
+                    float *pb = fold_blocks + (size_t)(it & 1) * pl * GPS * MT * 64;
 #pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const float block = w4_block(lo[m], hi[m]);
-                    if (wave == 0)
-                        gacc[m] = __builtin_fmaf(block, sc[gl], gacc[m]);
-                    else
-                        fold_blocks[((g - G0) * MT + m) * 64 + lane] = block;
+                    for (int m = 0; m < MT; ++m) pb[((wave * GPS + gl) * MT + m) * 64 + lane] = w4_block(lo[m], hi[m]);
+                    fold_scales[((size_t)(it & 1) * pl * GPS + wave * GPS + gl) * 64 + lane] = sc[gl];
+                } else {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const float block = w4_block(lo[m], hi[m]);
+                        if (wave == 0)
+                            gacc[m] = __builtin_fmaf(block, sc[gl], gacc[m]);
+                        else
+                            fold_blocks[((g - G0) * MT + m) * 64 + lane] = block;
+                    }
+                    if (wave != 0) fold_scales[(g - G0) * 64 + lane] = sc[gl];
                 }
-                if (wave != 0) fold_scales[(g - G0) * 64 + lane] = sc[gl];
             }
+        }
+        if constexpr (WIN) {
+            __syncthreads();
+            if (wave == 0) fold_round(it);
         }
     }
 
-    if (pl > 1) {
+    if (WIN) {
+        if (wave != 0) return;
+    } else if (pl > 1) {
         __syncthreads();
         if (wave != 0) return;
         for (int gi = 0; gi < G - G0; ++gi) {
@@ -606,18 +646,30 @@ static size_t bcast_lds_bytes(int mt, int pl, int sps, int G, int gps) {
     return bytes;
 }
 
-template <int FMT, int MT>
-static int launch_bcast(dim3 grid, dim3 block, size_t lds, hipStream_t st, const uint16_t *A, const uint8_t *W,
-                        const float *S, uint16_t *C, int M, int N, int K, int sps) {
+// Windowed fold: two round buffers of pl stripes' block sums and scales.
+static size_t bcast_win_lds_bytes(int mt, int pl, int gps) {
+    return (size_t)pl * (kSlotBytes + (size_t)2 * mt * 256 * 2) + (size_t)2 * pl * gps * 64 * (mt + 1) * sizeof(float);
+}
+
+template <int FMT, int MT, bool WIN>
+static int launch_bcast_one(dim3 grid, dim3 block, size_t lds, hipStream_t st, const uint16_t *A, const uint8_t *W,
+                            const float *S, uint16_t *C, int M, int N, int K, int sps) {
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     std::call_once(once, [] {
-        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_bcast_kernel<FMT, MT>),
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_bcast_kernel<FMT, MT, WIN>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     });
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
-    gemv_bcast_kernel<FMT, MT><<<grid, block, lds, st>>>(A, W, S, C, M, N, K, sps);
+    gemv_bcast_kernel<FMT, MT, WIN><<<grid, block, lds, st>>>(A, W, S, C, M, N, K, sps);
     return ECPU_OK;
+}
+
+template <int FMT, int MT>
+static int launch_bcast(bool win, dim3 grid, dim3 block, size_t lds, hipStream_t st, const uint16_t *A,
+                        const uint8_t *W, const float *S, uint16_t *C, int M, int N, int K, int sps) {
+    return win ? launch_bcast_one<FMT, MT, true>(grid, block, lds, st, A, W, S, C, M, N, K, sps)
+               : launch_bcast_one<FMT, MT, false>(grid, block, lds, st, A, W, S, C, M, N, K, sps);
 }
 
 // Small-M path of the group formats: every M rows in one launch (m-groups of
@@ -629,10 +681,10 @@ static int launch_bcast(dim3 grid, dim3 block, size_t lds, hipStream_t st, const
 // 6144x2048 16.4 vs 21.0 us, 4096x2048 16.3 vs 11.2 us).  The group-quad
 // kernels take (returns ECPU_ERR_UNSUPPORTED): up to four rows with fewer
 // than 768 waves or at most 6144 rows (g128 4096x4096 M=4: 13.0 vs 16.1 us,
-// 6144x2048 M=3: 9.8 vs 11.0 us), and up to eight rows when LDS leaves two
-// waves per tile or fewer (group 32, long K: 1024x4096 M=5 22 vs 50 us,
-// 4096x12288 113 vs 266 us) or takes any beyond 8192 rows (those go to the
-// 64-row tiles: g32 12288x2048 M=5 22.6 vs 29.8 us).
+// 6144x2048 M=3: 9.8 vs 11.0 us), up to eight rows when LDS leaves two waves
+// per tile or fewer and the windowed fold is not available (or takes any
+// beyond 8192 rows: those go to the 64-row tiles, g32 12288x2048 M=5 22.6 vs
+// 29.8 us), and five rows on small cramped shapes (below).
 static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
                      hipStream_t st, const char *fn) {
     const int nstripes = (int)(K / 256);
@@ -656,17 +708,41 @@ static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const
     int pl8, sps8, pl4, sps4;
     plan(8, pl8, sps8);
     plan(4, pl4, sps4);
-    const bool cramped = reduced && (pl4 <= 2 || N > 8192);
+    // The windowed fold keeps more waves where the parked block sums would
+    // not fit (group 32, long rows): the most parts (8, 4, 2) whose round
+    // buffers fit, used for four-row groups when that beats the parked plan
+    // (g32 4096x12288 M=16: 77 vs 266 us, 1024x4096 M=16: 27 vs 50 us; g128
+    // 4096x12288 M=16: 51 vs 58 us).  Eight-row groups keep the parked plan:
+    // their windowed buffers leave 2 waves and one workgroup per CU (g32
+    // 24576x4096 M=32: 453 vs 239 us).
+    auto win_parts = [&](int mt) {
+        int p = std::min(kMaxParts, nstripes);
+        while (p > 1 && bcast_win_lds_bytes(mt, p, gps) > kMaxLds) p /= 2;
+        return p;
+    };
+    const int env_win = env_int("PILM_HIP_BCAST_WIN", -1);
+    const int pl4_parked = pl4;
+    const int pw8 = win_parts(8), pw4 = win_parts(4);
+    const bool win8 = env_win == 1 && pw8 > 1;
+    const bool win4 = env_win == 1 ? pw4 > 1 : (env_win != 0 && pw4 > pl4);
+    if (win8) { pl8 = pw8; sps8 = (nstripes + pw8 - 1) / pw8; }
+    if (win4) { pl4 = pw4; sps4 = (nstripes + pw4 - 1) / pw4; }
+    const bool cramped = reduced && !win4 && (pl4 <= 2 || N > 8192);
+    // five rows on a small shape whose parked plan keeps two waves or fewer:
+    // two group-quad launches (4 + 1 rows) win (g32 1024x4096: 22.1 vs 26.7
+    // us, 2048x6144: 32.6 vs 39.4 us)
+    const bool five_gq = reduced && pl4_parked <= 2 && env_win != 1 && M == 5 && N <= 6144 && K <= 8192;
     const size_t waves8 = ntiles * pl8 * ((M + 7) / 8), waves4 = ntiles * pl4 * ((M + 3) / 4);
     const size_t pad8 = (M + 7) / 8 * 8, pad4 = (M + 3) / 4 * 4;   // rows computed, padding included
     int mt = (pad8 <= pad4 && waves8 >= 1536) ? 8 : 4;
     const int env_mt = env_int("PILM_HIP_BCAST_MT", 0);
     if (env_mt == 4 || env_mt == 8)
         mt = env_mt;
-    else if ((M <= 4 && (waves4 < 768 || N <= 6144)) || (M <= 8 && cramped))
+    else if ((M <= 4 && (waves4 < 768 || N <= 6144)) || (M <= 8 && cramped) || five_gq)
         return ECPU_ERR_UNSUPPORTED;
     const int pl = mt == 8 ? pl8 : pl4, sps = mt == 8 ? sps8 : sps4;
-    const size_t lds = bcast_lds_bytes(mt, pl, sps, G, gps);
+    const bool win = mt == 8 ? win8 : win4;
+    const size_t lds = win ? bcast_win_lds_bytes(mt, pl, gps) : bcast_lds_bytes(mt, pl, sps, G, gps);
     if (lds > kMaxLds) return fail(ECPU_ERR_DEVICE, "%s: small-M tile does not fit in LDS", fn);
     const size_t mgroups = (M + mt - 1) / mt;
     if (mgroups > 65535) return ECPU_ERR_UNSUPPORTED;
@@ -676,11 +752,11 @@ static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const
     uint16_t *c16 = (uint16_t *)C;
     int rc;
     if (fmt == F_W4G128)
-        rc = mt == 4 ? launch_bcast<F_W4G128, 4>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps)
-                     : launch_bcast<F_W4G128, 8>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps);
+        rc = mt == 4 ? launch_bcast<F_W4G128, 4>(win, grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps)
+                     : launch_bcast<F_W4G128, 8>(win, grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps);
     else
-        rc = mt == 4 ? launch_bcast<F_W4G32, 4>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps)
-                     : launch_bcast<F_W4G32, 8>(grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps);
+        rc = mt == 4 ? launch_bcast<F_W4G32, 4>(win, grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps)
+                     : launch_bcast<F_W4G32, 8>(win, grid, block, lds, st, a16, W, S, c16, (int)M, (int)N, (int)K, sps);
     if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the small-M kernel failed", fn);
     return ECPU_OK;
 }

@@ -70,7 +70,8 @@ SPLITS = [{"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_GQ": "0", "PI
           {"PILM_HIP_GQ_P": "8", "PILM_HIP_GQ_D": "8"}, {"PILM_HIP_GQ8": "0"}, {"PILM_HIP_GQ8": "1"},
           {"PILM_HIP_BCAST_PL": "1"}, {"PILM_HIP_BCAST_PL": "3"}, {"PILM_HIP_BCAST_MT": "8"},
           {"PILM_HIP_BCAST_MT": "8", "PILM_HIP_BCAST_PL": "2"}, {"PILM_HIP_BCAST": "0"},
-          {"PILM_HIP_BCAST": "0", "PILM_HIP_GQ": "0"}]
+          {"PILM_HIP_BCAST": "0", "PILM_HIP_GQ": "0"}, {"PILM_HIP_BCAST_WIN": "1", "PILM_HIP_BCAST_MT": "4"},
+          {"PILM_HIP_BCAST_WIN": "1", "PILM_HIP_BCAST_MT": "8"}, {"PILM_HIP_BCAST_WIN": "0"}]
 
 
 @pytest.mark.parametrize("env", SPLITS, ids=lambda e: "_".join(f"{k[9:]}{v}" for k, v in e.items()))
@@ -148,12 +149,12 @@ def test_fresh_shapes_against_oracle(fmt, dev):
 def test_long_rows_group_quad(fmt, dev):
     """K = 12288 (Qwen3-8B down_proj): 24 KB of activations per tile beside
     the rings (group 32: 48 KB of scales and block sums as well, so fewer
-    waves per tile, and launches of fewer activation rows); up to eight rows
-    where the small-M kernel's LDS would hold too few waves (group 32,
-    K = 4096 and 12288); the bits stay the oracle's."""
+    waves per tile, and launches of fewer activation rows); the small-M
+    kernel's windowed fold where its parked block sums would not fit (group
+    32, K = 4096 and 12288); the bits stay the oracle's."""
     gen = GV._gen()
     for m, n, k in ((1, 200, 12288), (2, 37, 12288), (4, 64, 12288), (5, 300, 12288), (8, 24, 12288),
-                    (5, 1024, 4096), (7, 90, 4096)):
+                    (5, 1024, 4096), (7, 90, 4096), (16, 100, 12288), (24, 70, 12288), (13, 500, 4096)):
         _say(f"[gpu] long rows {fmt} M={m} N={n} K={k}")
         x, w, s = gen.make_inputs(fmt, m, n, k, 4242 + m)
         y = run_gpu(fmt, x, w, s, dev)
