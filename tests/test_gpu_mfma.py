@@ -121,3 +121,24 @@ def test_mfma_split_k(splits, dev, monkeypatch):
         y = run_gpu(fmt, x, w, s, dev)
         check_close(fmt, y, gen.run(fmt, x, w, s, "oracle"), f"{fmt} splits={splits}")
         assert np.array_equal(y.view(np.uint8), run_gpu(fmt, x, w, s, dev).view(np.uint8)), "not deterministic"
+
+
+@pytest.mark.parametrize("fmt", ["w8a16", "w4g128", "w4"])
+@pytest.mark.parametrize("nseq", [12, 16])
+def test_continuous_batching_verify(fmt, nseq, dev):
+    """MTP verify under continuous batching (src/engine.py:374-570,
+    scheduler.py:70-178): every sequence's 1 + 4 draft rows go into one call,
+    M = 5 * nseq.  Each sequence's rows must come out as its own M = 5 call
+    gives them: bit-identical below the matrix-core threshold (12 sequences,
+    M = 60), within the matrix-core tolerance from it on (16 sequences,
+    M = 80)."""
+    gen = GV._gen()
+    n, k = 1024, 4096          # Qwen3-8B k_proj
+    x, w, s = gen.make_inputs(fmt, 5 * nseq, n, k, 9500 + nseq)
+    _say(f"[gpu] batched verify {fmt} sequences={nseq} M={5 * nseq}")
+    y = run_gpu(fmt, x, w, s, dev)
+    per = np.concatenate([run_gpu(fmt, x[5 * i:5 * i + 5], w, s, dev) for i in range(nseq)])
+    if 5 * nseq < 64:
+        assert np.array_equal(y.view(np.uint8), per.view(np.uint8)), fmt
+    else:
+        check_close(fmt, y, per, f"{fmt} batched M={5 * nseq}")
