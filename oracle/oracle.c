@@ -4,7 +4,7 @@
  * This file restates, in plain scalar C, the arithmetic of the reference's
  * CPU kernels so that the HIP product can be checked bit for bit.  It is
  * linked only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
- * leg, always as the checker and never as the thing measured or shipped.
+ * leg, always to compare against and never as the thing measured or shipped.
  *
  * Reference (paths relative to the piLM repository):
  *   src/ecpu/src/kernel/kernels.c

@@ -1,6 +1,6 @@
 """Pins the CPU oracle (oracle/oracle.c + oracle/oracle.py).
 
-The oracle is the checker for the HIP kernels, so it is checked first:
+The oracle is what the HIP kernels are compared with, so it is checked first:
   * against the golden vectors written from the reference's own kernels.c;
   * against the reference library built from source, on fresh seeds, when
     oracle/_ref has been built (it needs the reference sources);
