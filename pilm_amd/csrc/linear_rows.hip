@@ -1276,6 +1276,8 @@ template <int T>
 __device__ __forceinline__ void rbc_step8(float (&acc)[8], const float (&a)[8], const float (&w)[8]);
 template <int T>
 __device__ __forceinline__ void rbc_step4(float (&acc)[4], const float (&a)[4], const float (&w)[4]);
+template <int T>
+__device__ __forceinline__ void rbc_step5(float (&acc)[5], const float (&a)[5], const float (&w)[5]);
 
 #define PILM_RBC_DPP(T) " row_newbcast:" #T " row_mask:0xf bank_mask:0xf\n\t"
 #define PILM_RBC_DEF(T)                                                                                           \
@@ -1298,6 +1300,16 @@ __device__ __forceinline__ void rbc_step4(float (&acc)[4], const float (&a)[4], 
                      "v_fmac_f32_dpp %2, %6, %10" PILM_RBC_DPP(T) "v_fmac_f32_dpp %3, %7, %11" PILM_RBC_DPP(T)    \
                      : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])                                     \
                      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));   \
+    }                                                                                                             \
+    template <>                                                                                                   \
+    __device__ __forceinline__ void rbc_step5<T>(float (&acc)[5], const float (&a)[5], const float (&w)[5]) {      \
+        asm volatile("s_nop 1\n\t"                                                                                \
+                     "v_fmac_f32_dpp %0, %5, %10" PILM_RBC_DPP(T) "v_fmac_f32_dpp %1, %6, %11" PILM_RBC_DPP(T)    \
+                     "v_fmac_f32_dpp %2, %7, %12" PILM_RBC_DPP(T) "v_fmac_f32_dpp %3, %8, %13" PILM_RBC_DPP(T)    \
+                     "v_fmac_f32_dpp %4, %9, %14" PILM_RBC_DPP(T)                                                 \
+                     : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4])                       \
+                     : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(w[0]), "v"(w[1]), "v"(w[2]),    \
+                       "v"(w[3]), "v"(w[4]));                                                                     \
     }
 PILM_RBC_DEF(0) PILM_RBC_DEF(1) PILM_RBC_DEF(2) PILM_RBC_DEF(3) PILM_RBC_DEF(4) PILM_RBC_DEF(5) PILM_RBC_DEF(6)
 PILM_RBC_DEF(7) PILM_RBC_DEF(8) PILM_RBC_DEF(9) PILM_RBC_DEF(10) PILM_RBC_DEF(11) PILM_RBC_DEF(12)
@@ -1309,14 +1321,15 @@ template <int FMT, int MT, int CS>
 struct RbcFmt {
     using F = ChainFmt<FMT, CS>;
     static constexpr int SL = F::slots;                        // chains per lane
-    static constexpr int NF = MT * SL;                         // FMAs per lane and step (4 or 8)
-    static_assert(NF == 4 || NF == 8, "row-broadcast step width");
+    static constexpr int NF = MT * SL;                         // FMAs per lane and step (4, 5 or 8)
+    static_assert(NF == 4 || NF == 5 || NF == 8, "row-broadcast step width");
     static constexpr int ES = FMT == F_W8A32 ? 4 : 2;          // activation bytes
     static constexpr int SPE = F::w8 ? 128 : 256;              // row elements per stripe
     static constexpr int STEP = F::w8 ? 8 : 16;                // elements per step (a chain takes one)
     static constexpr int RB = SPE * ES;                        // activation bytes of a row per stripe
-    static constexpr int ACT = MT * RB;                        // activation bytes per slot
-    static_assert(ACT % 1024 == 0, "activation DMA granularity");
+    // activation bytes per slot, in whole 1 KB DMA instructions (five rows:
+    // the padding repeats the last row and is not read)
+    static constexpr int ACT = (MT * RB + 1023) / 1024 * 1024;
     static constexpr int SLOT = kQuadSlotBytes + ACT;          // weights (16 rows x 128 B) + activations
     static constexpr int PER = 2 + ACT / 1024;                 // DMA instructions per stripe
 };
@@ -1431,6 +1444,8 @@ __global__ __launch_bounds__(64 * CS) void gemv_rbc_kernel(const void *__restric
             }
             if constexpr (R::NF == 8)
                 rbc_step8<T>(fa, av, w);
+            else if constexpr (R::NF == 5)
+                rbc_step5<T>(fa, av, w);
             else
                 rbc_step4<T>(fa, av, w);
         };
@@ -1518,7 +1533,8 @@ int launch_rbc_one(int ntiles, int mgroups, hipStream_t st, const void *A, const
 
 // Per-row formats, 3 <= M < 64: one chain per lane (W8 over two waves per
 // tile, W4 over four), MT = 8 activation rows per wave where that computes
-// no more padding rows than MT = 4 and still leaves >= 2048 waves, else 4
+// no more padding rows than MT = 4 and still leaves >= 2048 waves, MT = 5
+// for five rows on larger shapes (below), else 4
 // (measured: W8A16 8192x4096 M=5 23.1 vs 29.0 us, W4 12288x2048 M=16 25.2
 // vs 27.2 us, W4 12288x2048 M=4 10.0 vs 13.5 us).
 int run_rbc(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
@@ -1527,24 +1543,33 @@ int run_rbc(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t 
     const int cs = fmt == F_W4ROW ? 4 : 2;
     const size_t pad8 = (M + 7) / 8 * 8, pad4 = (M + 3) / 4 * 4;
     int mt = pad8 <= pad4 && (size_t)ntiles * cs * (pad8 / 8) >= 2048 ? 8 : 4;
+    // MTP verify with four drafts: five rows, no padding, where the tiles
+    // alone give enough waves (>= 512 for W8, >= 1024 for W4; below, two
+    // m-groups of four spread further): W8A16 24576x4096 51.4 vs 67.5 us,
+    // 8192x4096 22.2 vs 23.6 us; 1024x4096 stays at 15.7 (vs 17.3) us.
+    if (M == 5 && (size_t)ntiles * cs >= (cs == 4 ? 1024u : 512u))
+        mt = 5;
     const int env_mt = env_int("PILM_HIP_RBC_MT", 0);
-    if (env_mt == 4 || env_mt == 8) mt = env_mt;
+    if (env_mt == 4 || env_mt == 5 || env_mt == 8) mt = env_mt;
     const size_t mgroups = (M + mt - 1) / mt;
     if (mgroups > 65535) return ECPU_ERR_UNSUPPORTED;
     const int mg = (int)mgroups;
     int rc;
     switch (fmt) {
         case F_W8A32:
-            rc = mt == 8 ? launch_rbc_one<F_W8A32, 8, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
-                         : launch_rbc_one<F_W8A32, 4, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
+            rc = mt == 8   ? launch_rbc_one<F_W8A32, 8, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                 : mt == 5 ? launch_rbc_one<F_W8A32, 5, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                           : launch_rbc_one<F_W8A32, 4, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
             break;
         case F_W8A16:
-            rc = mt == 8 ? launch_rbc_one<F_W8A16, 8, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
-                         : launch_rbc_one<F_W8A16, 4, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
+            rc = mt == 8   ? launch_rbc_one<F_W8A16, 8, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                 : mt == 5 ? launch_rbc_one<F_W8A16, 5, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                           : launch_rbc_one<F_W8A16, 4, 2>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
             break;
         default:
-            rc = mt == 8 ? launch_rbc_one<F_W4ROW, 8, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
-                         : launch_rbc_one<F_W4ROW, 4, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
+            rc = mt == 8   ? launch_rbc_one<F_W4ROW, 8, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                 : mt == 5 ? launch_rbc_one<F_W4ROW, 5, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K)
+                           : launch_rbc_one<F_W4ROW, 4, 4>(ntiles, mg, st, A, W, S, C, (int)M, (int)N, (int)K);
     }
     if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the small-M kernel failed", fn);
     return ECPU_OK;

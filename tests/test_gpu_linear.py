@@ -97,7 +97,8 @@ ROW_PATHS = [{"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "0", "PILM_HIP_ROWTILE": "64"
              {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "4"},
              {"PILM_HIP_CS": "0", "PILM_HIP_QUAD": "1", "PILM_HIP_RING": "16"},
              {"PILM_HIP_CS": "2"}, {"PILM_HIP_CS": "4"},
-             {"PILM_HIP_ROWS": "0"}, {"PILM_HIP_RBC": "0"}, {"PILM_HIP_RBC_MT": "4"},
+             {"PILM_HIP_ROWS": "0"}, {"PILM_HIP_RBC": "0"}, {"PILM_HIP_RBC_MT": "4"}, {"PILM_HIP_RBC_MT": "5"},
+             {"PILM_HIP_RBC_MT": "8"},
              {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "16"}, {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "32"},
              {"PILM_HIP_W8B": "1", "PILM_HIP_W8B_ROWS": "8"},
              {"PILM_HIP_W8B": "0"}, {"PILM_HIP_W4C8": "1"}, {"PILM_HIP_W4C8": "0"}]
@@ -109,7 +110,7 @@ def test_row_format_paths_identical(env, dev, monkeypatch):
     kernels (four waves per 64-row tile, four lanes per row, or two / four
     waves per 16-row tile), the one-wave-per-tile kernel, the byte-wave W8
     kernel (8-, 16- or 32-row tiles, or off) and the small-M row-broadcast
-    kernel (4 or 8 rows per wave, or off) give the same bits."""
+    kernel (4, 5 or 8 rows per wave, or off) give the same bits."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for case in GV.linear_cases(max_elems=1 << 24):
