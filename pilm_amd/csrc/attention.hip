@@ -727,10 +727,10 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
         a.nchunk = a.Lp / kChunk;
         // The score pass folds the chunk statistics once beyond 8 chunks (a
         // ticket); below, each P.V wave reads them all.  At most 64 P.V
-        // workgroups per kv head keep the final fold short; up to 3 chunks
-        // go to one workgroup, which needs no fold at all.
+        // workgroups per kv head keep the final fold short (one workgroup
+        // taking two or three chunks in turn measured slower than the fold).
         a.fold_in_pv = a.nchunk <= 8 ? 1 : 0;
-        a.cpw = a.nchunk <= 3 ? a.nchunk : (a.nchunk + 63) / 64;
+        a.cpw = (a.nchunk + 63) / 64;
         a.ngroups = (a.nchunk + a.cpw - 1) / a.cpw;
         a.write_cache = k_cache != nullptr ? 1 : 0;
         // scores keep the first launch's row stride so the regions stay in bounds

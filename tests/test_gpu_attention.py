@@ -94,6 +94,7 @@ CASES = [
     (2, 4, 4, 64, 129, 1, "strided"), (3, 8, 2, 256, 270, 32, "strided"), (1, 64, 2, 128, 33, 16, "none"),
     (4, 16, 8, 128, 512, 16, "strided"), (4, 16, 8, 128, 513, 16, "strided"), (2, 16, 4, 256, 300, 16, "strided"),
     (1, 8, 8, 64, 500, 4, "contiguous"), (1, 8, 2, 256, 300, 16, "strided"), (16, 16, 16, 64, 200, 16, "strided"),
+    (4, 16, 8, 128, 700, 16, "strided"), (1, 32, 8, 128, 1025, 16, "none"),
 ]
 
 
