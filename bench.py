@@ -15,6 +15,8 @@ replayed.
 Printed JSON line:
   value        algorithmic GB/s of the whole step (weights + scales +
                activations + outputs, each counted once) / wall time
+  hbm_copy_GBps  a 1 GiB device copy timed the same way (read + write), the
+               attainable streaming rate; pct_of_copy_peak = value against it
   roofline     the g128 GEMV kernels' algorithmic GB/s per launch (the
                group-quad kernels for the 196 projections, 8-row tiles for
                k/v/o/down and 16-row tiles for q/gate/up, the 64-row exact
@@ -246,6 +248,19 @@ SHAPES_1P7B_ROW = [("q_proj", 4096, 2048), ("k_proj", 1024, 2048), ("o_proj", 20
                    ("gate_up_proj", 12288, 2048), ("down_proj", 2048, 6144), LM_HEAD]
 SHAPES_8B = [("q_proj", 8192, 4096), ("k_proj", 1024, 4096), ("o_proj", 4096, 4096),
              ("gate_up_proj", 24576, 4096), ("down_proj", 4096, 12288), ("lm_head", 151936, 4096)]
+
+
+def copy_peak(torch, dev, nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Measured device-copy bandwidth on this GPU (read + write of a 1 GiB
+    tensor, HIP graph replay): the attainable streaming rate that the
+    datasheet's 8 TB/s overstates."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    g = capture(torch, lambda: [dst.copy_(src) for _ in range(reps)])
+    sec = time_graph(torch, g, 3, 1)
+    del g, src, dst
+    torch.cuda.empty_cache()
+    return 2 * nbytes * reps * 3 / sec / 1e9
 
 
 def sweep(torch, dev, sections) -> dict:
@@ -607,6 +622,7 @@ def main(argv=None) -> int:
     eager_ms = (time.perf_counter() - t0) / 3 * 1e3
 
     del g
+    copy_gbs = copy_peak(torch, dev)
     out = {
         "metric": "quant GEMV HBM GB/s (% of peak) + Qwen3-1.7B W4A16 decode tok/s, 1 GPU",
         "value": round(value, 1),
@@ -624,6 +640,8 @@ def main(argv=None) -> int:
                    "M": m, "calls_per_step": len(calls), "alg_bytes_per_step": step_bytes,
                    "entry_point": "ekernel_linear_w4a16g128_bf16", "launch": "HIP graph replay"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "hbm_copy_GBps": round(copy_gbs, 1),
+        "pct_of_copy_peak": round(100 * value / copy_gbs, 2),
         "decode_linear_tok_s": round(1e3 / ms_per_step, 1),
         "eager_ms_per_step": round(eager_ms, 3),
         "roofline": roof,
