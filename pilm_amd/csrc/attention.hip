@@ -141,13 +141,16 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     __shared__ int last;
     const int chunk = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int R = a.S * a.rep;
+    // row group z of the kv head: rows rz0 .. rz0 + RB - 1 of the launch's
+    // S * rep; scratch is indexed by kz (kv head and row group) over HZ
+    const int rz0 = blockIdx.z * RB, kz = kvh * gridDim.z + blockIdx.z, HZ = a.Hkv * gridDim.z;
+    const int R = min(RB, a.S * a.rep - rz0);
     // query rows r = s * rep + i (head kvh * rep + i, token s0 + s) as fp32
     for (int e = tid; e < RB * D; e += 256) {
         const int r = e / D, d = e - r * D;
         float v = 0.0f;
         if (r < R) {
-            const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+            const int s = (rz0 + r) / a.rep, h = kvh * a.rep + (rz0 + r - s * a.rep);
             v = bf16_bits(a.q[((size_t)(a.s0 + s) * a.H + h) * D + d]);
         }
         qs[e] = v;
@@ -161,7 +164,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
     if (valid) {
         const auto *kp = gbl((const u32x4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh));
-        auto *dst = (a.write_cache && j >= a.new0 + a.s0) ? gbl_w((u32x4 *)cache_row<D>(a, a.k_cache, j, kvh)) : nullptr;
+        auto *dst = (a.write_cache && blockIdx.z == 0 && j >= a.new0 + a.s0) ? gbl_w((u32x4 *)cache_row<D>(a, a.k_cache, j, kvh)) : nullptr;
 #pragma unroll 2
         for (int c = 0; c < D / 8; ++c) {
             const u32x4 kv = kp[c];
@@ -182,9 +185,9 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     float sc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-        const bool seen = valid && r < R && j <= a.new0 + a.s0 + r / a.rep;
+        const bool seen = valid && r < R && j <= a.new0 + a.s0 + (rz0 + r) / a.rep;
         sc[r] = seen ? bf16_round(bf16_round(acc[r]) * a.scale) : -__builtin_inff();
-        if (r < R) a.scores[((size_t)kvh * RB + r) * a.Lp + j] = f32_to_bf16(sc[r]);
+        if (r < R) a.scores[((size_t)kz * RB + r) * a.Lp + j] = f32_to_bf16(sc[r]);
     }
     // chunk statistics: max, then sum of exp(score - max)
 #pragma unroll
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     __syncthreads();
     if (a.fold_in_pv) {
         if (tid < R) {
-            float *st = a.stats + (((size_t)chunk * a.Hkv + kvh) * RB + tid) * 2;
+            float *st = a.stats + (((size_t)chunk * HZ + kz) * RB + tid) * 2;
             st[0] = cmax[tid];
             st[1] = ((wsum[0][tid] + wsum[1][tid]) + wsum[2][tid]) + wsum[3][tid];
         }
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     // takes rows w, w + 4, ..; lane c chunks c, c + 64, .. in order, then the
     // lanes meet in a fixed butterfly.
     if (tid < R) {
-        float *st = a.stats + (((size_t)chunk * a.Hkv + kvh) * RB + tid) * 2;
+        float *st = a.stats + (((size_t)chunk * HZ + kz) * RB + tid) * 2;
         __hip_atomic_store(st, cmax[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(st + 1, ((wsum[0][tid] + wsum[1][tid]) + wsum[2][tid]) + wsum[3][tid], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -224,13 +227,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     wait_vmcnt<0>();
     __syncthreads();
     if (tid == 0)
-        last = __hip_atomic_fetch_add(a.tickets + a.Hkv + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        last = __hip_atomic_fetch_add(a.tickets + HZ + kz, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                a.nchunk - 1;
     __syncthreads();
     if (!last) return;
-    const size_t cstride = (size_t)a.Hkv * RB * 2;
+    const size_t cstride = (size_t)HZ * RB * 2;
     for (int r = wave; r < R; r += 4) {
-        const float *st = a.stats + ((size_t)kvh * RB + r) * 2;
+        const float *st = a.stats + ((size_t)kz * RB + r) * 2;
         float m = -__builtin_inff();
         for (int c = lane; c < a.nchunk; c += 64)
             m = fmaxf(m, __hip_atomic_load(st + c * cstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -243,12 +246,12 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
         }
         l = wave_sum(l);
         if (lane == 0) {
-            float *gs = a.gstat + ((size_t)kvh * RB + r) * 2;
+            float *gs = a.gstat + ((size_t)kz * RB + r) * 2;
             gs[0] = m;
             gs[1] = 1.0f / l;
         }
     }
-    if (tid == 0) __hip_atomic_store(a.tickets + a.Hkv + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(a.tickets + HZ + kz, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int RB>
@@ -267,14 +270,15 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     const int lane = tid & 63, wave = tid >> 6;
     float *gm = red + 3 * RB * D + wave * 2 * RB;   // [RB] row max, then [RB] 1 / row sum (per wave)
     float *ginv = gm + RB;
-    const int R = a.S * a.rep;
+    const int rz0 = blockIdx.z * RB, kz = kvh * gridDim.z + blockIdx.z, HZ = a.Hkv * gridDim.z;   // (row group)
+    const int R = min(RB, a.S * a.rep - rz0);
     const float ninf = -__builtin_inff();
     const int t0 = wave * 64;
     if (lane < R) {
         if (a.fold_in_pv) {
             // (up to 8 chunks: the row's max and sum folded here, in chunk order)
-            const float *st = a.stats + ((size_t)kvh * RB + lane) * 2;
-            const size_t cstride = (size_t)a.Hkv * RB * 2;
+            const float *st = a.stats + ((size_t)kz * RB + lane) * 2;
+            const size_t cstride = (size_t)HZ * RB * 2;
             float mc[8], lc[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
             gm[lane] = m;
             ginv[lane] = 1.0f / l;
         } else {
-            const float *gs = a.gstat + ((size_t)kvh * RB + lane) * 2;
+            const float *gs = a.gstat + ((size_t)kz * RB + lane) * 2;
             gm[lane] = gs[0];
             ginv[lane] = gs[1];
         }
@@ -346,7 +350,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
         jn = min(64, a.L - (chunk * kChunk + t0));   // this wave's positions (may be <= 0)
         const int jl = chunk * kChunk + t0 + lane;
         const uint16_t *myrow = kv_row<D>(a, a.v_cache, a.v_new, min(jl, a.L - 1), kvh);
-        if (jl < a.L && a.write_cache && jl >= a.new0 + a.s0) {
+        if (jl < a.L && a.write_cache && blockIdx.z == 0 && jl >= a.new0 + a.s0) {
             auto *dst = gbl_w((u32x4 *)cache_row<D>(a, a.v_cache, jl, kvh));
 #pragma unroll 4
             for (int c = 0; c < D / 8; ++c) dst[c] = gbl((const u32x4 *)myrow)[c];
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
         for (int r = 0; r < RB; ++r) {
             float w = 0.0f;
             if (r < R) {
-                const float sc = bf16_bits(a.scores[((size_t)kvh * RB + r) * a.Lp + chunk * kChunk + t0 + lane]);
+                const float sc = bf16_bits(a.scores[((size_t)kz * RB + r) * a.Lp + chunk * kChunk + t0 + lane]);
                 if (sc != ninf) w = bf16_round(att_exp(sc - gm[r]) * ginv[r]);
             }
             p[r * kChunk + t0 + lane] = w;
@@ -399,7 +403,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
 
     auto store = [&](int r, int d, float x) {
         // attention.py:137-139: bf16 P.V, rows (s, h), bf16(out * bf16(sigmoid(gate)))
-        const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+        const int s = (rz0 + r) / a.rep, h = kvh * a.rep + (rz0 + r - s * a.rep);
         const size_t row = (size_t)(a.s0 + s) * a.H + h;
         uint16_t o = f32_to_bf16(x);
         if (a.gate) {
@@ -420,7 +424,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     // Group sums leave as agent-scope stores; once they have completed the
     // wave takes the kv head's ticket, and the last group folds them all in
     // group order with agent-scope loads.
-    float *mine = a.part + ((size_t)grp * a.Hkv + kvh) * RB * D;
+    float *mine = a.part + ((size_t)grp * HZ + kz) * RB * D;
 #pragma unroll
     for (int r = 0; r < RB; ++r)
         if (r < R)
@@ -429,11 +433,11 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
                 __hip_atomic_store(mine + r * D + E * lane + e, acc[r][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_vmcnt<0>();
     int ticket = 0;
-    if (lane == 0) ticket = __hip_atomic_fetch_add(a.tickets + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) ticket = __hip_atomic_fetch_add(a.tickets + kz, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ticket = __builtin_amdgcn_readfirstlane(ticket);
     if (ticket != a.ngroups - 1) return;
-    const size_t gstride = (size_t)a.Hkv * RB * D;
-    const float *base = a.part + (size_t)kvh * RB * D;
+    const size_t gstride = (size_t)HZ * RB * D;
+    const float *base = a.part + (size_t)kz * RB * D;
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -453,7 +457,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
             }
             store(r, d, x);
         }
-    if (lane == 0) __hip_atomic_store(a.tickets + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(a.tickets + kz, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Short contexts (L <= 512 positions, RB x D <= 1024): the whole step in
@@ -476,13 +480,14 @@ __global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
     __shared__ float red[(W - 1) * RB * D];
     const int kvh = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int R = a.S * a.rep;
+    const int rz0 = blockIdx.y * RB;   // row group
+    const int R = min(RB, a.S * a.rep - rz0);
     const float ninf = -__builtin_inff();
     for (int e = tid; e < RB * D; e += kSmallL) {
         const int r = e / D, d = e - r * D;
         float v = 0.0f;
         if (r < R) {
-            const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+            const int s = (rz0 + r) / a.rep, h = kvh * a.rep + (rz0 + r - s * a.rep);
             v = bf16_bits(a.q[((size_t)(a.s0 + s) * a.H + h) * D + d]);
         }
         qs[e] = v;
@@ -500,7 +505,7 @@ __global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
         for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
         if (valid) {
             const auto *kp = gbl((const u32x4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh));
-            const bool fresh = a.write_cache && j >= a.new0 + a.s0;
+            const bool fresh = a.write_cache && blockIdx.y == 0 && j >= a.new0 + a.s0;
             auto *kdst = fresh ? gbl_w((u32x4 *)cache_row<D>(a, a.k_cache, j, kvh)) : nullptr;
             if (fresh) {
                 auto *vdst = gbl_w((u32x4 *)cache_row<D>(a, a.v_cache, j, kvh));
@@ -526,7 +531,7 @@ __global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const bool seen = valid && r < R && j <= a.new0 + a.s0 + r / a.rep;
+            const bool seen = valid && r < R && j <= a.new0 + a.s0 + (rz0 + r) / a.rep;
             sc[r] = seen ? bf16_round(bf16_round(acc[r]) * a.scale) : ninf;
         }
     }
@@ -612,7 +617,7 @@ __global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
         if (r >= R) continue;
-        const int s = r / a.rep, h = kvh * a.rep + (r - s * a.rep);
+        const int s = (rz0 + r) / a.rep, h = kvh * a.rep + (rz0 + r - s * a.rep);
         const size_t row = (size_t)(a.s0 + s) * a.H + h;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -632,7 +637,7 @@ __global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
 }
 
 template <int D, int RB>
-int launch_attn(const AttnArgs &a, hipStream_t st) {
+int launch_attn(const AttnArgs &a, int nz, hipStream_t st) {
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     std::call_once(once, [] {
@@ -642,12 +647,12 @@ int launch_attn(const AttnArgs &a, hipStream_t st) {
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
     if constexpr (RB * D <= 1024) {
         if (a.L <= kSmallL && env_int("PILM_HIP_ATTN_SMALL", 1) != 0) {
-            attn_small_kernel<D, RB><<<dim3((unsigned)a.Hkv), kSmallL, 0, st>>>(a);
+            attn_small_kernel<D, RB><<<dim3((unsigned)a.Hkv, (unsigned)nz), kSmallL, 0, st>>>(a);
             return ECPU_OK;
         }
     }
-    attn_scores_kernel<D, RB><<<dim3((unsigned)a.nchunk, (unsigned)a.Hkv), 256, 0, st>>>(a);
-    attn_pv_kernel<D, RB><<<dim3((unsigned)a.ngroups, (unsigned)a.Hkv), 256, pv_lds_bytes<D, RB>(), st>>>(a);
+    attn_scores_kernel<D, RB><<<dim3((unsigned)a.nchunk, (unsigned)a.Hkv, (unsigned)nz), 256, 0, st>>>(a);
+    attn_pv_kernel<D, RB><<<dim3((unsigned)a.ngroups, (unsigned)a.Hkv, (unsigned)nz), 256, pv_lds_bytes<D, RB>(), st>>>(a);
     return ECPU_OK;
 }
 
@@ -658,15 +663,15 @@ int row_bucket(int R) {
 }
 
 template <int D>
-int launch_attn_rb(int rb, const AttnArgs &a, hipStream_t st) {
+int launch_attn_rb(int rb, int nz, const AttnArgs &a, hipStream_t st) {
     switch (rb) {
-        case 1: return launch_attn<D, 1>(a, st);
-        case 2: return launch_attn<D, 2>(a, st);
-        case 4: return launch_attn<D, 4>(a, st);
-        case 8: return launch_attn<D, 8>(a, st);
-        case 16: return launch_attn<D, 16>(a, st);
-        case 24: return launch_attn<D, 24>(a, st);
-        default: return launch_attn<D, 32>(a, st);
+        case 1: return launch_attn<D, 1>(a, nz, st);
+        case 2: return launch_attn<D, 2>(a, nz, st);
+        case 4: return launch_attn<D, 4>(a, nz, st);
+        case 8: return launch_attn<D, 8>(a, nz, st);
+        case 16: return launch_attn<D, 16>(a, nz, st);
+        case 24: return launch_attn<D, 24>(a, nz, st);
+        default: return launch_attn<D, 32>(a, nz, st);
     }
 }
 
@@ -692,7 +697,7 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
     const size_t off_stat = (score_floats + pad - 1) / pad * pad;
     const size_t off_gstat = off_stat + (stat_floats + pad - 1) / pad * pad;
     const size_t off_part = off_gstat + ((size_t)Hkv * rb_full * 2 + pad - 1) / pad * pad;
-    int rc = split_scratch(st, off_part + part_floats, 2 * (size_t)Hkv, &P, &T, fn);
+    int rc = split_scratch(st, off_part + part_floats, 8 * (size_t)Hkv, &P, &T, fn);
     if (rc != ECPU_OK) return rc;
 
     AttnArgs a;
@@ -721,7 +726,7 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
         a.s0 = s0;
         a.S = std::min(per, S - s0);
         const int R = a.S * rep;
-        const int rb = row_bucket(R);
+        int rb = row_bucket(R);
         a.L = a.new0 + s0 + a.S;
         a.Lp = (a.L + kChunk - 1) / kChunk * kChunk;
         a.nchunk = a.Lp / kChunk;
@@ -735,10 +740,22 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
         a.write_cache = k_cache != nullptr ? 1 : 0;
         // scores keep the first launch's row stride so the regions stay in bounds
         if (rb > rb_full) return fail(ECPU_ERR_DEVICE, "%s: internal row bucket", fn);
+        // More than 8 rows per kv head: row groups of 8 on the grid's third
+        // dimension, each rereading the kv head's K and V, where the grid is
+        // small or the sequence's K and V stay in the 256 MB last-level cache
+        // (8B MTP verify, 5 tokens x 4 heads: 4096 positions 87.7 -> 43.0 us,
+        // 32768: 246 -> 159 us, 384: 72 -> 26 us)
+        int nz = 1;
+        const int env_rg = env_int("PILM_HIP_ATTN_ROWGROUPS", 1);   // 0 never, 2 always
+        const size_t kv_bytes = (size_t)a.L * Hkv * D * 2 * 2;
+        if (rb > 8 && env_rg != 0 && (env_rg == 2 || a.nchunk * Hkv < 512 || kv_bytes <= ((size_t)192 << 20))) {
+            nz = (R + 7) / 8;
+            rb = 8;
+        }
         switch (D) {
-            case 64: rc = launch_attn_rb<64>(rb, a, st); break;
-            case 128: rc = launch_attn_rb<128>(rb, a, st); break;
-            default: rc = launch_attn_rb<256>(rb, a, st); break;
+            case 64: rc = launch_attn_rb<64>(rb, nz, a, st); break;
+            case 128: rc = launch_attn_rb<128>(rb, nz, a, st); break;
+            default: rc = launch_attn_rb<256>(rb, nz, a, st); break;
         }
         if (rc != ECPU_OK) return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the attention kernel failed", fn);
         rc = check_launch(fn);

@@ -117,6 +117,18 @@ def test_short_context_two_launch_path(case, dev, monkeypatch):
     _check(out, ref, str(case))
 
 
+@pytest.mark.parametrize("case", [c for c in CASES if c[0] * (c[1] // c[2]) > 8],
+                         ids=lambda c: "S{}_H{}_kv{}_D{}_L{}".format(*c))
+def test_without_row_groups(case, dev, monkeypatch):
+    """More than 8 query rows per kv head run as row groups of 8 on small
+    grids; the single-group kernels (16, 24 or 32 rows) give the same results."""
+    monkeypatch.setenv("PILM_HIP_ATTN_ROWGROUPS", "0")
+    S, H, Hkv, D, L, BS, gate = case
+    _say(f"[gpu] attention one row group {case}")
+    out, ref = _run_both(dev, S, H, Hkv, D, L, BS, True, gate, seed=S * 100003 + L)
+    _check(out, ref, str(case))
+
+
 @pytest.mark.parametrize("S,H,Hkv,D", [(1, 16, 8, 128), (33, 16, 8, 128), (7, 32, 8, 64)])
 def test_no_cache_prefill(S, H, Hkv, D, dev):
     """attention.py:115-116: the rows attend to each other only (causal)."""
