@@ -740,17 +740,28 @@ int run_paged_attention(const ekernel_paged_attention_desc_t *d, const uint16_t 
         a.write_cache = k_cache != nullptr ? 1 : 0;
         // scores keep the first launch's row stride so the regions stay in bounds
         if (rb > rb_full) return fail(ECPU_ERR_DEVICE, "%s: internal row bucket", fn);
-        // More than 8 rows per kv head: row groups of 8 on the grid's third
-        // dimension, each rereading the kv head's K and V, where the grid is
-        // small or the sequence's K and V stay in the 256 MB last-level cache
-        // (8B MTP verify, 5 tokens x 4 heads: 4096 positions 87.7 -> 43.0 us,
-        // 32768: 246 -> 159 us, 384: 72 -> 26 us)
+        // Query rows in groups on the grid's third dimension, each group
+        // rereading the kv head's K and V: more than 8 rows go in groups of 8
+        // where the grid is small or the sequence's K and V stay in the 256 MB
+        // last-level cache, and groups halve while the grid has fewer than
+        // 512 workgroups (one per kv head and group for the one-launch
+        // kernel, one per chunk for the two-launch one).  Measured: 8B MTP
+        // verify (5 tokens x 4 heads) at 4096 positions 87.7 -> 33.6 us, at
+        // 32768 246 -> 161 us; 8B decode at 384 positions 18.0 -> 12.1 us;
+        // 1.7B 4-token verify at 4096 41.3 -> 27.1 us.
         int nz = 1;
-        const int env_rg = env_int("PILM_HIP_ATTN_ROWGROUPS", 1);   // 0 never, 2 always
-        const size_t kv_bytes = (size_t)a.L * Hkv * D * 2 * 2;
-        if (rb > 8 && env_rg != 0 && (env_rg == 2 || a.nchunk * Hkv < 512 || kv_bytes <= ((size_t)192 << 20))) {
-            nz = (R + 7) / 8;
-            rb = 8;
+        const int env_rg = env_int("PILM_HIP_ATTN_ROWGROUPS", 1);   // 0 never, 2 always (groups of 8)
+        if (env_rg != 0) {
+            const size_t kv_bytes = (size_t)a.L * Hkv * D * 2 * 2;
+            const bool one_launch = a.L <= kSmallL;
+            const size_t base = one_launch ? (size_t)Hkv : (size_t)a.nchunk * Hkv;
+            int g = rb;
+            if (rb > 8 && (env_rg == 2 || base < 512 || kv_bytes <= ((size_t)192 << 20))) g = 8;
+            if (env_rg != 2)
+                while (g > 1 && (size_t)((R + g - 1) / g) * base < 512) g /= 2;
+            g = row_bucket(g);
+            nz = (R + g - 1) / g;
+            rb = g;
         }
         switch (D) {
             case 64: rc = launch_attn_rb<64>(rb, nz, a, st); break;
