@@ -732,13 +732,18 @@ static int run_bcast(int fmt, size_t M, size_t N, size_t K, const void *A, const
     // two group-quad launches (4 + 1 rows) win (g32 1024x4096: 22.1 vs 26.7
     // us, 2048x6144: 32.6 vs 39.4 us)
     const bool five_gq = reduced && pl4_parked <= 2 && env_win != 1 && M == 5 && N <= 6144 && K <= 8192;
+    // up to four rows stay here (windowed) when the 8-row group-quad kernel
+    // could not take them in one launch (its LDS: rings, the rows, 8 rows'
+    // scales and block sums; g32 4096x12288 M=4: 3 + 1 rows, 86 us)
+    const bool gq8_one = (size_t)32768 + M * K * 2 + (size_t)8 * G * 4 * (1 + M) <= kMaxLds;
+    const bool keep_small = win4 && !gq8_one;
     const size_t waves8 = ntiles * pl8 * ((M + 7) / 8), waves4 = ntiles * pl4 * ((M + 3) / 4);
     const size_t pad8 = (M + 7) / 8 * 8, pad4 = (M + 3) / 4 * 4;   // rows computed, padding included
     int mt = (pad8 <= pad4 && waves8 >= 1536) ? 8 : 4;
     const int env_mt = env_int("PILM_HIP_BCAST_MT", 0);
     if (env_mt == 4 || env_mt == 8)
         mt = env_mt;
-    else if ((M <= 4 && (waves4 < 768 || N <= 6144)) || (M <= 8 && cramped) || five_gq)
+    else if ((M <= 4 && (waves4 < 768 || N <= 6144) && !keep_small) || (M <= 8 && cramped) || five_gq)
         return ECPU_ERR_UNSUPPORTED;
     const int pl = mt == 8 ? pl8 : pl4, sps = mt == 8 ? sps8 : sps4;
     const bool win = mt == 8 ? win8 : win4;
