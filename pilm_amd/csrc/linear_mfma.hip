@@ -355,8 +355,8 @@ void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const floa
     }
 }
 
-// Output tile per workgroup: 256 x 128 (waves 2 x 2 of 128 x 64) from M =
-// 2048, 128 x 128 from 128, 64 x 128 below (measured).
+// Output tile per workgroup: 128 x 128 (waves 2 x 2 of 64 x 64) from M =
+// 128, 64 x 128 below; 256 x 128 on request (PILM_HIP_MFMA_BM).
 template <int FMT>
 void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, const uint8_t *W, const float *S,
                      void *C, float *P, int splits, int sps, int M, int N, int K) {
@@ -382,7 +382,12 @@ bool mfma_supports(size_t K, const void *A, const uint8_t *W) {
 int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn) {
     if (!mfma_supports(K, A, W)) return fail(ECPU_ERR_UNSUPPORTED, "%s: shape not taken by the matrix-core path", fn);
-    const int bm = M >= 2048 ? 256 : (M >= 128 ? 128 : 64);
+    // 128-row tiles from M = 128 (256-row tiles at M = 2048 measured no
+    // faster for W4 and slower for W8A32: 8B gate_up 851 vs 926 us, down 450
+    // vs 551 us; W4 g128 down 287 vs 317 us), 64 below
+    int bm = M >= 128 ? 128 : 64;
+    const int env_bm = env_int("PILM_HIP_MFMA_BM", 0);
+    if (env_bm == 64 || env_bm == 128 || env_bm == 256) bm = env_bm;
     const size_t blocks = ((N + 127) / 128) * ((M + bm - 1) / bm);
     const int nsteps = (int)(K / kBK);
     // Split K while the output tiles alone leave the GPU under-filled: aim at

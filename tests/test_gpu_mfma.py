@@ -142,3 +142,18 @@ def test_continuous_batching_verify(fmt, nseq, dev):
         assert np.array_equal(y.view(np.uint8), per.view(np.uint8)), fmt
     else:
         check_close(fmt, y, per, f"{fmt} batched M={5 * nseq}")
+
+
+@pytest.mark.parametrize("bm", ["64", "128", "256"])
+@pytest.mark.parametrize("fmt", ["w8a32", "w4g128", "w4g32"])
+def test_mfma_tile_heights(bm, fmt, dev, monkeypatch):
+    """Every output-tile height (64, 128, 256 rows of M) stays within the
+    matrix-core tolerance, ragged M and N included."""
+    monkeypatch.setenv("PILM_HIP_MFMA_BM", bm)
+    gen = GV._gen()
+    m, n, k = 300, 1000, 2048
+    _say(f"[gpu] mfma tile {bm} {fmt} {m}x{n}x{k}")
+    x, w, s = gen.make_inputs(fmt, m, n, k, 8800 + int(bm))
+    y = run_gpu(fmt, x, w, s, dev)
+    ref = gen.run(fmt, x, w, s, "oracle")
+    check_close(fmt, y, ref, f"{fmt} BM={bm}")
