@@ -144,16 +144,18 @@ def test_continuous_batching_verify(fmt, nseq, dev):
         check_close(fmt, y, per, f"{fmt} batched M={5 * nseq}")
 
 
-@pytest.mark.parametrize("bm", ["64", "128", "256"])
-@pytest.mark.parametrize("fmt", ["w8a32", "w4g128", "w4g32"])
-def test_mfma_tile_heights(bm, fmt, dev, monkeypatch):
-    """Every output-tile height (64, 128, 256 rows of M) stays within the
-    matrix-core tolerance, ragged M and N included."""
+@pytest.mark.parametrize("bm,wm", [("64", "1"), ("64", "2"), ("128", "1"), ("128", "2"), ("256", "2")])
+@pytest.mark.parametrize("fmt", ["w8a32", "w4g128", "w4g32", "w4"])
+def test_mfma_tile_heights(bm, wm, fmt, dev, monkeypatch):
+    """Every output-tile height (64, 128, 256 rows of M) and wave layout
+    (1 x 4 or 2 x 2) stays within the matrix-core tolerance, ragged M and N
+    included."""
     monkeypatch.setenv("PILM_HIP_MFMA_BM", bm)
+    monkeypatch.setenv("PILM_HIP_MFMA_WM", wm)
     gen = GV._gen()
     m, n, k = 300, 1000, 2048
-    _say(f"[gpu] mfma tile {bm} {fmt} {m}x{n}x{k}")
-    x, w, s = gen.make_inputs(fmt, m, n, k, 8800 + int(bm))
+    _say(f"[gpu] mfma tile {bm} waves {wm} {fmt} {m}x{n}x{k}")
+    x, w, s = gen.make_inputs(fmt, m, n, k, 8800 + int(bm) + int(wm))
     y = run_gpu(fmt, x, w, s, dev)
     ref = gen.run(fmt, x, w, s, "oracle")
-    check_close(fmt, y, ref, f"{fmt} BM={bm}")
+    check_close(fmt, y, ref, f"{fmt} BM={bm} WM={wm}")
