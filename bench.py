@@ -37,6 +37,12 @@ Profiling helpers (rocprofv3 runs the program, these read its output):
                         the copy kernel; written to profiles/ and reported as
                         roofline.traffic while the kernel source is unchanged
   --stats-summary CSV   rocprofv3 --kernel-trace --stats output -> summary
+  --attn-pmc-pass       paged-attention calls (Qwen3-8B heads, one decode row,
+                        32768 positions) plus the copy kernel, for one
+                        counter pass
+  --attn-traffic F W    FETCH_SIZE / WRITE_SIZE CSVs of two such passes ->
+                        bytes per dispatch of each attention kernel beside
+                        the K or V bytes it must read
 """
 from __future__ import annotations
 
@@ -482,6 +488,72 @@ def pmc_pass(torch, dev, steps: int) -> None:
           f"{CALIB_BYTES} B", flush=True)
 
 
+ATTN_PMC_CASE = ("qwen3_8b", 32, 8, 1, 32768)   # model, H, Hkv, S, L (16-token blocks, D = 128)
+
+
+def attn_pmc_pass(torch, dev, calls: int) -> None:
+    """Eager paged-attention calls at one shape (Qwen3-8B heads, one decode
+    row over 32768 cached positions), then the plain copy kernel, so that
+    FETCH_SIZE / WRITE_SIZE per dispatch of each attention kernel can be set
+    against the K and V bytes it has to read."""
+    from pilm_amd import bindings as abi
+    _, h, hkv, s_rows, L = ATTN_PMC_CASE
+    bs, d = 16, 128
+    nblk = (L + bs - 1) // bs
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    kc = torch.randn(nblk, bs, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+    vc = torch.randn(nblk, bs, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+    ids = torch.randperm(nblk, device=dev, generator=gen).to(torch.int32)
+    q = torch.randn(s_rows, h, d, device=dev, generator=gen).to(torch.bfloat16)
+    kn = torch.randn(s_rows, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+    vn = torch.randn(s_rows, hkv, d, device=dev, generator=gen).to(torch.bfloat16)
+    qg = torch.randn(s_rows, h, 2 * d, device=dev, generator=gen).to(torch.bfloat16)
+    o = torch.empty(s_rows, h * d, device=dev, dtype=torch.bfloat16)
+    abi.set_stream(torch.cuda.current_stream().cuda_stream)
+    for _ in range(calls):
+        rc = abi.paged_attention_bf16_ptr(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                          ids.data_ptr(), qg.data_ptr() + 2 * d, o.data_ptr(),
+                                          s_rows, h, hkv, d, L, bs, nblk, nblk, 2 * d)
+        if rc != 0:
+            raise RuntimeError(f"ekernel_paged_attention_bf16 failed: rc={rc} ({abi.last_error()})")
+    torch.cuda.synchronize()
+    del kc, vc
+    torch.cuda.empty_cache()
+    x = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(f"[bench] attention pmc pass: {calls} calls S={s_rows} H={h} Hkv={hkv} D={d} L={L}, "
+          f"3 copy kernels of {CALIB_BYTES} B", flush=True)
+
+
+def attn_traffic_summary(fetch_csv: str, write_csv: str) -> dict:
+    """Bytes per dispatch of each attention kernel from the two counter runs
+    of attn_pmc_pass, scaled by the copy kernel's known size, beside the
+    bytes the kernel must move (K for the scores kernel, V for the P.V
+    kernel: L * Hkv * D * 2 each)."""
+    f = _counter_means(fetch_csv, "FETCH_SIZE")
+    w = _counter_means(write_csv, "WRITE_SIZE")
+    (cf, _), (cw, _) = _pick(f, "neg_kernel"), _pick(w, "neg_kernel")
+    ff, fw = CALIB_BYTES / (cf * 1024), CALIB_BYTES / (cw * 1024)
+    _, h, hkv, s_rows, L = ATTN_PMC_CASE
+    kv_one = L * hkv * 128 * 2
+    out = {"case": {"S": s_rows, "H": h, "Hkv": hkv, "D": 128, "L": L, "block_size": 16},
+           "fetch_factor": round(ff, 4), "write_factor": round(fw, 4)}
+    for needle in ("attn_scores_kernel", "attn_pv_kernel"):
+        hits = [k for k in f if needle in k]
+        if not hits:
+            continue
+        (kf, n) = _pick(f, needle)
+        (kw, _) = _pick(w, needle)
+        out[needle] = {"fetch_bytes": round(kf * 1024 * ff), "write_bytes": round(kw * 1024 * fw),
+                       "must_read_bytes": kv_one, "fetch_over_must": round(kf * 1024 * ff / kv_one, 4),
+                       "dispatches": n}
+    return out
+
+
 def _counter_means(csv_path: str, counter: str) -> dict:
     """{kernel name: mean counter value per dispatch} from a rocprofv3
     counter_collection.csv."""
@@ -571,6 +643,8 @@ def main(argv=None) -> int:
     ap.add_argument("--pmc-pass", action="store_true")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--stats-summary", metavar="STATS_CSV")
+    ap.add_argument("--attn-pmc-pass", action="store_true")
+    ap.add_argument("--attn-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args(argv)
     if args.traffic:
         rec = traffic_summary(*args.traffic)
@@ -587,6 +661,9 @@ def main(argv=None) -> int:
     if args.stats_summary:
         print(stats_summary(args.stats_summary))
         return 0
+    if args.attn_traffic:
+        print(json.dumps(attn_traffic_summary(*args.attn_traffic)))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: there is no multi-GPU path (asked for --gpus {args.gpus}); "
               "the decode GEMV would shard by output rows, each GPU holding W[N/G, K] and its scales",
@@ -600,6 +677,9 @@ def main(argv=None) -> int:
     dev = torch.device("cuda:0")
     if args.pmc_pass:
         pmc_pass(torch, dev, args.steps)
+        return 0
+    if args.attn_pmc_pass:
+        attn_pmc_pass(torch, dev, args.steps)
         return 0
     m = 1
     print(f"[bench] building step: {len(step_shapes())} W4A16-g128 linears, M={m}", flush=True)

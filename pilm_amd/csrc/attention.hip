@@ -165,19 +165,39 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     if (valid) {
         const auto *kp = gbl((const u32x4 *)kv_row<D>(a, a.k_cache, a.k_new, j, kvh));
         auto *dst = (a.write_cache && blockIdx.z == 0 && j >= a.new0 + a.s0) ? gbl_w((u32x4 *)cache_row<D>(a, a.k_cache, j, kvh)) : nullptr;
-#pragma unroll 2
-        for (int c = 0; c < D / 8; ++c) {
-            const u32x4 kv = kp[c];
-            if (dst) dst[c] = kv;
-            const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+        // The loads of a row go out a whole 128-byte line at a time: issued
+        // two by two with the dot in between, a line's later 16-byte pieces
+        // were asked for after other waves' traffic had evicted it from L2,
+        // and K came from HBM 1.9 times (8B decode, 32768 positions).  The
+        // cache store sits outside the dot: inside it, its branch split the
+        // line into blocks and the compiler hoisted every LDS read of q
+        // ahead of the FMAs (272 VGPRs at 4 rows, 76 now).
+        constexpr int kLine = 8;
+#pragma unroll 1
+        for (int c0 = 0; c0 < D / 8; c0 += kLine) {
+            u32x4 kv[kLine];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float k0 = bf16_lo(w[t]), k1 = bf16_hi(w[t]);
+            for (int i = 0; i < kLine; ++i) kv[i] = kp[c0 + i];
+            if (dst) {
 #pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t], k0, acc[r]);
-                    acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t + 1], k1, acc[r]);
+                for (int i = 0; i < kLine; ++i) dst[c0 + i] = kv[i];
+            }
+#pragma unroll
+            for (int i = 0; i < kLine; ++i) {
+                const int c = c0 + i;
+                const uint32_t w[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float k0 = bf16_lo(w[t]), k1 = bf16_hi(w[t]);
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t], k0, acc[r]);
+                        acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t + 1], k1, acc[r]);
+                    }
                 }
+                // (keeps the LDS reads of q beside their FMAs, not all
+                // hoisted ahead of the line)
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
