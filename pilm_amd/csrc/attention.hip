@@ -533,19 +533,32 @@ __global__ __launch_bounds__(kSmallL) void attn_small_kernel(AttnArgs a) {
 #pragma unroll 4
                 for (int c = 0; c < D / 8; ++c) vdst[c] = vsrc[c];
             }
-#pragma unroll 2
-            for (int c = 0; c < D / 8; ++c) {
-                const u32x4 kv = kp[c];
-                if (kdst) kdst[c] = kv;
-                const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+            // a whole 128-byte line of the key row per batch of loads, the
+            // cache store outside the dot (as in the score pass)
+            constexpr int kLine = 8;
+#pragma unroll 1
+            for (int c0 = 0; c0 < D / 8; c0 += kLine) {
+                u32x4 kv[kLine];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const float k0 = bf16_lo(w[t]), k1 = bf16_hi(w[t]);
+                for (int i = 0; i < kLine; ++i) kv[i] = kp[c0 + i];
+                if (kdst) {
 #pragma unroll
-                    for (int r = 0; r < RB; ++r) {
-                        acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t], k0, acc[r]);
-                        acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t + 1], k1, acc[r]);
+                    for (int i = 0; i < kLine; ++i) kdst[c0 + i] = kv[i];
+                }
+#pragma unroll
+                for (int i = 0; i < kLine; ++i) {
+                    const int c = c0 + i;
+                    const uint32_t w[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float k0 = bf16_lo(w[t]), k1 = bf16_hi(w[t]);
+#pragma unroll
+                        for (int r = 0; r < RB; ++r) {
+                            acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t], k0, acc[r]);
+                            acc[r] = __builtin_fmaf(qs[r * D + 8 * c + 2 * t + 1], k1, acc[r]);
+                        }
                     }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
