@@ -254,6 +254,16 @@ int eram_hip_load_file(const char *path, size_t n, const size_t *file_offsets, c
 int ecpu_hip_set_stream(void *hip_stream);
 void *ecpu_hip_get_stream(void);
 
+/* Activation rows from which the linear entry points use the matrix-core
+ * GEMM (fp16 operands, within 1e-2 of the reference per output row) instead
+ * of the bit-exact kernels.  rows >= 0 sets it for the process (0 = never);
+ * rows < 0 returns to PILM_HIP_MFMA_MIN_M (default 64).  A caller that needs
+ * the reference's bits at any M -- e.g. a batched MTP verify whose tokens
+ * must equal per-sequence verification -- sets it above its M.  Not per
+ * thread: calls in flight on other threads see the change. */
+int ecpu_hip_set_matrix_core_min_rows(int rows);
+int ecpu_hip_matrix_core_min_rows(void);
+
 /* Per-call GPU timing of the linear entry points, the native counterpart of
  * the per-linear stage profiler in src/models/base/linear.py:148-169.
  * Between begin and end every linear call records a HIP event pair on its
@@ -298,6 +308,90 @@ int ekernel_paged_attention_bf16(const ekernel_paged_attention_desc_t *desc, con
                                  const uint16_t *k_new, const uint16_t *v_new, uint16_t *k_cache,
                                  uint16_t *v_cache, const int32_t *block_ids, const uint16_t *gate,
                                  uint16_t *out);
+
+/* ---- one Qwen3 decoder layer's torch steps on device (no C counterpart: the
+ * reference runs them in torch on the CPU, src/models/base/layers.py:101-195,
+ * src/models/qwen3/attention.py:82-139, src/models/qwen3/model.py:54-70).
+ * Each reproduces the reference's torch CPU roundings bit for bit (torch's
+ * CPU summation orders, SLEEF's expf_u10, bf16 intermediates); the fixture
+ * they are checked against was written with torch's AVX2 kernels and oneDNN
+ * off, the reference's measured platform. --------------------------------- */
+typedef struct {
+    size_t rows;         /* rows of x */
+    size_t hidden;       /* elements per row, 32 .. 8192 */
+    float eps;           /* GemmaRMSNorm eps (layers.py:138) */
+} ekernel_rmsnorm_desc_t;
+
+/* GemmaRMSNorm (layers.py:130-147) of each row, optionally after the residual
+ * add of TransformerBlock.forward (model.py:63-69): h = bf16(x + residual)
+ * (h = x when residual is NULL), residual_out = h (when not NULL),
+ * out = bf16(bf16(weight + 1) * bf16(h * (1 / sqrt(mean(h^2) + eps)))), the
+ * mean summed in torch's CPU order.  All bf16 [rows, hidden]; out and
+ * residual_out may alias x or residual row for row. */
+int ekernel_rmsnorm_gemma_bf16(const ekernel_rmsnorm_desc_t *desc, const uint16_t *x, const uint16_t *residual,
+                               const uint16_t *weight, uint16_t *out, uint16_t *residual_out);
+
+typedef struct {
+    size_t S;              /* tokens of this step */
+    size_t n_heads, n_kv_heads, head_dim;
+    size_t rot_dim;        /* rotated leading dims (head_dim * partial_rotary_factor) */
+    size_t q_stride;       /* elements between consecutive tokens' rows of qg */
+    size_t kv_stride;      /* ... of k and of v */
+    size_t pos0;           /* position of the first token (ignored when step is given) */
+    size_t max_positions;  /* rows of the cos / sin tables */
+    size_t block_size, num_blocks, n_block_ids;
+    float eps;             /* q_norm / k_norm eps */
+} ekernel_qk_rope_desc_t;
+
+/* FullAttention.forward up to the cache write (attention.py:82-97): per token
+ * s and head h, q_out[s, h, :] = rope(GemmaRMSNorm(qg[s, h*2D : h*2D + D])),
+ * and per kv head the roped, normalized k[s, kh*D ...] and v[s, kh*D ...]
+ * stored at position p = pos0 + s of the paged caches [num_blocks,
+ * block_size, n_kv_heads, D] (block block_ids[p / block_size], slot p %
+ * block_size).  Rope is apply_rope's (layers.py:150-195) with the fp32
+ * tables cos/sin [max_positions, rot_dim/2] the caller builds as
+ * _rope_cos_sin does.  step (device int32, may be NULL): step[0] replaces
+ * pos0, so a captured graph can advance it. */
+int ekernel_qk_norm_rope_bf16(const ekernel_qk_rope_desc_t *desc, const uint16_t *qg, const uint16_t *k,
+                              const uint16_t *v, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                              const float *cos_table, const float *sin_table, const int32_t *step,
+                              uint16_t *q_out, uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids);
+
+typedef struct {
+    size_t S, n_heads, n_kv_heads, head_dim;   /* head_dim 64, 128 or 256 */
+    size_t cache_len;      /* positions once this step's S tokens are cached (ignored when step is given) */
+    size_t block_size, num_blocks, n_block_ids;
+    size_t gate_row_stride;    /* elements between tokens' gates (0 with gate NULL) */
+    size_t gate_head_stride;   /* elements between heads' gates */
+} ekernel_attention_exact_desc_t;
+
+/* attention.py:99-139 over the paged cache (the step's rows already stored):
+ * out[s, h*D + d] = bf16(P.V) * bf16(sigmoid(gate[s*gate_row_stride +
+ * h*gate_head_stride + d])) with the bf16 scores bf16(bf16(q.k) * (1/sqrt D)),
+ * the causal mask j <= cache_len - S + s, fp32 softmax rounded to bf16, and
+ * kv head h / (n_heads / n_kv_heads); every sum in torch's CPU order, so the
+ * output is bit-identical to the reference's.  step (device int32, may be
+ * NULL): step[1] replaces cache_len (clamped to [S, n_block_ids *
+ * block_size]).  Block ids outside [0, num_blocks) are clamped, never read
+ * out of bounds.  Up to 64 KB of LDS: (n_heads / n_kv_heads) x n_block_ids x
+ * block_size positions of scores. */
+int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, const uint16_t *q,
+                                 const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *block_ids,
+                                 const uint16_t *gate, const int32_t *step, uint16_t *out);
+
+/* out[m, i] = bf16(bf16(silu(gate[m*in_stride + i])) * up[m*in_stride + i])
+ * (F.silu(gate(x)) * up(x), layers.py:188-193), m < rows, i < n. */
+int ekernel_silu_mul_bf16(const uint16_t *gate, const uint16_t *up, size_t rows, size_t n, size_t in_stride,
+                          uint16_t *out);
+
+/* Greedy decode step on device: id = argmax of the bf16 logits[n] (the first
+ * index of the largest value, as torch.argmax picks it for finite logits,
+ * src/engine.py:551); then tokens[state[2]] = id (while state[2] <
+ * max_tokens), state[2] += 1, *next_id = id, state[0] = state[1],
+ * state[1] += 1 (state = {pos0, cache_len, count}, the decode position
+ * advancing for the next step). */
+int ekernel_greedy_step_bf16(const uint16_t *logits, size_t n, int32_t *state, int32_t *tokens, size_t max_tokens,
+                             int64_t *next_id);
 
 #ifdef __cplusplus
 }

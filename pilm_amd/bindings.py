@@ -43,6 +43,11 @@ _OPTIONAL_KERNEL_SYMBOLS = [
     "ekernel_rmsnorm_bf16",
     "ekernel_gated_delta_recurrent_f32",
     "ekernel_paged_attention_bf16",
+    "ekernel_rmsnorm_gemma_bf16",
+    "ekernel_qk_norm_rope_bf16",
+    "ekernel_attention_exact_bf16",
+    "ekernel_silu_mul_bf16",
+    "ekernel_greedy_step_bf16",
 ]
 
 DEFAULT_LIB = Path(__file__).resolve().parent / "lib" / "libecpu.so"
@@ -152,6 +157,24 @@ class EkernelPagedAttentionDesc(ctypes.Structure):
     ]
 
 
+class EkernelRmsnormDesc(ctypes.Structure):
+    """ekernel_rmsnorm_desc_t (no C counterpart: layers.py:130-147 runs in torch)."""
+    _fields_ = [("rows", ctypes.c_size_t), ("hidden", ctypes.c_size_t), ("eps", ctypes.c_float)]
+
+
+class EkernelQkRopeDesc(ctypes.Structure):
+    """ekernel_qk_rope_desc_t (attention.py:82-97)."""
+    _fields_ = [(n, ctypes.c_size_t) for n in ("S", "n_heads", "n_kv_heads", "head_dim", "rot_dim", "q_stride",
+                                               "kv_stride", "pos0", "max_positions", "block_size", "num_blocks",
+                                               "n_block_ids")] + [("eps", ctypes.c_float)]
+
+
+class EkernelAttentionExactDesc(ctypes.Structure):
+    """ekernel_attention_exact_desc_t (attention.py:99-139)."""
+    _fields_ = [(n, ctypes.c_size_t) for n in ("S", "n_heads", "n_kv_heads", "head_dim", "cache_len", "block_size",
+                                               "num_blocks", "n_block_ids", "gate_row_stride", "gate_head_stride")]
+
+
 _LINEAR_ARGTYPES = [ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p,
                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
 
@@ -219,6 +242,25 @@ def _configure(lib):
         lib.ekernel_paged_attention_bf16.argtypes = [ctypes.POINTER(EkernelPagedAttentionDesc)] + \
             [ctypes.c_void_p] * 8
         lib.ekernel_paged_attention_bf16.restype = ctypes.c_int
+    if hasattr(lib, "ekernel_rmsnorm_gemma_bf16"):
+        lib.ekernel_rmsnorm_gemma_bf16.argtypes = [ctypes.POINTER(EkernelRmsnormDesc)] + [ctypes.c_void_p] * 5
+        lib.ekernel_rmsnorm_gemma_bf16.restype = ctypes.c_int
+        lib.ekernel_qk_norm_rope_bf16.argtypes = [ctypes.POINTER(EkernelQkRopeDesc)] + [ctypes.c_void_p] * 12
+        lib.ekernel_qk_norm_rope_bf16.restype = ctypes.c_int
+        lib.ekernel_attention_exact_bf16.argtypes = [ctypes.POINTER(EkernelAttentionExactDesc)] + \
+            [ctypes.c_void_p] * 7
+        lib.ekernel_attention_exact_bf16.restype = ctypes.c_int
+        lib.ekernel_silu_mul_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                              ctypes.c_size_t, ctypes.c_void_p]
+        lib.ekernel_silu_mul_bf16.restype = ctypes.c_int
+        lib.ekernel_greedy_step_bf16.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.ekernel_greedy_step_bf16.restype = ctypes.c_int
+    if hasattr(lib, "ecpu_hip_set_matrix_core_min_rows"):
+        lib.ecpu_hip_set_matrix_core_min_rows.argtypes = [ctypes.c_int]
+        lib.ecpu_hip_set_matrix_core_min_rows.restype = ctypes.c_int
+        lib.ecpu_hip_matrix_core_min_rows.argtypes = []
+        lib.ecpu_hip_matrix_core_min_rows.restype = ctypes.c_int
     if hasattr(lib, "ecpu_hip_set_stream"):
         lib.ecpu_hip_set_stream.argtypes = [ctypes.c_void_p]
         lib.ecpu_hip_set_stream.restype = ctypes.c_int
@@ -241,31 +283,13 @@ ECPU_PRECISION_I4 = 6
 ISA_NAMES = {0: "scalar", 1: "avx2", 2: "avx512", 3: "amx", 4: "neon", 5: "sve", 6: "gfx950"}
 
 
-def init(device_type=EDEV_HIP, n_threads=0, kv_cache_budget=4 * 1024**3):
+def library_info() -> dict:
+    """What the loaded library is: its path, version string, the ISA it
+    reports, and which of the optional entry points it exports."""
     lib = _load_lib()
-    cfg = lib.ecpu_config_default()
-    cfg.device_type = device_type
-    cfg.n_threads = n_threads
-    cfg.kv_cache_budget_bytes = kv_cache_budget
-    rc = lib.ecpu_init(ctypes.byref(cfg))
-    if rc != 0:
-        err = lib.ecpu_last_error()
-        raise RuntimeError(f"ecpu_init failed ({rc}): {err.decode() if err else 'unknown'}")
-    return lib
-
-
-def version():
-    return _load_lib().ecpu_version().decode()
-
-
-def detect_isa():
-    lib = _load_lib()
-    return ISA_NAMES.get(lib.ekernel_detect_isa(), "unknown")
-
-
-def library_path():
-    _load_lib()
-    return _lib_path
+    return {"path": _lib_path, "version": lib.ecpu_version().decode(),
+            "isa": ISA_NAMES.get(lib.ekernel_detect_isa(), "unknown"),
+            "entry_points": {name: hasattr(lib, name) for name in _OPTIONAL_KERNEL_SYMBOLS}}
 
 
 def last_error() -> str | None:
@@ -306,6 +330,15 @@ def set_stream(stream_handle: int) -> None:
     _load_lib().ecpu_hip_set_stream(ctypes.c_void_p(stream_handle or None))
 
 
+def set_matrix_core_min_rows(rows: int) -> None:
+    """Rows from which linears use the matrix cores (0 = never; < 0 = default)."""
+    _load_lib().ecpu_hip_set_matrix_core_min_rows(int(rows))
+
+
+def matrix_core_min_rows() -> int:
+    return int(_load_lib().ecpu_hip_matrix_core_min_rows())
+
+
 def profile_begin() -> None:
     """Start recording a HIP event pair around every linear call."""
     _load_lib().ecpu_hip_profile_begin()
@@ -327,17 +360,6 @@ def profile_read() -> dict:
         name, calls, ms, nbytes, flops = line.split()
         out[name] = {"calls": int(calls), "ms": float(ms), "bytes": float(nbytes), "flops": float(flops)}
     return out
-
-
-def gemm_f32_ptr(a_ptr: int, b_ptr: int, c_ptr: int, m: int, n: int, k: int,
-                 transpose_a: bool = False, transpose_b: bool = False, isa: int | None = None) -> int:
-    lib = _load_lib()
-    if isa is None:
-        isa = lib.ekernel_detect_isa()
-    desc = EkernelGemmDesc(m, n, k, ECPU_PRECISION_F32, ECPU_PRECISION_F32, ECPU_PRECISION_F32,
-                           int(transpose_a), int(transpose_b))
-    return lib.ekernel_gemm(ctypes.byref(desc), ctypes.c_void_p(a_ptr), ctypes.c_void_p(b_ptr),
-                            ctypes.c_void_p(c_ptr), int(isa))
 
 
 def _linear_ptr(name: str, a_ptr: int, w_ptr: int, scales_ptr: int, c_ptr: int, m: int, n: int, k: int,

@@ -13,6 +13,7 @@ weight lives on.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Tuple
 
 import torch
@@ -63,7 +64,11 @@ def gemm_f32(a: torch.Tensor, b: torch.Tensor, transpose_b: bool = False) -> tor
         raise ValueError(f"incompatible GEMM shapes: a={tuple(a.shape)} b={tuple(b.shape)} transpose_b={transpose_b}")
     out = torch.empty((m, n), dtype=torch.float32, device=a.device)
     _bind_stream(a)
-    rc = abi.gemm_f32_ptr(a.data_ptr(), b.data_ptr(), out.data_ptr(), m, n, k, False, transpose_b)
+    desc = abi.EkernelGemmDesc(m, n, k, abi.ECPU_PRECISION_F32, abi.ECPU_PRECISION_F32, abi.ECPU_PRECISION_F32,
+                               0, int(transpose_b))
+    lib = abi._load_lib()
+    rc = lib.ekernel_gemm(ctypes.byref(desc), ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                          ctypes.c_void_p(out.data_ptr()), lib.ekernel_detect_isa())
     if rc != 0:
         raise _rc_error("ekernel_gemm", rc)
     return out
@@ -99,6 +104,16 @@ def _require_2d(name: str, weight: torch.Tensor) -> None:
         raise ValueError(f"{name} must be 2D, got shape={tuple(weight.shape)}")
 
 
+def _div32(a: torch.Tensor, b) -> torch.Tensor:
+    """The correctly rounded fp32 quotient, as torch's CPU division gives it,
+    on any device: the quotient of the fp32 operands in fp64, rounded once to
+    fp32 (fp64 carries more than 2 x 24 + 2 bits, so rounding twice equals
+    rounding once).  torch on the GPU divides by a Python scalar through its
+    reciprocal, which rounds differently."""
+    b = b.to(torch.float64) if isinstance(b, torch.Tensor) else float(b)
+    return (a.to(torch.float64) / b).to(torch.float32)
+
+
 def quantize_weight_i8_per_row(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """ckernel.py:70-75: scale = max|w|/127 (>= 1e-8), round half-even, clamp +-127."""
     if weight.dtype != torch.float32:
@@ -106,8 +121,8 @@ def quantize_weight_i8_per_row(weight: torch.Tensor) -> tuple[torch.Tensor, torc
     _require_2d("weight", weight)
     weight = weight.contiguous()
     max_abs = weight.abs().amax(dim=1)
-    scales = torch.clamp(max_abs / 127.0, min=1e-8).to(torch.float32)
-    qweight = torch.round(weight / scales.unsqueeze(1)).clamp(-127, 127).to(torch.int8).contiguous()
+    scales = torch.clamp(_div32(max_abs, 127.0), min=1e-8).to(torch.float32)
+    qweight = torch.round(_div32(weight, scales.unsqueeze(1))).clamp(-127, 127).to(torch.int8).contiguous()
     return qweight, scales.contiguous()
 
 
@@ -146,8 +161,8 @@ def quantize_weight_i4_per_row_chunked(weight: torch.Tensor, rows_per_chunk: int
         end = min(start + rows_per_chunk, rows)
         chunk = weight[start:end].to(torch.float32).contiguous()
         max_abs = chunk.abs().amax(dim=1)
-        chunk_scales = torch.clamp(max_abs / 7.0, min=1e-8).to(torch.float32)
-        q = torch.round(chunk / chunk_scales.unsqueeze(1)).clamp(-7, 7).to(torch.int16)
+        chunk_scales = torch.clamp(_div32(max_abs, 7.0), min=1e-8).to(torch.float32)
+        q = torch.round(_div32(chunk, chunk_scales.unsqueeze(1))).clamp(-7, 7).to(torch.int16)
         qweight[start:end].copy_(_pack_nibbles(q))
         scales[start:end].copy_(chunk_scales)
     return qweight.contiguous(), scales.contiguous()
@@ -172,8 +187,8 @@ def quantize_weight_i4_grouped_chunked(weight: torch.Tensor, group_size: int = 3
             chunk = torch.nn.functional.pad(chunk, (0, groups * group_size - cols))
         grouped = chunk.reshape(end - start, groups, group_size)
         max_abs = grouped.abs().amax(dim=2)
-        chunk_scales = torch.clamp(max_abs / 7.0, min=1e-8).to(torch.float32)
-        q = torch.round(grouped / chunk_scales.unsqueeze(2)).clamp(-7, 7).to(torch.int16)
+        chunk_scales = torch.clamp(_div32(max_abs, 7.0), min=1e-8).to(torch.float32)
+        q = torch.round(_div32(grouped, chunk_scales.unsqueeze(2))).clamp(-7, 7).to(torch.int16)
         q = q.reshape(end - start, groups * group_size)[:, :cols]
         qweight[start:end].copy_(_pack_nibbles(q))
         scales[start:end].copy_(chunk_scales)
@@ -351,6 +366,30 @@ def swiglu_bf16(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     rc = abi.swiglu_bf16_ptr(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel())
     if rc != 0:
         raise _rc_error("ekernel_swiglu_bf16", rc)
+    return out
+
+
+def silu_mul_bf16(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """torch.nn.functional.silu(gate) * up on bf16 tensors with the roundings
+    of torch's CPU kernels (silu rounded to bf16, then the product): the
+    reference's default activation between gate/up and down (linear.py:408-421,
+    534-545), on the device."""
+    if gate.device.type != _GPU or up.device.type != _GPU:
+        raise ValueError("gate and up must be GPU tensors")
+    if gate.dtype != torch.bfloat16 or up.dtype != torch.bfloat16:
+        raise ValueError("gate and up must be torch.bfloat16")
+    if tuple(gate.shape) != tuple(up.shape):
+        raise ValueError(f"gate/up shapes differ: gate={tuple(gate.shape)} up={tuple(up.shape)}")
+    _same_device(gate, up)
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    n = gate.shape[-1] if gate.ndim else 1
+    rows = gate.numel() // max(n, 1)
+    _bind_stream(gate)
+    rc = abi._load_lib().ekernel_silu_mul_bf16(ctypes.c_void_p(gate.data_ptr()), ctypes.c_void_p(up.data_ptr()),
+                                               rows, n, n, ctypes.c_void_p(out.data_ptr()))
+    if rc != 0:
+        raise _rc_error("ekernel_silu_mul_bf16", rc)
     return out
 
 

@@ -1,0 +1,580 @@
+// The elementwise and attention steps of one Qwen3 decoder layer on gfx950,
+// with the roundings of piLM's torch CPU path (src/models/base/layers.py:101-176,
+// src/models/qwen3/attention.py:95-139, src/models/qwen3/model.py:10-127).
+//
+// piLM runs these steps in torch on the CPU.  Greedy tokens of a random-init
+// model sit on bf16 near-ties, so every rounding of that path is kept here:
+//   * sums in torch's CPU orders: the reduction of `mean` over a contiguous
+//     row (eight-float vectors, four interleaved accumulators, a cascade of
+//     16-row levels, then the lanes in order), the softmax's lane reduction
+//     (chains j mod 8 folded ((0+4)+(2+6))+((1+5)+(3+7))), the score dot of
+//     the bf16 batched product (a halving tree: element i paired with
+//     i + D/2, then i + D/4, ...), and its P.V dot (four accumulators on
+//     j mod 4, the tail on the first, folded in order);
+//   * exp as torch's CPU kernels compute it for softmax, sigmoid and silu
+//     (SLEEF's expf_u10, restated below from its published algorithm);
+//   * every intermediate tensor rounded to bf16 where torch's is bf16, every
+//     fp32 product and sum rounded separately (no contraction), true division
+//     and square root.
+// The products of two bf16 values are exact in fp32, so an FMA there rounds
+// exactly like torch's separate multiply and add.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "gemv_device.h"
+#include "internal.h"
+
+#pragma clang fp contract(off)
+
+namespace pilm {
+
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float bfr(float x) { return bf(f32_to_bf16(x)); }   // round to bf16, as float
+__device__ __forceinline__ float sq(float x) { return x * x; }
+
+// Correctly rounded square root of a positive normal float.  v_sqrt_f32 is
+// within one ulp of it; of s and its two neighbours, the residuals
+// x - s_dn * s and x - s_up * s (exact through FMA) decide which one the true
+// root rounds to, as in the correctly rounded sqrt expansions.
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float dn = __int_as_float(__float_as_int(s) - 1);
+    const float up = __int_as_float(__float_as_int(s) + 1);
+    float r = s;
+    if (__builtin_fmaf(-dn, s, x) <= 0.0f) r = dn;
+    if (__builtin_fmaf(-up, s, x) > 0.0f) r = up;
+    return r;
+}
+
+// SLEEF expf_u10 (sleefsimdsp.c xexpf): q = rint(d / ln 2), Cody-Waite
+// reduction with the two-part ln 2, a degree-6 polynomial in FMA Horner form,
+// 1 + s + s^2 u, scaled by 2^q in two halves; 0 below -104, inf above 100.
+__device__ __forceinline__ float sleef_expf(float d) {
+    const float q = rintf(d * 1.442695040888963407359924681001892137426645954152985934135449406931f);
+    const int qi = (int)q;
+    float s = __builtin_fmaf(q, -0.693145751953125f, d);
+    s = __builtin_fmaf(q, -1.428606765330187045e-06f, s);
+    float u = 0.000198527617612853646278381f;
+    u = __builtin_fmaf(u, s, 0.00139304355252534151077271f);
+    u = __builtin_fmaf(u, s, 0.00833336077630519866943359f);
+    u = __builtin_fmaf(u, s, 0.0416664853692054748535156f);
+    u = __builtin_fmaf(u, s, 0.166666671633720397949219f);
+    u = __builtin_fmaf(u, s, 0.5f);
+    const float ss = s * s;
+    u = 1.0f + __builtin_fmaf(ss, u, s);
+    const int q1 = qi >> 1;
+    u = u * __int_as_float((q1 + 127) << 23);
+    u = u * __int_as_float((qi - q1 + 127) << 23);
+    if (d < -104.0f) u = 0.0f;
+    if (d > 100.0f) u = __builtin_inff();
+    return u;
+}
+
+// torch's sum of the squares of n contiguous fp32 values (n >= 32; the
+// squares of bf16 values are exact, as x.pow(2) stores them): chain t (t < 32) of a
+// workgroup's first wave owns lane l = t & 7 of the vectors v = 4r + k, k =
+// t >> 3, accumulated through the 16-row level cascade; the 32 chain values,
+// the vectors left over by the four-way interleave and the scalar tail are
+// then folded by one lane in torch's order.  `x` is in LDS; `tmp` holds 32
+// floats of LDS.  Every thread of the workgroup calls it (it synchronizes)
+// and gets the sum.
+__device__ float torch_row_sumsq(const float *x, int n, float *tmp, float *result) {
+    const int t = threadIdx.x;
+    const int nvec = n / 8, size_ilp = nvec / 4;
+    if (t < 32) {
+        const int k = t >> 3, l = t & 7;
+        int clog = 0;
+        while ((1 << clog) < size_ilp) ++clog;
+        const int level_power = max(4, clog / 4);
+        const int step = 1 << level_power, mask = step - 1;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        int r = 0;
+        while (r + step <= size_ilp) {
+            for (int j = 0; j < step; ++j, ++r) acc[0] = acc[0] + sq(x[8 * (4 * r + k) + l]);
+            for (int j = 1; j < 4; ++j) {
+                acc[j] = acc[j] + acc[j - 1];
+                acc[j - 1] = 0.0f;
+                if ((r & (mask << (j * level_power))) != 0) break;
+            }
+        }
+        for (; r < size_ilp; ++r) acc[0] = acc[0] + sq(x[8 * (4 * r + k) + l]);
+        float a = acc[0];
+        for (int j = 1; j < 4; ++j) a = a + acc[j];
+        if (k == 0)
+            for (int v = 4 * size_ilp; v < nvec; ++v) a = a + sq(x[8 * v + l]);
+        tmp[t] = a;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float fin = 0.0f;
+        for (int i = 8 * nvec; i < n; ++i) fin = fin + sq(x[i]);
+        for (int l = 0; l < 8; ++l) fin = fin + (((tmp[l] + tmp[8 + l]) + tmp[16 + l]) + tmp[24 + l]);
+        *result = fin;
+    }
+    __syncthreads();
+    return *result;
+}
+
+// GemmaRMSNorm (layers.py:130-147) of one row held in LDS as fp32 values:
+// bf16((w + 1) * bf16(x * rsqrt(mean(x^2) + eps))).
+__device__ void gemma_norm_row(float *xs, int n, const uint16_t *__restrict__ w, float eps, float *tmp,
+                               float *result, uint16_t *__restrict__ out) {
+    const float sum = torch_row_sumsq(xs, n, tmp, result);
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sum, (float)n) + eps));
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float y = bfr(xs[i] * r);
+        const float wp = bfr(bf(w[i]) + 1.0f);
+        const uint16_t o = f32_to_bf16(wp * y);
+        if (out) out[i] = o;
+        xs[i] = bf(o);
+    }
+    __syncthreads();
+}
+
+// ---- residual add + GemmaRMSNorm ------------------------------------------
+// Row m: h = bf16(x + residual) (or x), residual_out = h, out = norm(h).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict__ x,
+                                                      const uint16_t *__restrict__ res,
+                                                      const uint16_t *__restrict__ w, uint16_t *__restrict__ out,
+                                                      uint16_t *__restrict__ res_out, int n, float eps) {
+    extern __shared__ float lds[];
+    float *xs = lds, *tmp = lds + n, *result = tmp + 32;
+    const size_t row = (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float h = bf(x[row + i]);
+        if (res) {
+            h = bfr(h + bf(res[row + i]));
+            if (res_out) res_out[row + i] = f32_to_bf16(h);
+        }
+        xs[i] = h;
+    }
+    __syncthreads();
+    gemma_norm_row(xs, n, w, eps, tmp, result, out + row);
+}
+
+// ---- q/k GemmaRMSNorm + rope + cache write ---------------------------------
+// Workgroup (s, head): head < H normalizes q (the first D of the head's 2D
+// q_proj outputs) into q_out[s, head, :]; head >= H normalizes k of kv head
+// head - H and stores it, with v, into the cache at position pos0 + s.  Rope
+// (layers.py:150-195, NeoX halves) on the first rot dims: with c, s the fp32
+// tables at the position, (a, b) = (x[f], x[f + rot/2]) becomes
+// (a c - b s, a s + b c), each product and sum rounded, then bf16.
+__global__ __launch_bounds__(128) void qk_rope_kernel(
+    const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
+    size_t q_stride, size_t kv_stride, const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
+    const float *__restrict__ cos_t, const float *__restrict__ sin_t, int max_pos, const int32_t *__restrict__ step,
+    int pos0_host, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
+    const int32_t *__restrict__ block_ids, int n_block_ids, int block_size, int num_blocks, int H, int Hkv, int D,
+    int rot, float eps) {
+    extern __shared__ float lds[];
+    float *xs = lds, *tmp = lds + D, *result = tmp + 32;
+    const int s = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+    const bool is_q = head < H;
+    const int hk = is_q ? head : head - H;
+    const uint16_t *src = is_q ? qg + (size_t)s * q_stride + (size_t)hk * 2 * D : kin + (size_t)s * kv_stride + (size_t)hk * D;
+    for (int i = t; i < D; i += blockDim.x) xs[i] = bf(src[i]);
+    __syncthreads();
+    gemma_norm_row(xs, D, is_q ? qw : kw, eps, tmp, result, nullptr);
+    const int pos = (step ? step[0] : pos0_host) + s;
+    const int pc = min(max(pos, 0), max_pos - 1);
+    const int nf = rot / 2;
+    uint16_t *dst;
+    if (is_q) {
+        dst = q_out + ((size_t)s * H + hk) * D;
+    } else {
+        const int bi = min(max(pos / block_size, 0), n_block_ids - 1);
+        const int blk = min(max(block_ids[bi], 0), num_blocks - 1);
+        const size_t row = (((size_t)blk * block_size + pos % block_size) * Hkv + hk) * D;
+        dst = k_cache + row;
+        const uint16_t *vs = vin + (size_t)s * kv_stride + (size_t)hk * D;
+        for (int i = t; i < D; i += blockDim.x) v_cache[row + i] = vs[i];
+    }
+    for (int i = t; i < D; i += blockDim.x) {
+        float o = xs[i];
+        if (i < rot) {
+            const int f = i < nf ? i : i - nf;
+            const float c = cos_t[(size_t)pc * nf + f], sn = sin_t[(size_t)pc * nf + f];
+            const float a = xs[f], b = xs[f + nf];
+            o = i < nf ? (a * c) - (b * sn) : (a * sn) + (b * c);
+        }
+        dst[i] = f32_to_bf16(o);
+    }
+}
+
+// ---- attention in torch's CPU order ----------------------------------------
+// Workgroup (kv head, query row s, column slice z) computes the rep = H / Hkv
+// heads that read this kv head, for head dimensions [z * DS, z * DS + DS).
+// Scores of the visible positions j <= cache_len - S + s go to LDS (bf16
+// values as fp32) and become softmax weights per head; then thread
+// (head, column, chain k) sums its chain of P.V (positions j = k mod 4; the
+// tail beyond the last multiple of four on chain 0) from value rows staged in
+// LDS 64 positions at a time, and chain 0's thread folds the four chains in
+// order and applies the gate.  naive: torch's small product kernel
+// (S * cache_len * D < 400) sums both dots in plain order.
+constexpr int kChunk = 64;     // positions per staged value chunk
+constexpr int kDS = 32;        // head dimensions per workgroup
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_exact_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache,
+    const int32_t *__restrict__ block_ids, int n_block_ids, int num_blocks, int block_size,
+    const uint16_t *__restrict__ gate, size_t gate_row_stride, size_t gate_head_stride,
+    const int32_t *__restrict__ step, int cache_len_host, int S, int H, int Hkv, int max_len, float scale,
+    uint16_t *__restrict__ out) {
+    extern __shared__ float lds[];
+    const int kh = blockIdx.x, s = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
+    const int rep = H / Hkv;
+    int cache_len = step ? step[1] : cache_len_host;
+    cache_len = min(max(cache_len, S), max_len);
+    const int vis = cache_len - S + s + 1;   // visible positions 0 .. vis-1
+    const bool naive = (long long)S * cache_len * D < 400;
+    const int scs = (max_len + 3) & ~3;                        // score row stride (16-byte rows)
+    float *qs = lds;                                           // [rep][D]
+    float *sc = qs + rep * D;                                  // [rep][scs]
+    float *part = sc + (size_t)rep * scs;                      // [rep][kDS][4] chain sums
+    int *bids = (int *)(part + rep * kDS * 4);                 // [n_block_ids]
+    uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [2][kChunk][kDS]
+    for (int i = t; i < rep * D; i += blockDim.x) {
+        const int r = i / D, d = i % D;
+        qs[i] = bf(q[((size_t)s * H + kh * rep + r) * D + d]);
+    }
+    for (int i = t; i < n_block_ids; i += blockDim.x) bids[i] = min(max(block_ids[i], 0), num_blocks - 1);
+    __syncthreads();
+
+    auto row_of = [&](int j) -> size_t {
+        const int blk = bids[min(j / block_size, n_block_ids - 1)];
+        return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
+    };
+
+    // scores
+    for (int j = t; j < vis; j += blockDim.x) {
+        const u32x4 *kr = (const u32x4 *)(k_cache + row_of(j));
+        uint32_t kv[D / 2];
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            const u32x4 c = kr[i];
+            kv[4 * i] = c[0];
+            kv[4 * i + 1] = c[1];
+            kv[4 * i + 2] = c[2];
+            kv[4 * i + 3] = c[3];
+        }
+        for (int r = 0; r < rep; ++r) {
+            const float *qr = qs + r * D;
+            float dot;
+            if (naive) {
+                dot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < D; ++i)
+                    dot = dot + qr[i] * (i & 1 ? bf16_hi(kv[i / 2]) : bf16_lo(kv[i / 2]));
+            } else {
+                float p[D / 2];
+#pragma unroll
+                for (int i = 0; i < D / 2; ++i) {
+                    const int i2 = i + D / 2;
+                    const float ka = i & 1 ? bf16_hi(kv[i / 2]) : bf16_lo(kv[i / 2]);
+                    const float kb = i2 & 1 ? bf16_hi(kv[i2 / 2]) : bf16_lo(kv[i2 / 2]);
+                    p[i] = __builtin_fmaf(qr[i], ka, qr[i2] * kb);
+                }
+#pragma unroll
+                for (int w = D / 4; w >= 1; w >>= 1)
+#pragma unroll
+                    for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
+                dot = p[0];
+            }
+            sc[(size_t)r * scs + j] = bfr(bfr(dot) * scale);
+        }
+    }
+    __syncthreads();
+
+    // softmax per head: wave r (looping when rep exceeds the wave count)
+    const int wave = t >> 6, lane = t & 63;
+    for (int r = wave; r < rep; r += blockDim.x / 64) {
+        float *x = sc + (size_t)r * scs;
+        float mx = -__builtin_inff();
+        for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float sum = 0.0f;
+        if (cache_len >= 8) {
+            float a = 0.0f;
+            if (lane < 8) {
+                a = lane < vis ? x[lane] : 0.0f;
+                for (int j = lane + 8; j < vis; j += 8) a = a + x[j];
+            }
+            const float b = a + __shfl_xor(a, 4);    // lanes c < 4: (c) + (c + 4)
+            const float c = b + __shfl_xor(b, 2);    // ((0+4) + (2+6)), ((1+5) + (3+7))
+            sum = __shfl(c + __shfl_xor(c, 1), 0);
+        } else {
+            for (int j = 0; j < vis; ++j) sum = sum + x[j];
+        }
+        const float inv = __fdiv_rn(1.0f, sum);
+        for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
+    }
+    __syncthreads();
+
+    // P.V: thread (r, column c, chain k); value rows of this slice staged in LDS
+    const int main_len = naive ? 0 : (cache_len / 4) * 4;
+    const int nthr = rep * kDS * 4;
+    const int d0 = z * kDS;
+    auto stage = [&](int ch, int buf) {
+        // kChunk rows x kDS columns of bf16 = kChunk x 64 bytes, 16 bytes per thread
+        uint16_t *dst = vs + (size_t)buf * kChunk * kDS;
+        for (int i = t; i < kChunk * (kDS / 8); i += blockDim.x) {
+            const int jj = i / (kDS / 8), piece = i % (kDS / 8);
+            const int j = ch * kChunk + jj;
+            u32x4 val = {0u, 0u, 0u, 0u};
+            if (j < vis) val = *(const u32x4 *)(v_cache + row_of(j) + d0 + 8 * piece);
+            *(u32x4 *)(dst + jj * kDS + 8 * piece) = val;
+        }
+    };
+    const int nch = (vis + kChunk - 1) / kChunk;
+    for (int base = 0; base < nthr; base += blockDim.x) {
+        const int i = base + t;
+        const bool active = i < nthr;
+        const int r = active ? i / (kDS * 4) : 0, c = (i / 4) % kDS, k = i & 3;
+        const float *w = sc + (size_t)r * scs;
+        float acc = 0.0f;
+        stage(0, 0);
+        __syncthreads();
+        for (int ch = 0; ch < nch; ++ch) {
+            if (ch + 1 < nch) stage(ch + 1, (ch + 1) & 1);
+            const uint16_t *vb = vs + (size_t)(ch & 1) * kChunk * kDS;
+            const int j0 = ch * kChunk, j1 = min(vis, j0 + kChunk);
+            if (active) {
+                if (naive) {
+                    if (k == 0)
+                        for (int j = j0; j < j1; ++j) acc = __builtin_fmaf(w[j], bf(vb[(j - j0) * kDS + c]), acc);
+                } else {
+                    // chain k: positions j = k mod 4 below main_len; chain 0 also takes the tail
+                    for (int j = j0 + k; j < min(j1, main_len); j += 4)
+                        acc = __builtin_fmaf(w[j], bf(vb[(j - j0) * kDS + c]), acc);
+                    if (k == 0)
+                        for (int j = max(j0, main_len); j < j1; ++j)
+                            acc = __builtin_fmaf(w[j], bf(vb[(j - j0) * kDS + c]), acc);
+                }
+            }
+            __syncthreads();
+        }
+        if (active) part[i - base] = acc;
+        __syncthreads();
+        if (active && k == 0) {
+            const float *pp = part + (i - base);
+            float o = naive ? pp[0] : ((pp[0] + pp[1]) + pp[2]) + pp[3];
+            o = bfr(o);
+            const int h = kh * rep + r, d = d0 + c;
+            if (gate) {
+                const float g = bf(gate[(size_t)s * gate_row_stride + (size_t)h * gate_head_stride + d]);
+                o = o * bfr(__fdiv_rn(1.0f, 1.0f + sleef_expf(-g)));
+            }
+            out[((size_t)s * H + h) * D + d] = f32_to_bf16(o);
+        }
+        __syncthreads();
+    }
+}
+
+// ---- SiLU(gate) * up --------------------------------------------------------
+// out = bf16(bf16(g / (1 + exp(-g))) * u): F.silu(gate) * up on bf16 tensors.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ g, const uint16_t *__restrict__ u,
+                                                       size_t in_stride, uint16_t *__restrict__ out, int n,
+                                                       int rows) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)n * rows) return;
+    const size_t m = i / n, c = i % n;
+    const float gv = bf(g[m * in_stride + c]);
+    const float sl = bfr(__fdiv_rn(gv, 1.0f + sleef_expf(-gv)));
+    out[i] = f32_to_bf16(sl * bf(u[m * in_stride + c]));
+}
+
+// ---- greedy step ------------------------------------------------------------
+// argmax of bf16 logits (first index of the largest value: torch.argmax on
+// the fp32 copy for finite logits), then the decode state advances:
+// tokens[count] = id, next_id = id, pos0 = cache_len, cache_len += 1, count += 1.
+__global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t *__restrict__ logits, int n,
+                                                      int32_t *__restrict__ state, int32_t *__restrict__ tokens,
+                                                      int64_t *__restrict__ next_id, int max_tokens) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int t = threadIdx.x;
+    float bv = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    for (int i = t; i < n; i += 1024) {
+        const float v = bf(logits[i]);
+        if (v > bv || (v == bv && i < bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        sv[t >> 6] = bv;
+        si[t >> 6] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        bv = sv[0];
+        bi = si[0];
+        for (int w = 1; w < 16; ++w)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        if (bi == 0x7FFFFFFF) bi = 0;
+        const int count = state[2];
+        if (count < max_tokens) tokens[count] = bi;
+        state[2] = count + 1;
+        next_id[0] = bi;
+        state[0] = state[1];
+        state[1] = state[1] + 1;
+    }
+}
+
+}  // namespace
+
+}  // namespace pilm
+
+using namespace pilm;
+
+extern "C" {
+
+int ekernel_rmsnorm_gemma_bf16(const ekernel_rmsnorm_desc_t *desc, const uint16_t *x, const uint16_t *residual,
+                               const uint16_t *weight, uint16_t *out, uint16_t *residual_out) {
+    static const char *fn = "ekernel_rmsnorm_gemma_bf16";
+    if (!desc || !x || !weight || !out) return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    const size_t M = desc->rows, n = desc->hidden;
+    if (M == 0) return ECPU_OK;
+    if (n < 32 || n > 8192) return fail(ECPU_ERR_UNSUPPORTED, "%s: hidden %zu outside [32, 8192]", fn, n);
+    const size_t bytes = M * n * 2;
+    int rc = check_device_buffer(x, bytes, "x", fn);
+    if (rc == ECPU_OK && residual) rc = check_device_buffer(residual, bytes, "residual", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(weight, n * 2, "weight", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(out, bytes, "out", fn);
+    if (rc == ECPU_OK && residual_out) rc = check_device_buffer(residual_out, bytes, "residual_out", fn);
+    if (rc != ECPU_OK) return rc;
+    const size_t lds = (n + 64) * sizeof(float);
+    rmsnorm_kernel<<<(unsigned)M, 256, lds, current_stream()>>>(x, residual, weight, out, residual_out, (int)n,
+                                                                desc->eps);
+    return check_launch(fn);
+}
+
+int ekernel_qk_norm_rope_bf16(const ekernel_qk_rope_desc_t *desc, const uint16_t *qg, const uint16_t *k,
+                              const uint16_t *v, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                              const float *cos_table, const float *sin_table, const int32_t *step,
+                              uint16_t *q_out, uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids) {
+    static const char *fn = "ekernel_qk_norm_rope_bf16";
+    if (!desc || !qg || !k || !v || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !q_out || !k_cache ||
+        !v_cache || !block_ids)
+        return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    const ekernel_qk_rope_desc_t &d = *desc;
+    if (d.S == 0) return ECPU_OK;
+    if (d.head_dim < 32 || d.head_dim > 256 || d.head_dim % 8 || d.rot_dim > d.head_dim || d.rot_dim % 2 ||
+        d.n_kv_heads == 0 || d.n_heads % d.n_kv_heads || d.block_size == 0 || d.n_block_ids == 0 ||
+        d.max_positions == 0)
+        return fail(ECPU_ERR_PARAM, "%s: inconsistent descriptor", fn);
+    if (!step && (d.pos0 + d.S > d.max_positions || d.pos0 + d.S > d.n_block_ids * d.block_size))
+        return fail(ECPU_ERR_PARAM, "%s: positions %zu..%zu beyond the tables", fn, d.pos0, d.pos0 + d.S - 1);
+    const size_t D = d.head_dim;
+    int rc = check_device_buffer(q_out, d.S * d.n_heads * D * 2, "q_out", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(k_cache, d.num_blocks * d.block_size * d.n_kv_heads * D * 2, "k_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(v_cache, d.num_blocks * d.block_size * d.n_kv_heads * D * 2, "v_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(block_ids, d.n_block_ids * 4, "block_ids", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(cos_table, d.max_positions * (d.rot_dim / 2) * 4, "cos_table", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(sin_table, d.max_positions * (d.rot_dim / 2) * 4, "sin_table", fn);
+    if (rc != ECPU_OK) return rc;
+    const dim3 grid((unsigned)d.S, (unsigned)(d.n_heads + d.n_kv_heads));
+    const size_t lds = (D + 64) * sizeof(float);
+    qk_rope_kernel<<<grid, 128, lds, current_stream()>>>(
+        qg, k, v, d.q_stride, d.kv_stride, q_norm_w, k_norm_w, cos_table, sin_table, (int)d.max_positions, step, (int)d.pos0,
+        q_out, k_cache, v_cache, block_ids, (int)d.n_block_ids, (int)d.block_size, (int)d.num_blocks,
+        (int)d.n_heads, (int)d.n_kv_heads, (int)D, (int)d.rot_dim, d.eps);
+    return check_launch(fn);
+}
+
+int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, const uint16_t *q,
+                                 const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *block_ids,
+                                 const uint16_t *gate, const int32_t *step, uint16_t *out) {
+    static const char *fn = "ekernel_attention_exact_bf16";
+    if (!desc || !q || !k_cache || !v_cache || !block_ids || !out)
+        return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    const ekernel_attention_exact_desc_t &d = *desc;
+    if (d.S == 0) return ECPU_OK;
+    if (d.n_kv_heads == 0 || d.n_heads % d.n_kv_heads || d.block_size == 0 || d.n_block_ids == 0)
+        return fail(ECPU_ERR_PARAM, "%s: inconsistent descriptor", fn);
+    if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: head_dim %zu (64, 128 or 256)", fn, d.head_dim);
+    const size_t max_len = d.n_block_ids * d.block_size;
+    if (!step && (d.cache_len < d.S || d.cache_len > max_len))
+        return fail(ECPU_ERR_PARAM, "%s: cache_len %zu outside [S, %zu]", fn, d.cache_len, max_len);
+    const size_t rep = d.n_heads / d.n_kv_heads, D = d.head_dim;
+    const size_t lds = (rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * kDS * 4 + ((d.n_block_ids + 3) & ~(size_t)3)) * 4 +
+                       2 * kChunk * kDS * 2;
+    if (lds > 64 * 1024)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu positions x %zu heads per kv head exceed LDS", fn, max_len, rep);
+    const size_t cache_bytes = d.num_blocks * d.block_size * d.n_kv_heads * D * 2;
+    int rc = check_device_buffer(q, d.S * d.n_heads * D * 2, "q", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(k_cache, cache_bytes, "k_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(v_cache, cache_bytes, "v_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(block_ids, d.n_block_ids * 4, "block_ids", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(out, d.S * d.n_heads * D * 2, "out", fn);
+    if (rc != ECPU_OK) return rc;
+    const dim3 grid((unsigned)d.n_kv_heads, (unsigned)d.S, (unsigned)(D / kDS));
+    const float scale = (float)(1.0 / __builtin_sqrt((double)D));
+    hipStream_t st = current_stream();
+#define PILM_ATTN_EXACT(DD)                                                                                         \
+    attn_exact_kernel<DD><<<grid, 256, lds, st>>>(q, k_cache, v_cache, block_ids, (int)d.n_block_ids,             \
+                                                  (int)d.num_blocks, (int)d.block_size, gate, d.gate_row_stride,    \
+                                                  d.gate_head_stride, step, (int)d.cache_len, (int)d.S,             \
+                                                  (int)d.n_heads, (int)d.n_kv_heads, (int)max_len, scale, out)
+    if (D == 64) PILM_ATTN_EXACT(64);
+    else if (D == 128) PILM_ATTN_EXACT(128);
+    else PILM_ATTN_EXACT(256);
+#undef PILM_ATTN_EXACT
+    return check_launch(fn);
+}
+
+int ekernel_silu_mul_bf16(const uint16_t *gate, const uint16_t *up, size_t rows, size_t n, size_t in_stride,
+                          uint16_t *out) {
+    static const char *fn = "ekernel_silu_mul_bf16";
+    if (!gate || !up || !out) return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    if (rows == 0 || n == 0) return ECPU_OK;
+    if (in_stride < n) return fail(ECPU_ERR_PARAM, "%s: row stride %zu < %zu", fn, in_stride, n);
+    const size_t in_bytes = ((rows - 1) * in_stride + n) * 2;
+    int rc = check_device_buffer(gate, in_bytes, "gate", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(up, in_bytes, "up", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(out, rows * n * 2, "out", fn);
+    if (rc != ECPU_OK) return rc;
+    const size_t total = rows * n;
+    silu_mul_kernel<<<(unsigned)((total + 255) / 256), 256, 0, current_stream()>>>(gate, up, in_stride, out, (int)n,
+                                                                                   (int)rows);
+    return check_launch(fn);
+}
+
+int ekernel_greedy_step_bf16(const uint16_t *logits, size_t n, int32_t *state, int32_t *tokens, size_t max_tokens,
+                             int64_t *next_id) {
+    static const char *fn = "ekernel_greedy_step_bf16";
+    if (!logits || !state || !tokens || !next_id || n == 0) return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    int rc = check_device_buffer(logits, n * 2, "logits", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(state, 3 * 4, "state", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(tokens, max_tokens * 4, "tokens", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(next_id, 8, "next_id", fn);
+    if (rc != ECPU_OK) return rc;
+    greedy_kernel<<<1, 1024, 0, current_stream()>>>(logits, (int)n, state, tokens, next_id, (int)max_tokens);
+    return check_launch(fn);
+}
+
+}  // extern "C"

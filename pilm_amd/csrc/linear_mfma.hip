@@ -9,10 +9,17 @@
 //     group formats the fp16 weights of a group are multiplied by the group
 //     scale rounded to fp16 (relative error <= 2^-11), per-row scales are
 //     applied in fp32 at the end;
-//   * activations are converted to fp16 once per tile: bf16 -> fp16 is exact
-//     for |a| in [2^-14, 65504]; an fp32 activation becomes two fp16 parts,
-//     hi = fp16(a) and lo = fp16(a - hi), multiplied by two MFMAs (22 of its
-//     24 bits survive, so cancelling fp32 activations stay accurate);
+//   * activations are converted to fp16 once per tile after scaling each row
+//     by a power of two that puts its largest magnitude in [2^14, 2^15): then
+//     bf16 -> fp16 is exact for every value within 2^28 of the row's largest,
+//     and an fp32 activation becomes two fp16 parts, hi = fp16(a) and
+//     lo = fp16(a - hi), multiplied by two MFMAs (22 of its 24 bits survive,
+//     so cancelling fp32 activations stay accurate);
+//   * group scales are scaled the same way per weight row (largest in
+//     [2^11, 2^12), so scale x weight stays below 2^15 and off the fp16
+//     subnormals); the epilogue multiplies both powers of two back out, which
+//     is exact, so any finite fp32 / bf16 activation and any scale keep the
+//     fp16 path's relative accuracy;
 //   * products are exact in the MFMA, sums are fp32 in an order that differs
 //     from the reference: outputs agree with the reference to ~1e-3 relative
 //     (the MFMA path tolerance is 1e-2).
@@ -30,6 +37,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 
@@ -93,35 +101,91 @@ __device__ __forceinline__ void split_hi(float (&v)[8], float (&hi)[8]) {
     }
 }
 
-// Activations [M, K] (bf16 or fp32) -> X[plane][M][K] fp16, each 8-element
-// block in the weight unpack order; one thread per block.
+// Power-of-two exponent e with maxv * 2^e in [2^(top-1), 2^top); 0 for a zero
+// or non-finite maximum (such rows convert unscaled, as the reference would
+// propagate their infinities and NaNs).
+__device__ __forceinline__ int range_exp(float maxv, int top) {
+    if (!(maxv > 0.0f) || !__builtin_isfinite(maxv)) return 0;
+    int ex;
+    (void)frexpf(maxv, &ex);   // maxv in [2^(ex-1), 2^ex)
+    return top - ex;
+}
+
+__device__ __forceinline__ float block_max_256(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
 template <int FMT>
-__global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ A, u32x4 *__restrict__ X,
-                                                      size_t blocks) {
-    using F = MF<FMT>;
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= blocks) return;
-    float v[8];
-    if constexpr (F::a32) {
-        const f32x4 *p = (const f32x4 *)A + 2 * i;
+__device__ __forceinline__ void load_act8(const void *__restrict__ A, size_t blk, float (&v)[8]) {
+    if constexpr (MF<FMT>::a32) {
+        const f32x4 *p = (const f32x4 *)A + 2 * blk;
         const f32x4 x0 = p[0], x1 = p[1];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             v[e] = x0[e];
             v[4 + e] = x1[e];
         }
-        float hi[8];
-        split_hi(v, hi);
-        X[i] = act_block<FMT>(hi);
-        X[blocks + i] = act_block<FMT>(v);
     } else {
-        const u32x4 x = ((const u32x4 *)A)[i];
+        const u32x4 x = ((const u32x4 *)A)[blk];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             v[2 * e] = bf16_lo(x[e]);
             v[2 * e + 1] = bf16_hi(x[e]);
         }
-        X[i] = act_block<FMT>(v);
+    }
+}
+
+// Activations [M, K] (bf16 or fp32) -> X[plane][M][K] fp16, each 8-element
+// block in the weight unpack order.  Workgroup m < M takes activation row m:
+// its largest magnitude sets the row exponent E[m], then every value is
+// scaled by 2^E[m] (exact) and converted.  Workgroups beyond M (group formats
+// only) set the weight-row exponents E[M + n] from each row's largest scale.
+template <int FMT>
+__global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ A, u32x4 *__restrict__ X,
+                                                      int *__restrict__ E, int M, int K,
+                                                      const float *__restrict__ S, int N, int G) {
+    using F = MF<FMT>;
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    if ((int)blockIdx.x >= M) {
+        if constexpr (F::group > 0) {
+            const int n = ((int)blockIdx.x - M) * 256 + tid;
+            if (n < N) {
+                float mx = 0.0f;
+                for (int g = 0; g < G; ++g) mx = fmaxf(mx, fabsf(S[(size_t)n * G + g]));
+                E[M + n] = range_exp(mx, 12);
+            }
+        }
+        return;
+    }
+    const int m = blockIdx.x;
+    const size_t nb = (size_t)K / 8, row0 = (size_t)m * nb, blocks = (size_t)M * nb;
+    float mx = 0.0f;
+    for (size_t b = tid; b < nb; b += 256) {
+        float v[8];
+        load_act8<FMT>(A, row0 + b, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+    }
+    const int ex = range_exp(block_max_256(mx, red), 15);
+    if (tid == 0) E[m] = ex;
+    for (size_t b = tid; b < nb; b += 256) {
+        float v[8];
+        load_act8<FMT>(A, row0 + b, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = ldexpf(v[e], ex);
+        if constexpr (F::a32) {
+            float hi[8];
+            split_hi(v, hi);
+            X[row0 + b] = act_block<FMT>(hi);
+            X[blocks + row0 + b] = act_block<FMT>(v);
+        } else {
+            X[row0 + b] = act_block<FMT>(v);
+        }
     }
 }
 
@@ -133,8 +197,8 @@ template <int FMT, int BM, int BN, int WM>
 __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 *__restrict__ X,
                                                                 const uint8_t *__restrict__ W,
                                                                 const float *__restrict__ S, void *__restrict__ C,
-                                                                float *__restrict__ P, int M, int N, int K,
-                                                                int steps_per_split) {
+                                                                float *__restrict__ P, const int *__restrict__ E,
+                                                                int M, int N, int K, int steps_per_split) {
     using F = MF<FMT>;
     constexpr int WN = 4 / WM;
     constexpr int TM = BM / WM / 32;     // 32x32 tiles per wave along M
@@ -209,13 +273,18 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
     constexpr int SPS = F::group == 32 ? 2 : 1;
     const int G = F::group > 0 ? (K + F::group - 1) / F::group : 1;
     float sreg[TN][SPS];
+    int wexp[TN];   // weight-row exponents (group formats): scales are taken times 2^wexp
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+        wexp[j] = F::group > 0 ? E[M + min(n0 + ncol_base + j * 32 + (lane & 31), N - 1)] : 0;
     auto load_scales = [&](int t) {
         if constexpr (F::group > 0) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int n = min(n0 + ncol_base + j * 32 + (lane & 31), N - 1);
 #pragma unroll
-                for (int g = 0; g < SPS; ++g) sreg[j][g] = S[(size_t)n * G + ((t0 + t) * kBK) / F::group + g];
+                for (int g = 0; g < SPS; ++g)
+                    sreg[j][g] = ldexpf(S[(size_t)n * G + ((t0 + t) * kBK) / F::group + g], wexp[j]);
             }
         }
     };
@@ -316,7 +385,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
                     pz[(size_t)m * N + n] = acc[i][j][e];
                     continue;
                 }
-                const float y = acc[i][j][e] * sc;
+                const float y = ldexpf(acc[i][j][e], -(E[m] + wexp[j])) * sc;
                 if constexpr (F::a32)
                     ((float *)C)[(size_t)m * N + n] = y;
                 else
@@ -329,14 +398,17 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
 // formats) and the output conversion.
 template <int FMT>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restrict__ P, const float *__restrict__ S,
-                                                          void *__restrict__ C, int M, int N, int splits) {
+                                                          void *__restrict__ C, const int *__restrict__ E, int M,
+                                                          int N, int splits) {
     using F = MF<FMT>;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total = (size_t)M * N;
     if (idx >= total) return;
     float y = 0.0f;
     for (int z = 0; z < splits; ++z) y += P[(size_t)z * total + idx];
-    if constexpr (F::group == 0) y *= S[idx % N];
+    const int m = (int)(idx / N), n = (int)(idx % N);
+    y = ldexpf(y, -(E[m] + (F::group > 0 ? E[M + n] : 0)));
+    if constexpr (F::group == 0) y *= S[n];
     if constexpr (F::a32)
         ((float *)C)[idx] = y;
     else
@@ -344,24 +416,25 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 }
 
 template <int FMT, int BM, int BN, int WM>
-void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const float *S, void *C, float *P, int splits,
-                 int sps, int M, int N, int K) {
+void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const float *S, void *C, float *P,
+                 const int *E, int splits, int sps, int M, int N, int K) {
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
-    gemm_mfma_kernel<FMT, BM, BN, WM><<<grid, kMfmaThreads, 0, st>>>(X, W, S, C, splits > 1 ? P : nullptr, M, N, K,
-                                                                     sps);
+    gemm_mfma_kernel<FMT, BM, BN, WM><<<grid, kMfmaThreads, 0, st>>>(X, W, S, C, splits > 1 ? P : nullptr, E, M, N,
+                                                                     K, sps);
     if (splits > 1) {
         const size_t total = (size_t)M * N;
-        split_reduce_kernel<FMT><<<(unsigned)((total + 255) / 256), 256, 0, st>>>(P, S, C, M, N, splits);
+        split_reduce_kernel<FMT><<<(unsigned)((total + 255) / 256), 256, 0, st>>>(P, S, C, E, M, N, splits);
     }
 }
 
 // Output tile per workgroup: 128 x 128 (waves 2 x 2 of 64 x 64) from M =
 // 128, 64 x 128 below; 256 x 128 on request (PILM_HIP_MFMA_BM).
 template <int FMT>
-void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, const uint8_t *W, const float *S,
-                     void *C, float *P, int splits, int sps, int M, int N, int K) {
-    const size_t blocks = (size_t)M * K / 8;
-    act_prep_kernel<FMT><<<(unsigned)((blocks + 255) / 256), 256, 0, st>>>(A, (u32x4 *)X, blocks);
+void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, int *E, const uint8_t *W,
+                     const float *S, void *C, float *P, int splits, int sps, int M, int N, int K) {
+    const int G = MF<FMT>::group > 0 ? (K + MF<FMT>::group - 1) / MF<FMT>::group : 0;
+    const unsigned wrows = MF<FMT>::group > 0 ? (unsigned)((N + 255) / 256) : 0u;
+    act_prep_kernel<FMT><<<(unsigned)M + wrows, 256, 0, st>>>(A, (u32x4 *)X, E, M, K, S, N, G);
     // waves 1 x 4 (each wave all of the tile's rows, a quarter of its
     // columns, so every weight is decoded once) for int4 weights below 128
     // rows: 8B gate_up W4 g128 M=64 47.9 vs 53.2 us, M=80 59.8 vs 71.1 us;
@@ -370,18 +443,25 @@ void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, c
     const int env_wm = env_int("PILM_HIP_MFMA_WM", 0);
     if (env_wm == 1 || env_wm == 2) wm = env_wm;
     if (bm == 256)
-        launch_mfma<FMT, 256, 128, 2>(st, X, W, S, C, P, splits, sps, M, N, K);
+        launch_mfma<FMT, 256, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
     else if (bm == 128)
-        wm == 1 ? launch_mfma<FMT, 128, 128, 1>(st, X, W, S, C, P, splits, sps, M, N, K)
-                : launch_mfma<FMT, 128, 128, 2>(st, X, W, S, C, P, splits, sps, M, N, K);
+        wm == 1 ? launch_mfma<FMT, 128, 128, 1>(st, X, W, S, C, P, E, splits, sps, M, N, K)
+                : launch_mfma<FMT, 128, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
     else
-        wm == 1 ? launch_mfma<FMT, 64, 128, 1>(st, X, W, S, C, P, splits, sps, M, N, K)
-                : launch_mfma<FMT, 64, 128, 2>(st, X, W, S, C, P, splits, sps, M, N, K);
+        wm == 1 ? launch_mfma<FMT, 64, 128, 1>(st, X, W, S, C, P, E, splits, sps, M, N, K)
+                : launch_mfma<FMT, 64, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
 }
 
 }  // namespace
 
-int mfma_min_m() { return env_int("PILM_HIP_MFMA_MIN_M", 64); }
+// Row threshold of the matrix-core path: ecpu_hip_set_matrix_core_min_rows()
+// when set (>= 0), else PILM_HIP_MFMA_MIN_M, default 64.
+static std::atomic<int> g_mfma_min_rows{-1};
+
+int mfma_min_m() {
+    const int v = g_mfma_min_rows.load(std::memory_order_relaxed);
+    return v >= 0 ? v : env_int("PILM_HIP_MFMA_MIN_M", 64);
+}
 
 bool mfma_supports(size_t K, const void *A, const uint8_t *W) {
     return K > 0 && K % kBK == 0 && ((((uintptr_t)A) | ((uintptr_t)W)) & 15) == 0;
@@ -413,21 +493,30 @@ int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
         const int rc = split_scratch(st, (size_t)splits * M * N, 1, &P, &T, fn);
         if (rc != ECPU_OK) return rc;
     }
+    // activation planes, then the row exponents (M activation rows, N weight rows)
     void *X = nullptr;
-    const size_t xbytes = (size_t)M * K * 2 * (fmt == F_W8A32 ? 2 : 1);
+    const size_t xbytes = ((size_t)M * K * 2 * (fmt == F_W8A32 ? 2 : 1) + 255) & ~(size_t)255;
     {
-        const int rc = act_scratch(xbytes, &X, fn);
+        const int rc = act_scratch(xbytes + (M + N) * sizeof(int), &X, fn);
         if (rc != ECPU_OK) return rc;
     }
     const _Float16 *Xh = (const _Float16 *)X;
+    int *E = (int *)((char *)X + xbytes);
     switch (fmt) {
-        case F_W8A32: launch_mfma_fmt<F_W8A32>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        case F_W8A16: launch_mfma_fmt<F_W8A16>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        case F_W4ROW: launch_mfma_fmt<F_W4ROW>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        case F_W4G128: launch_mfma_fmt<F_W4G128>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
-        default: launch_mfma_fmt<F_W4G32>(bm, st, A, Xh, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W8A32: launch_mfma_fmt<F_W8A32>(bm, st, A, Xh, E, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W8A16: launch_mfma_fmt<F_W8A16>(bm, st, A, Xh, E, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W4ROW: launch_mfma_fmt<F_W4ROW>(bm, st, A, Xh, E, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        case F_W4G128: launch_mfma_fmt<F_W4G128>(bm, st, A, Xh, E, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
+        default: launch_mfma_fmt<F_W4G32>(bm, st, A, Xh, E, W, S, C, P, splits, sps, (int)M, (int)N, (int)K); break;
     }
     return ECPU_OK;
 }
 
 }  // namespace pilm
+
+extern "C" int ecpu_hip_set_matrix_core_min_rows(int rows) {
+    pilm::g_mfma_min_rows.store(rows < 0 ? -1 : rows, std::memory_order_relaxed);
+    return ECPU_OK;
+}
+
+extern "C" int ecpu_hip_matrix_core_min_rows(void) { return pilm::mfma_min_m(); }

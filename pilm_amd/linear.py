@@ -11,12 +11,14 @@ inputs live on the GPU; the kernels are the HIP library's, called through
 pilm_amd.ckernel.
 
 Differences, all on the device side:
-  * the fused W4 SwiGLU kernel is used for one-row inputs unless
-    PILM_W4_SWIGLU_FUSED=0 (piLM enables it with =1: on its CPU it gave no
-    win, here it saves a launch and the [g | u] round trip);
-  * the SwiGLU activation between the two linears is torch's
-    `F.silu(gate) * up` (PILM_SWIGLU_ACT_BACKEND=torch, the default, as in
-    piLM) or the library's bf16 SwiGLU (=ckernel).
+  * the SwiGLU activation between the two linears reproduces torch's CPU
+    `F.silu(gate) * up` bit for bit (PILM_SWIGLU_ACT_BACKEND=torch, the
+    default, as in piLM; computed by ekernel_silu_mul_bf16, because torch's
+    own GPU silu rounds differently) or is the library's bf16 SwiGLU
+    (=ckernel, the reference's ekernel_swiglu_bf16);
+  * the fused W4 SwiGLU kernel (one-row inputs) is opt-in with
+    PILM_W4_SWIGLU_FUSED=1, as in piLM; it rounds silu(g) * u once, the
+    default path rounds silu(g) to bf16 first.
 """
 from __future__ import annotations
 
@@ -50,15 +52,18 @@ def _unrows(out: torch.Tensor, squeeze: bool, original_shape) -> torch.Tensor:
 
 
 def _swiglu_act(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
-    """linear.py:408-421 / 534-545: torch silu * up, or the bf16 kernel."""
-    if (os.environ.get("PILM_SWIGLU_ACT_BACKEND", "torch").lower() == "ckernel"
-            and gate.dtype == torch.bfloat16 and gate.device.type == _GPU):
-        return ckernel.swiglu_bf16(gate, up)
+    """linear.py:408-421 / 534-545: silu(gate) * up as torch computes it on
+    the CPU (bf16), or the reference's bf16 SwiGLU kernel (=ckernel)."""
+    if gate.dtype == torch.bfloat16 and gate.device.type == _GPU:
+        if os.environ.get("PILM_SWIGLU_ACT_BACKEND", "torch").lower() == "ckernel":
+            return ckernel.swiglu_bf16(gate, up)
+        return ckernel.silu_mul_bf16(gate, up)
     return F.silu(gate) * up
 
 
 def _w4_swiglu_fused_enabled() -> bool:
-    return os.environ.get("PILM_W4_SWIGLU_FUSED", "1") != "0"
+    """linear.py:43-49: the fused W4 SwiGLU kernel only with PILM_W4_SWIGLU_FUSED=1."""
+    return os.environ.get("PILM_W4_SWIGLU_FUSED", "0") == "1"
 
 
 class QuantizedW8A32Linear(nn.Module):

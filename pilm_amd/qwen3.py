@@ -1,0 +1,326 @@
+"""Qwen3 decoder on one MI355X: piLM's Qwen3Model and its greedy decode loop
+with every step on the device.
+
+Mirrors src/models/qwen3/model.py:10-127 (TransformerBlock, Qwen3Model),
+src/models/qwen3/attention.py:46-141 (FullAttention: gated q_proj, q/k
+GemmaRMSNorm, rope, paged KV, sigmoid gate) and the greedy path of
+src/engine.py:319-664 (prefill in block-aligned chunks of at most one
+16-token block, one token per step after it, argmax of the bf16 logits):
+  * linears: the quantized-linear entry points of the HIP libecpu (W4A16 g128
+    here), bit-identical to the reference's C kernels; q/k/v and gate/up are
+    row-concatenated into one matrix each, which leaves every output row's
+    arithmetic unchanged;
+  * everything else: the decoder-step entry points (ekernel_rmsnorm_gemma_bf16,
+    ekernel_qk_norm_rope_bf16, ekernel_attention_exact_bf16,
+    ekernel_silu_mul_bf16, ekernel_greedy_step_bf16), which reproduce the
+    reference's torch CPU roundings;
+  * the rope tables are computed once on the host with torch's CPU operations
+    in the reference's order (layers.py:50-78) and uploaded.
+A decode step is captured once into a HIP graph; its kernels read the
+position from a device state word that the greedy step advances, so
+successive replays generate successive tokens with no host work in between.
+
+There is no CPU path: the library must be built and a GPU present.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+from dataclasses import dataclass, field
+
+import torch
+
+from . import bindings as abi
+from . import ckernel
+from . import synth_model as SM
+
+
+@dataclass
+class Qwen3Config:
+    layers: int = 28
+    hidden: int = 2048
+    heads: int = 16
+    kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 6144
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+    partial_rotary: float = 1.0
+    block_size: int = 16
+    group_size: int = 128
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "Qwen3Config":
+        return cls(**{k: d[k] for k in cls.__dataclass_fields__ if k in d})
+
+    @property
+    def rot_dim(self) -> int:
+        return int(self.head_dim * self.partial_rotary)
+
+
+QWEN3_1P7B = Qwen3Config()
+QWEN3_8B = Qwen3Config(layers=36, hidden=4096, heads=32, kv_heads=8, intermediate=12288)
+
+
+def rope_tables(theta: float, rot_dim: int, positions: int):
+    """cos, sin fp32 [positions, rot_dim / 2] with torch's CPU operations in
+    the order of _rope_inv_freq and _rope_cos_sin (layers.py:50-78)."""
+    n_freq = rot_dim // 2
+    inv = 1.0 / (theta ** (torch.arange(0, n_freq, dtype=torch.float32) / n_freq))
+    pos = torch.arange(positions, dtype=torch.long).to(torch.float32).reshape(-1)
+    freqs = pos.unsqueeze(1) * inv.unsqueeze(0)
+    return torch.cos(freqs), torch.sin(freqs)
+
+
+def _sha(t: torch.Tensor) -> str:
+    return hashlib.sha256(t.detach().contiguous().cpu().view(-1).view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+@dataclass
+class Qwen3Weights:
+    """Device-resident weights: bf16 embedding and norms, W4A16 g128 linears
+    (qweight uint8 [N, K/2], scales fp32 [N, K/128]) with q/k/v and gate/up
+    concatenated row-wise."""
+    cfg: Qwen3Config
+    embed: torch.Tensor
+    layers: list
+    norm: torch.Tensor
+    lm_head: tuple
+    quantized_sha: dict = field(default_factory=dict)
+
+    @classmethod
+    def synthetic(cls, cfg: Qwen3Config, seed: int, std: float = 0.02, device="cuda", hashes: bool = False):
+        """Random-init weights ~N(0, std) (pilm_amd.synth_model, bit-identical on
+        any device), every Linear quantized on the device with the reference's
+        grouped int4 quantizer (ckernel.quantize_weight_i4_grouped_chunked)."""
+        ids = SM.tensor_ids(cfg.layers)
+        qsha = {}
+        D, H, Hq, Hkv, I = cfg.head_dim, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.intermediate
+
+        def bf16(name, shape):
+            return SM.normal_f32(seed, ids[name], shape, std, device=device).to(torch.bfloat16)
+
+        def quant(name, out_f, in_f):
+            w = SM.normal_f32(seed, ids[name], (out_f, in_f), std, device=device)
+            q, s = ckernel.quantize_weight_i4_grouped_chunked(w, group_size=cfg.group_size, rows_per_chunk=8192)
+            del w
+            if hashes:
+                qsha[name] = [_sha(q), _sha(s)]
+            return q, s
+
+        def cat(parts):
+            return torch.cat([p[0] for p in parts]).contiguous(), torch.cat([p[1] for p in parts]).contiguous()
+
+        layers = []
+        for i in range(cfg.layers):
+            p = f"layers.{i}."
+            qkv = cat([quant(p + "self_attn.q_proj", 2 * Hq * D, H), quant(p + "self_attn.k_proj", Hkv * D, H),
+                       quant(p + "self_attn.v_proj", Hkv * D, H)])
+            gate_up = cat([quant(p + "mlp.gate", I, H), quant(p + "mlp.up", I, H)])
+            layers.append({
+                "in_norm": bf16(p + "input_layernorm", (H,)),
+                "post_norm": bf16(p + "post_attention_layernorm", (H,)),
+                "q_norm": bf16(p + "self_attn.q_norm", (D,)),
+                "k_norm": bf16(p + "self_attn.k_norm", (D,)),
+                "qkv": qkv,
+                "o": quant(p + "self_attn.o_proj", H, Hq * D),
+                "gate_up": gate_up,
+                "down": quant(p + "mlp.down", H, I),
+            })
+        return cls(cfg, bf16("embed_tokens", (cfg.vocab, H)), layers, bf16("norm", (H,)),
+                   quant("lm_head", cfg.vocab, H), qsha)
+
+    def linear_bytes_per_token(self) -> int:
+        """Weight + scale bytes the linears of one decode token read."""
+        tot = sum(q.numel() + 4 * s.numel() for L in self.layers for (q, s) in (L["qkv"], L["o"], L["gate_up"],
+                                                                                 L["down"]))
+        return tot + self.lm_head[0].numel() + 4 * self.lm_head[1].numel()
+
+
+def _vp(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None else None)
+
+
+class Qwen3Decoder:
+    """One sequence's decode state: paged KV caches, rope tables, the device
+    state word {pos0, cache_len, count} and the step buffers."""
+
+    def __init__(self, weights: Qwen3Weights, max_positions: int, max_new_tokens: int = 1024):
+        self.w = w = weights
+        self.cfg = c = weights.cfg
+        dev = w.embed.device
+        self.dev = dev
+        self.lib = abi._load_lib()
+        bs = c.block_size
+        self.max_pos = max_positions
+        self.nblocks = (max_positions + bs - 1) // bs
+        kv_shape = (self.nblocks, bs, c.kv_heads, c.head_dim)
+        self.k_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.layers)]
+        self.v_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.layers)]
+        # the reference's block manager hands out block ids; any assignment gives the same arithmetic
+        self.block_ids = torch.arange(self.nblocks, dtype=torch.int32, device=dev)
+        cos, sin = rope_tables(c.rope_theta, c.rot_dim, max_positions)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        S, H, D, Hq, I = bs, c.hidden, c.head_dim, c.heads, c.intermediate
+        e = dict(dtype=torch.bfloat16, device=dev)
+        self.nqkv = w.layers[0]["qkv"][0].shape[0]
+        self.x = torch.empty((S, H), **e)
+        self.res = torch.empty((S, H), **e)
+        self.h = torch.empty((S, H), **e)
+        self.qkv = torch.empty((S, self.nqkv), **e)
+        self.q = torch.empty((S, Hq, D), **e)
+        self.attn = torch.empty((S, Hq * D), **e)
+        self.o = torch.empty((S, H), **e)
+        self.gu = torch.empty((S, 2 * I), **e)
+        self.act = torch.empty((S, I), **e)
+        self.mlp = torch.empty((S, H), **e)
+        self.logits = torch.empty((c.vocab,), **e)
+        self.state = torch.zeros(4, dtype=torch.int32, device=dev)      # pos0, cache_len, count
+        self.max_new = max_new_tokens
+        self.tokens = torch.zeros(max_new_tokens, dtype=torch.int32, device=dev)
+        self.next_id = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.graph = None
+        self._descs = {}
+
+    # ---------------------------------------------------------------- calls
+    def _check(self, rc: int, name: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{name} failed: rc={rc} ({abi.last_error()})")
+
+    def _desc(self, key, maker):
+        d = self._descs.get(key)
+        if d is None:
+            d = self._descs[key] = maker()
+        return d
+
+    def _linear(self, x, wq, out, m):
+        q, s = wq
+        d = self._desc(("lin", m, q.shape[0], x.shape[1]),
+                       lambda: abi.EkernelLinearW8A32Desc(m, q.shape[0], x.shape[1]))
+        self._check(self.lib.ekernel_linear_w4a16g128_bf16(ctypes.byref(d), _vp(x), _vp(q), _vp(s), _vp(out), 6),
+                    "ekernel_linear_w4a16g128_bf16")
+
+    def _norm(self, x, res, weight, out, res_out, m):
+        d = self._desc(("norm", m), lambda: abi.EkernelRmsnormDesc(m, self.cfg.hidden, self.cfg.eps))
+        self._check(self.lib.ekernel_rmsnorm_gemma_bf16(ctypes.byref(d), _vp(x), _vp(res), _vp(weight), _vp(out),
+                                                        _vp(res_out)), "ekernel_rmsnorm_gemma_bf16")
+
+    def _forward(self, m: int, with_logits: bool):
+        """The model over the m tokens in self.x at the positions the state
+        word names; with_logits: final norm + lm_head of the last token."""
+        c, L = self.cfg, self.lib
+        D, Hq, Hkv, I = c.head_dim, c.heads, c.kv_heads, c.intermediate
+        rope = self._desc(("rope", m), lambda: abi.EkernelQkRopeDesc(
+            m, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, 0, self.max_pos, c.block_size, self.nblocks,
+            self.nblocks, c.eps))
+        att = self._desc(("attn", m), lambda: abi.EkernelAttentionExactDesc(
+            m, Hq, Hkv, D, m, c.block_size, self.nblocks, self.nblocks, self.nqkv, 2 * D))
+        qkv_p = self.qkv.data_ptr()
+        k_off, v_off = 2 * Hq * D * 2, (2 * Hq * D + Hkv * D) * 2
+        res_in = None
+        for li, Lw in enumerate(self.w.layers):
+            if li == 0:
+                self._norm(self.x, None, Lw["in_norm"], self.h, None, m)
+                res_in = self.x
+            else:
+                self._norm(self.mlp, self.res, Lw["in_norm"], self.h, self.res, m)
+                res_in = self.res
+            self._linear(self.h, Lw["qkv"], self.qkv, m)
+            self._check(L.ekernel_qk_norm_rope_bf16(
+                ctypes.byref(rope), ctypes.c_void_p(qkv_p), ctypes.c_void_p(qkv_p + k_off),
+                ctypes.c_void_p(qkv_p + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos), _vp(self.sin),
+                _vp(self.state), _vp(self.q), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(self.block_ids)),
+                "ekernel_qk_norm_rope_bf16")
+            self._check(L.ekernel_attention_exact_bf16(
+                ctypes.byref(att), _vp(self.q), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(self.block_ids),
+                ctypes.c_void_p(qkv_p + D * 2), _vp(self.state), _vp(self.attn)), "ekernel_attention_exact_bf16")
+            self._linear(self.attn, Lw["o"], self.o, m)
+            self._norm(self.o, res_in, Lw["post_norm"], self.h, self.res, m)
+            self._linear(self.h, Lw["gate_up"], self.gu, m)
+            gp = self.gu.data_ptr()
+            self._check(L.ekernel_silu_mul_bf16(ctypes.c_void_p(gp), ctypes.c_void_p(gp + I * 2), m, I, 2 * I,
+                                                _vp(self.act)), "ekernel_silu_mul_bf16")
+            self._linear(self.act, Lw["down"], self.mlp, m)
+        if with_logits:
+            last = m - 1
+            self._norm(self.mlp[last:m], self.res[last:m], self.w.norm, self.h, None, 1)
+            self._linear(self.h[:1], self.w.lm_head, self.logits.view(1, -1), 1)
+            self._check(L.ekernel_greedy_step_bf16(_vp(self.logits), c.vocab, _vp(self.state), _vp(self.tokens),
+                                                   self.max_new, _vp(self.next_id)), "ekernel_greedy_step_bf16")
+
+    def _bind(self):
+        abi.set_stream(torch.cuda.current_stream(self.dev).cuda_stream)
+
+    # ---------------------------------------------------------------- public
+    def prefill(self, prompt: list) -> None:
+        """Prompt tokens in the engine's chunks (each within one KV block);
+        the last chunk's logits give the first generated token."""
+        c = self.cfg
+        if len(prompt) + 1 > self.max_pos:
+            raise ValueError(f"prompt of {len(prompt)} tokens exceeds {self.max_pos} positions")
+        self._bind()
+        ids = torch.tensor(prompt, dtype=torch.int64, device=self.dev)
+        pos = 0
+        while pos < len(prompt):
+            n = min(len(prompt) - pos, c.block_size - pos % c.block_size)
+            self.state.copy_(torch.tensor([pos, pos + n, 0, 0], dtype=torch.int32))
+            torch.index_select(self.w.embed, 0, ids[pos:pos + n], out=self.x[:n])
+            self._forward(n, with_logits=pos + n == len(prompt))
+            pos += n
+
+    def decode_step(self) -> None:
+        """One token: embedding of the last generated id, the model, lm_head,
+        argmax; advances the state word."""
+        torch.index_select(self.w.embed, 0, self.next_id, out=self.x[:1])
+        self._forward(1, with_logits=True)
+
+    def capture(self) -> None:
+        """Capture decode_step into a HIP graph (the state word makes each
+        replay the next position).  One eager step first sizes the library's
+        per-device scratch (split-K sums and tickets), which must not be
+        allocated while a graph is being captured; the state, the next id and
+        the token list are restored after it, and the first replay recomputes
+        that step (its cache rows come out the same)."""
+        saved = (self.state.clone(), self.next_id.clone(), self.tokens.clone())
+        self._bind()
+        self.decode_step()
+        torch.cuda.synchronize(self.dev)
+        self.state.copy_(saved[0])
+        self.next_id.copy_(saved[1])
+        self.tokens.copy_(saved[2])
+        s = torch.cuda.Stream(self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+            self._bind()
+            self.decode_step()
+        torch.cuda.synchronize(self.dev)
+        self._bind()
+        self.graph = g
+
+    def generate(self, prompt: list, n_new: int, graph: bool = True, on_logits=None) -> list:
+        """Greedy tokens after the prompt (src/engine.py:383-659 with
+        temperature 0, top_k 0).  on_logits(i, logits) sees the bf16 logits
+        each token i was chosen from (eager steps only)."""
+        if n_new > self.max_new or len(prompt) + n_new > self.max_pos:
+            raise ValueError("sequence longer than the decoder was sized for")
+        if on_logits is not None:
+            graph = False
+        self.prefill(prompt)
+        if on_logits is not None:
+            on_logits(0, self.logits)
+        if graph and n_new > 1:
+            if self.graph is None:
+                self.capture()        # records the step; nothing runs until a replay
+            for _ in range(n_new - 1):
+                self.graph.replay()
+        else:
+            self._bind()
+            for i in range(1, n_new):
+                self.decode_step()
+                if on_logits is not None:
+                    on_logits(i, self.logits)
+        torch.cuda.synchronize(self.dev)
+        return self.tokens[:n_new].tolist()

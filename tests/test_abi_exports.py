@@ -50,13 +50,16 @@ def test_every_declared_symbol_is_exported(lib_path):
 
 def test_library_loads_and_configures(lib_path):
     lib = abi._load_lib()
-    assert abi.library_path() == str(lib_path)
-    assert abi.version().endswith("gfx950")
-    assert abi.detect_isa() == "gfx950"
-    assert all(abi.available_kernel_symbols()[s] for s in (
+    info = abi.library_info()
+    assert info["path"] == str(lib_path)
+    assert info["version"].endswith("gfx950")
+    assert info["isa"] == "gfx950"
+    assert all(info["entry_points"][s] for s in (
         "ekernel_gemm", "ekernel_linear_w8a32", "ekernel_linear_w8a16_bf16", "ekernel_linear_w4a16_bf16",
         "ekernel_linear_w4a16g32_bf16", "ekernel_linear_w4a16g128_bf16", "ekernel_swiglu_bf16",
-        "ekernel_linear_w8a16_bf16_argmax", "ekernel_swiglu_w4a16_bf16"))
+        "ekernel_linear_w8a16_bf16_argmax", "ekernel_swiglu_w4a16_bf16", "ekernel_rmsnorm_gemma_bf16",
+        "ekernel_qk_norm_rope_bf16", "ekernel_attention_exact_bf16", "ekernel_silu_mul_bf16",
+        "ekernel_greedy_step_bf16"))
     vt = lib.edevice_get  # exported registry accessor
     assert vt is not None
 
@@ -69,6 +72,10 @@ def test_descriptor_layout_matches_reference():
     # ekernel_w4a16_swiglu_desc_t (kernel/api.h:44-50): five size_t
     assert ctypes.sizeof(abi.EkernelW4A16SwiGLUDesc) == 40
     assert abi.EkernelW4A16SwiGLUDesc.down_in_features.offset == 32
+    # the decoder steps' descriptors (ecpu_hip.h): size_t fields, then the float eps
+    assert abi.EkernelRmsnormDesc.eps.offset == 16 and ctypes.sizeof(abi.EkernelRmsnormDesc) == 24
+    assert abi.EkernelQkRopeDesc.eps.offset == 96 and ctypes.sizeof(abi.EkernelQkRopeDesc) == 104
+    assert ctypes.sizeof(abi.EkernelAttentionExactDesc) == 80
 
 
 def test_missing_symbol_fails_loudly(tmp_path, monkeypatch):

@@ -1,0 +1,308 @@
+"""GPU: the decoder-step kernels and the device decoder, bit for bit.
+
+Each entry point (ekernel_rmsnorm_gemma_bf16, ekernel_qk_norm_rope_bf16,
+ekernel_attention_exact_bf16, ekernel_silu_mul_bf16, ekernel_greedy_step_bf16)
+is compared byte for byte with the oracle (oracle/decoder.c, pinned against
+torch's CPU kernels and the reference's fixture by test_oracle_decoder.py) on
+seeded inputs, through the C ABI.  Then the whole device decoder
+(pilm_amd.qwen3) must reproduce the fixtures piLM's own Engine.generate wrote:
+the quantized weights' hashes, every step's bf16 logits and the greedy tokens
+-- for a two-layer model and for Qwen3-1.7B (128-token prompt, 256 tokens).
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import decoder as OD
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _dev16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint16).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def _bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _rand16(rng, shape, scale=1.0):
+    from pilm_amd import synth as S
+    return S.f32_to_bf16_bits((rng.standard_normal(shape) * scale).astype(np.float32)).reshape(shape)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from pilm_amd import bindings as abi
+    return abi._load_lib()
+
+
+def _bind():
+    from pilm_amd import bindings as abi
+    abi.set_stream(torch.cuda.current_stream().cuda_stream)
+
+
+def _vp(t):
+    import ctypes
+    return ctypes.c_void_p(t.data_ptr() if t is not None else None)
+
+
+# --------------------------------------------------------------- rmsnorm
+
+@pytest.mark.parametrize("rows,n", [(1, 2048), (16, 2048), (3, 4096), (2, 128), (5, 296), (1, 8192)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rmsnorm_kernel(lib, dev, rows, n, with_res):
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(rows * n + with_res)
+    x, r, w = _rand16(rng, (rows, n), 3.0), _rand16(rng, (rows, n)), _rand16(rng, (n,), 0.02)
+    want, want_res = OD.rmsnorm_gemma_bf16(x, r if with_res else None, w, 1e-6)
+    xd, rd, wd = _dev16(x, dev), _dev16(r, dev), _dev16(w, dev)
+    out, res_out = torch.empty_like(xd), torch.empty_like(xd)
+    _say(f"[gpu] rmsnorm rows={rows} n={n} residual={with_res}")
+    _bind()
+    d = abi.EkernelRmsnormDesc(rows, n, 1e-6)
+    rc = lib.ekernel_rmsnorm_gemma_bf16(ctypes.byref(d), _vp(xd), _vp(rd if with_res else None), _vp(wd), _vp(out),
+                                        _vp(res_out if with_res else None))
+    assert rc == 0, abi.last_error()
+    assert np.array_equal(_bits(out), want)
+    if with_res:
+        assert np.array_equal(_bits(res_out), want_res)
+
+
+def test_rmsnorm_in_place_residual(lib, dev):
+    """The decoder passes residual and residual_out as one buffer."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(7)
+    x, r, w = _rand16(rng, (4, 2048)), _rand16(rng, (4, 2048)), _rand16(rng, (2048,), 0.02)
+    want, want_res = OD.rmsnorm_gemma_bf16(x, r, w, 1e-6)
+    xd, rd, wd = _dev16(x, dev), _dev16(r, dev), _dev16(w, dev)
+    out = torch.empty_like(xd)
+    _bind()
+    rc = lib.ekernel_rmsnorm_gemma_bf16(ctypes.byref(abi.EkernelRmsnormDesc(4, 2048, 1e-6)), _vp(xd), _vp(rd),
+                                        _vp(wd), _vp(out), _vp(rd))
+    assert rc == 0
+    assert np.array_equal(_bits(out), want) and np.array_equal(_bits(rd), want_res)
+
+
+# ----------------------------------------------------- q/k norm + rope + attention
+
+def _attn_case(rng, S, H, Hkv, D, pos0, bs=16, spare=3):
+    L = pos0 + S
+    nblk = (L + bs - 1) // bs
+    nphys = nblk + spare
+    block_ids = rng.permutation(nphys)[:nblk].astype(np.int32)
+    kc = _rand16(rng, (nphys, bs, Hkv, D))
+    vc = _rand16(rng, (nphys, bs, Hkv, D))
+    qkv = _rand16(rng, (S, (2 * H + 2 * Hkv) * D))          # fused [q | gate per head][k][v]
+    qw, kw = _rand16(rng, (D,), 0.02), _rand16(rng, (D,), 0.02)
+    return L, block_ids, kc, vc, qkv, qw, kw
+
+
+@pytest.mark.parametrize("S,H,Hkv,D,pos0", [(1, 16, 8, 128, 383), (16, 16, 8, 128, 112), (16, 16, 8, 128, 0),
+                                            (5, 32, 8, 128, 2043), (1, 4, 2, 128, 0), (3, 8, 8, 64, 17),
+                                            (2, 4, 1, 256, 40), (1, 16, 8, 128, 2), (1, 16, 8, 128, 7)])
+def test_qk_rope_then_attention(lib, dev, S, H, Hkv, D, pos0):
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(S * 7919 + pos0 + H)
+    bs = 16
+    L, block_ids, kc, vc, qkv, qw, kw = _attn_case(rng, S, H, Hkv, D, pos0, bs)
+    cos, sin = OD.rope_tables(1e6, D, L + 1)
+    stride = qkv.shape[1]
+    qg, k, v = qkv[:, :2 * H * D], qkv[:, 2 * H * D:2 * H * D + Hkv * D], qkv[:, 2 * H * D + Hkv * D:]
+    kc_o, vc_o = kc.copy(), vc.copy()
+    q_want = OD.qk_norm_rope_bf16(qg, k, v, qw, kw, cos, sin, pos0, kc_o, vc_o, block_ids, n_heads=H, n_kv_heads=Hkv,
+                                  head_dim=D, rot_dim=D, eps=1e-6, block_size=bs)
+    gate = qkv.reshape(-1)[D:]
+    want = OD.attention_exact_bf16(q_want, kc_o, vc_o, block_ids, L, gate, stride, 2 * D, block_size=bs)
+
+    qkv_d, kc_d, vc_d = _dev16(qkv, dev), _dev16(kc, dev), _dev16(vc, dev)
+    bid_d = torch.from_numpy(block_ids).to(dev)
+    cos_d, sin_d = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    qw_d, kw_d = _dev16(qw, dev), _dev16(kw, dev)
+    q_d = torch.empty((S, H, D), dtype=torch.bfloat16, device=dev)
+    out_d = torch.empty((S, H * D), dtype=torch.bfloat16, device=dev)
+    step = torch.tensor([pos0, L, 0, 0], dtype=torch.int32, device=dev)
+    nblk = len(block_ids)
+    _say(f"[gpu] qk rope + attention S={S} H={H} Hkv={Hkv} D={D} pos0={pos0}")
+    _bind()
+    p = qkv_d.data_ptr()
+    for use_step in (False, True):
+        kc_d.copy_(_dev16(kc, dev))
+        vc_d.copy_(_dev16(vc, dev))
+        rd = abi.EkernelQkRopeDesc(S, H, Hkv, D, D, stride, stride, pos0, L + 1, bs, kc.shape[0], nblk, 1e-6)
+        rc = lib.ekernel_qk_norm_rope_bf16(ctypes.byref(rd), ctypes.c_void_p(p), ctypes.c_void_p(p + 2 * H * D * 2),
+                                           ctypes.c_void_p(p + (2 * H * D + Hkv * D) * 2), _vp(qw_d), _vp(kw_d),
+                                           _vp(cos_d), _vp(sin_d), _vp(step if use_step else None), _vp(q_d),
+                                           _vp(kc_d), _vp(vc_d), _vp(bid_d))
+        assert rc == 0, abi.last_error()
+        assert np.array_equal(_bits(q_d), q_want)
+        assert np.array_equal(_bits(kc_d), kc_o) and np.array_equal(_bits(vc_d), vc_o)
+        ad = abi.EkernelAttentionExactDesc(S, H, Hkv, D, L, bs, kc.shape[0], nblk, stride, 2 * D)
+        rc = lib.ekernel_attention_exact_bf16(ctypes.byref(ad), _vp(q_d), _vp(kc_d), _vp(vc_d), _vp(bid_d),
+                                              ctypes.c_void_p(p + D * 2), _vp(step if use_step else None), _vp(out_d))
+        assert rc == 0, abi.last_error()
+        got = _bits(out_d)
+        bad = np.argwhere(got != want)
+        assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()} (step={use_step})"
+
+
+@pytest.mark.parametrize("L", [1, 2, 3, 4, 5, 8, 9, 64, 65, 129, 512])
+def test_attention_decode_lengths_no_gate(lib, dev, L):
+    """Decode over every small length (torch's small-matrix kernel below four
+    positions, the tail rules of the four- and eight-way sums) and chunk edges,
+    without the gate."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(L)
+    H, Hkv, D, bs = 16, 8, 128, 16
+    nblk = (L + bs - 1) // bs
+    block_ids = np.arange(nblk, dtype=np.int32)[::-1].copy()
+    kc, vc = _rand16(rng, (nblk, bs, Hkv, D), 2.0), _rand16(rng, (nblk, bs, Hkv, D))
+    q = _rand16(rng, (1, H, D), 2.0)
+    want = OD.attention_exact_bf16(q, kc, vc, block_ids, L, block_size=bs)
+    out = torch.empty((1, H * D), dtype=torch.bfloat16, device=dev)
+    _bind()
+    _say(f"[gpu] attention decode L={L}")
+    ad = abi.EkernelAttentionExactDesc(1, H, Hkv, D, L, bs, nblk, nblk, 0, 0)
+    qd, kd, vd = _dev16(q, dev), _dev16(kc, dev), _dev16(vc, dev)     # held: the kernel reads them
+    bd = torch.from_numpy(block_ids).to(dev)
+    rc = lib.ekernel_attention_exact_bf16(ctypes.byref(ad), _vp(qd), _vp(kd), _vp(vd), _vp(bd), None, None,
+                                          _vp(out))
+    assert rc == 0, abi.last_error()
+    assert np.array_equal(_bits(out), want)
+
+
+def test_attention_rejects_bad_arguments(lib, dev):
+    import ctypes
+    from pilm_amd import bindings as abi
+    q = torch.zeros((1, 4, 128), dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros((2, 16, 2, 128), dtype=torch.bfloat16, device=dev)
+    bid = torch.zeros(2, dtype=torch.int32, device=dev)
+    out = torch.empty((1, 512), dtype=torch.bfloat16, device=dev)
+    _bind()
+    for desc in (abi.EkernelAttentionExactDesc(1, 4, 2, 128, 33, 16, 2, 2, 0, 0),    # cache_len > table
+                 abi.EkernelAttentionExactDesc(1, 4, 3, 128, 8, 16, 2, 2, 0, 0),     # heads % kv heads
+                 abi.EkernelAttentionExactDesc(1, 4, 2, 96, 8, 16, 2, 2, 0, 0)):     # head_dim
+        assert lib.ekernel_attention_exact_bf16(ctypes.byref(desc), _vp(q), _vp(kc), _vp(kc), _vp(bid), None, None,
+                                                _vp(out)) != 0
+    host = torch.zeros((1, 4, 128), dtype=torch.bfloat16)
+    desc = abi.EkernelAttentionExactDesc(1, 4, 2, 128, 8, 16, 2, 2, 0, 0)
+    assert lib.ekernel_attention_exact_bf16(ctypes.byref(desc), _vp(host), _vp(kc), _vp(kc), _vp(bid), None, None,
+                                            _vp(out)) == -1
+
+
+# ------------------------------------------------------------ silu, greedy
+
+def test_silu_mul_every_bf16_gate(lib, dev):
+    rng = np.random.default_rng(3)
+    n = 65536
+    g = np.arange(n, dtype=np.uint32).astype(np.uint16).reshape(4, n // 4)
+    u = _rand16(rng, (4, n // 4))
+    gu = np.concatenate([g, u], axis=1)                     # one [rows, 2I] buffer as the decoder has it
+    want = OD.silu_mul_bf16(g, u, 4, n // 4, n // 4)
+    gd = _dev16(gu, dev)
+    out = torch.empty((4, n // 4), dtype=torch.bfloat16, device=dev)
+    _bind()
+    p = gd.data_ptr()
+    import ctypes
+    rc = lib.ekernel_silu_mul_bf16(ctypes.c_void_p(p), ctypes.c_void_p(p + (n // 4) * 2), 4, n // 4, n // 2,
+                                   _vp(out))
+    assert rc == 0
+    from pilm_amd import synth as S
+    fin = np.isfinite(S.bf16_bits_to_f32(g)) & np.isfinite(S.bf16_bits_to_f32(want))
+    assert np.array_equal(_bits(out)[fin], want[fin])
+
+
+@pytest.mark.parametrize("n", [1, 5, 4096, 151936])
+def test_greedy_step(lib, dev, n):
+    rng = np.random.default_rng(n)
+    logits = _rand16(rng, (n,), 3.0)
+    if n > 100:
+        top = logits.view(np.uint16)[np.argmax(_f(logits))]
+        logits[[n // 3, n - 2]] = top                      # ties: the lowest index wins
+    want = OD.argmax_bf16(logits)
+    ld = _dev16(logits, dev)
+    state = torch.tensor([10, 11, 2, 0], dtype=torch.int32, device=dev)
+    toks = torch.full((4,), -1, dtype=torch.int32, device=dev)
+    nid = torch.zeros(1, dtype=torch.int64, device=dev)
+    _bind()
+    assert lib.ekernel_greedy_step_bf16(_vp(ld), n, _vp(state), _vp(toks), 4, _vp(nid)) == 0
+    torch.cuda.synchronize()
+    assert state.tolist() == [11, 12, 3, 0]
+    assert toks.tolist() == [-1, -1, want, -1] and nid.item() == want
+
+
+def _f(b):
+    from pilm_amd import synth as S
+    return S.bf16_bits_to_f32(b)
+
+
+# --------------------------------------------------------- the whole decoder
+
+def _fixture(name):
+    return json.loads((GOLDEN / f"decode_{name}.json").read_text())
+
+
+def _decoder(fx, dev, hashes):
+    from pilm_amd import qwen3 as Q
+    c = fx["config"]
+    cfg = Q.Qwen3Config.from_dict(c)
+    w = Q.Qwen3Weights.synthetic(cfg, c["seed"], c["std"], device=dev, hashes=hashes)
+    return w, Q.Qwen3Decoder(w, max_positions=c["prompt"] + c["new_tokens"] + 1, max_new_tokens=c["new_tokens"])
+
+
+def test_decoder_tiny_matches_reference(dev):
+    fx = _fixture("tiny")
+    _say("[gpu] decoder, two-layer model: weights")
+    w, dec = _decoder(fx, dev, hashes=True)
+    assert w.quantized_sha == fx["quantized_sha"]
+    shas = []
+    _say("[gpu] decoder, two-layer model: eager steps with logits")
+    toks = dec.generate(fx["prompt"], len(fx["tokens"]), on_logits=lambda i, lg: shas.append(OD.sha_u16(_bits(lg))))
+    want = [lg["sha"] for lg in fx["logits"]]
+    first = next((i for i, (a, b) in enumerate(zip(shas, want)) if a != b), None)
+    assert first is None, f"logits differ first at step {first}"
+    assert toks == fx["tokens"]
+    _say("[gpu] decoder, two-layer model: graph replay")
+    from pilm_amd import qwen3 as Q
+    dec2 = Q.Qwen3Decoder(w, max_positions=dec.max_pos, max_new_tokens=dec.max_new)
+    assert dec2.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
+    # a second sequence on the same decoder (graph already captured) starts clean
+    assert dec2.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
+
+
+def test_decoder_qwen3_1p7b_matches_reference(dev):
+    """Config 4: Qwen3-1.7B W4A16 g128, 128-token prompt, 256 greedy tokens."""
+    fx = _fixture("qwen3_1p7b")
+    _say("[gpu] decoder Qwen3-1.7B: weights (generated and quantized on the device)")
+    w, dec = _decoder(fx, dev, hashes=True)
+    bad = [k for k in fx["quantized_sha"] if fx["quantized_sha"][k] != w.quantized_sha.get(k)]
+    assert not bad, f"{len(bad)} quantized tensors differ from the reference quantizer's, e.g. {bad[:3]}"
+    _say("[gpu] decoder Qwen3-1.7B: 256 tokens, graph replay")
+    toks = dec.generate(fx["prompt"], len(fx["tokens"]), graph=True)
+    if toks != fx["tokens"]:
+        i = next(i for i in range(len(toks)) if toks[i] != fx["tokens"][i])
+        lg = fx["logits"][i]
+        pytest.fail(f"token {i} differs: {toks[i]} vs {fx['tokens'][i]} (reference top two {lg['top']})")
+    _say("[gpu] decoder Qwen3-1.7B: eager steps, logits of the first 16 tokens")
+    from pilm_amd import qwen3 as Q
+    dec2 = Q.Qwen3Decoder(w, max_positions=dec.max_pos, max_new_tokens=dec.max_new)
+    shas = []
+    dec2.generate(fx["prompt"], 16, on_logits=lambda i, lg: shas.append(OD.sha_u16(_bits(lg))))
+    assert shas == [lg["sha"] for lg in fx["logits"][:16]]

@@ -159,3 +159,83 @@ def test_mfma_tile_heights(bm, wm, fmt, dev, monkeypatch):
     y = run_gpu(fmt, x, w, s, dev)
     ref = gen.run(fmt, x, w, s, "oracle")
     check_close(fmt, y, ref, f"{fmt} BM={bm} WM={wm}")
+
+
+# ----------------------------------------------------- range of the fp16 operands
+
+RANGE_CASES = {
+    # name: (activation factor, scale factor)
+    "tiny_x": (1e-20, 1.0),          # below fp16's normal range
+    "large_x": (1e30, 1.0),          # far beyond 65504
+    "tiny_scales": (1.0, 1e-7),      # group scale x weight in the fp16 subnormals
+    "large_scales": (1.0, 1e6),      # group scale x weight beyond 65504
+    "mixed_rows": (None, 1.0),       # each activation row at its own magnitude, 1e-20 .. 1e20
+}
+
+
+def _scaled_inputs(fmt, case, m=96, n=160, k=1024, seed=77):
+    gen = GV._gen()
+    x, w, s = gen.make_inputs(fmt, m, n, k, seed)
+    xs, ss = RANGE_CASES[case]
+    xf = x.astype(np.float64) if fmt == "w8a32" else S.bf16_bits_to_f32(x).astype(np.float64)
+    if xs is None:
+        xf = xf * (10.0 ** np.linspace(-20, 20, m))[:, None]
+    else:
+        xf = xf * xs
+    x = xf.astype(np.float32) if fmt == "w8a32" else S.f32_to_bf16_bits(xf.astype(np.float32))
+    return x, w, (s.astype(np.float64) * ss).astype(np.float32)
+
+
+@pytest.mark.parametrize("splits", ["auto", "3"])
+@pytest.mark.parametrize("case", list(RANGE_CASES))
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mfma_operand_range(fmt, case, splits, dev, monkeypatch):
+    """Activations and scales far outside fp16's range keep the matrix-core
+    tolerance: each activation row and each weight row is scaled by a power
+    of two into range before the fp16 conversion and scaled back exactly."""
+    if splits != "auto":
+        monkeypatch.setenv("PILM_HIP_MFMA_SPLITS", splits)
+    x, w, s = _scaled_inputs(fmt, case)
+    gen = GV._gen()
+    _say(f"[gpu] mfma range {fmt} {case} splits={splits}")
+    y = run_gpu(fmt, x, w, s, dev)
+    check_close(fmt, y, gen.run(fmt, x, w, s, "oracle"), f"{fmt} {case}")
+
+
+@pytest.mark.parametrize("special", ["large_x", "denormal_x"])
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mfma_golden_extremes_at_prefill_rows(fmt, special, dev):
+    """The golden files' extreme activations (x 1e30, x 1e-39 subnormal),
+    generated the same way at M = 96.  Subnormal outputs carry only a few bits
+    in either order of summation, so the bound adds K subnormal steps."""
+    gen = GV._gen()
+    m, n, k = 96, 70, 256
+    x, w, s = gen.make_inputs(fmt, m, n, k, 4711, special)
+    _say(f"[gpu] mfma golden extreme {fmt} {special}")
+    y = as_f32(fmt, run_gpu(fmt, x, w, s, dev))
+    ref = as_f32(fmt, gen.run(fmt, x, w, s, "oracle"))
+    assert np.all(np.isfinite(y))
+    sub = k * 2.0 ** -149 + (0.0 if fmt == "w8a32" else 2.0 ** -133)
+    tol = TOL_MAX_REL * np.abs(ref).max(axis=1, keepdims=True) + sub
+    bad = np.abs(y - ref) > tol
+    assert not bad.any(), f"{bad.sum()} outputs beyond tolerance"
+
+
+@pytest.mark.parametrize("fmt", ["w8a16", "w4g128", "w4"])
+def test_matrix_core_threshold_setter(fmt, dev):
+    """ecpu_hip_set_matrix_core_min_rows: above M every row stays bit-exact;
+    0 never takes the matrix cores; a negative value returns to the default."""
+    from pilm_amd import bindings as abi
+    gen = GV._gen()
+    x, w, s = gen.make_inputs(fmt, 80, 256, 1024, 321)
+    ref = gen.run(fmt, x, w, s, "oracle")
+    try:
+        for rows in (81, 0):
+            abi.set_matrix_core_min_rows(rows)
+            assert abi.matrix_core_min_rows() == rows
+            _say(f"[gpu] threshold {rows} {fmt} M=80")
+            assert np.array_equal(run_gpu(fmt, x, w, s, dev).view(np.uint8), ref.view(np.uint8))
+    finally:
+        abi.set_matrix_core_min_rows(-1)
+    assert abi.matrix_core_min_rows() == 64
+    check_close(fmt, run_gpu(fmt, x, w, s, dev), ref, f"{fmt} default threshold")

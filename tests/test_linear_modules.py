@@ -155,9 +155,28 @@ def _w4_swiglu(dev, h=256, i=512):
 
 
 @pytest.mark.gpu
+def test_w4_swiglu_module_default_is_reference_default(dev, monkeypatch):
+    """Unset switches: piLM's default path (linear.py:43-49, 534-545) --
+    gate_up GEMV, torch's CPU silu(gate) * up in bf16, down GEMV -- for one
+    row and for several, bit for bit."""
+    from oracle import decoder as OD
+    monkeypatch.delenv("PILM_W4_SWIGLU_FUSED", raising=False)
+    monkeypatch.delenv("PILM_SWIGLU_ACT_BACKEND", raising=False)
+    mod, (x, gu, gs, dw, ds), i = _w4_swiglu(dev)
+    xs = np.concatenate([x, S.activations_bf16(33, 2, x.shape[1])])
+    _say("[gpu] W4 SwiGLU module, default path")
+    for rows in (xs[:1], xs):
+        y = _bits(mod(_dev_bf16(rows, dev)))
+        g_u = O.linear_w4a16_bf16(rows, gu, gs)
+        act = OD.silu_mul_bf16(g_u, g_u[:, i:], rows.shape[0], i, 2 * i)
+        assert np.array_equal(y, O.linear_w4a16_bf16(act, dw, ds))
+
+
+@pytest.mark.gpu
 def test_w4_swiglu_module_fused_and_unfused(dev, monkeypatch):
     mod, ins, i = _w4_swiglu(dev)
     x = ins[0]
+    monkeypatch.setenv("PILM_W4_SWIGLU_FUSED", "1")
     _say("[gpu] W4 SwiGLU module, one row (fused kernel)")
     assert np.array_equal(_bits(mod(_dev_bf16(x, dev).reshape(-1))), O.swiglu_w4a16_bf16(*ins, i)[0])
     # unfused with the library's SwiGLU activation: the same bits, row by row
