@@ -2,15 +2,24 @@
 """Benchmark of the quantized decode GEMV path on one MI355X.
 
 Workload (one "step"): every W4A16 group-128 linear of one Qwen3-1.7B decode
-token, M = 1, in the reference's block layout -- per layer q 4096x2048 (gated
-q_proj), k 1024x2048, v 1024x2048, o 2048x2048, gate 6144x2048,
-up 6144x2048, down 2048x6144, for 28 layers, plus lm_head 151936x2048.
-Every layer has its own weights resident in HBM (0.98 GB per step, far
-beyond the 256 MB Infinity Cache), activations are bf16 ~N(0,1), packed int4
-weights uniform over all 256 byte values, fp32 group scales ~U(0.001, 0.02)
-rounded through fp16.  The step's 197 linear calls go through the C ABI
-entry point ekernel_linear_w4a16g128_bf16, captured once into a HIP graph and
-replayed.
+token, M = 1, in the reference's block layout, as the device decoder
+(pilm_amd.qwen3) issues them -- per layer the q/k/v projections as one
+6144x2048 matrix (gated q 4096 + k 1024 + v 1024 rows), o 2048x2048, gate/up
+as one 12288x2048 matrix, down 2048x6144, for 28 layers, plus lm_head
+151936x2048 (113 calls; --layout separate issues the 197 per-projection
+calls instead; the bytes are the same).  Every layer has its own weights
+resident in HBM (0.98 GB per step, far beyond the 256 MB Infinity Cache),
+activations are bf16 ~N(0,1), packed int4 weights uniform over all 256 byte
+values, fp32 group scales ~U(0.001, 0.02) rounded through fp16.  The calls go
+through the C ABI entry point ekernel_linear_w4a16g128_bf16, captured once
+into a HIP graph and replayed.
+
+Then the whole decoder (--no-decode skips it): Qwen3-1.7B W4A16-g128 with
+random-init weights (seed 1, generated and quantized on the device), a
+128-token prompt prefilled in 16-token chunks, 256 greedy tokens with the
+decode step replayed as one HIP graph; decode tok/s over the 255 graph steps,
+and whether the tokens equal the reference engine's
+(tests/golden/decode_qwen3_1p7b.json).
 
 Printed JSON line:
   value        algorithmic GB/s of the whole step (weights + scales +
@@ -18,11 +27,13 @@ Printed JSON line:
   hbm_copy_GBps  a 1 GiB device copy timed the same way (read + write), the
                attainable streaming rate; pct_of_copy_peak = value against it
   roofline     the g128 GEMV kernels' algorithmic GB/s per launch (the
-               group-quad kernels for the 196 projections, 8-row tiles for
-               k/v/o/down and 16-row tiles for q/gate/up, the 64-row exact
-               kernel for lm_head; they are the step's only kernels): HIP
-               events on the replay stream around the timed replays, divided
-               by the launches, against 8 TB/s
+               group-quad kernels for qkv (16-row tiles) and o/down (8-row
+               tiles), the 64-row exact kernel for gate_up and lm_head; they
+               are the step's only kernels): HIP events on the replay stream
+               around the timed replays, divided by the launches, against
+               8 TB/s
+  decode_tok_s whole-decoder greedy tokens per second (attention, norms, rope,
+               SwiGLU, lm_head and argmax included), HIP graph per token
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
   sweep        per-shape times with --sweep [sections]: g128 (default),
@@ -68,8 +79,12 @@ TRAFFIC_FILE = ROOT / "profiles" / "gemv_w4a16g128_m1_qwen3_1p7b_decode.traffic.
 CALIB_BYTES = 1 << 30                              # copy kernel: reads and writes 1 GiB
 LAYERS = 28
 HIDDEN = 2048
-LAYER_SHAPES = [("q_proj", 4096, 2048), ("k_proj", 1024, 2048), ("v_proj", 1024, 2048), ("o_proj", 2048, 2048),
-                ("gate_proj", 6144, 2048), ("up_proj", 6144, 2048), ("down_proj", 2048, 6144)]
+LAYER_SHAPES_SEPARATE = [("q_proj", 4096, 2048), ("k_proj", 1024, 2048), ("v_proj", 1024, 2048),
+                         ("o_proj", 2048, 2048), ("gate_proj", 6144, 2048), ("up_proj", 6144, 2048),
+                         ("down_proj", 2048, 6144)]
+LAYER_SHAPES_FUSED = [("qkv_proj", 6144, 2048), ("o_proj", 2048, 2048), ("gate_up_proj", 12288, 2048),
+                      ("down_proj", 2048, 6144)]
+LAYER_SHAPES = LAYER_SHAPES_FUSED
 LM_HEAD = ("lm_head", 151936, 2048)
 
 
@@ -80,6 +95,51 @@ def alg_bytes(m: int, n: int, k: int) -> int:
 
 def step_shapes():
     return [(name, n, k) for _ in range(LAYERS) for (name, n, k) in LAYER_SHAPES] + [LM_HEAD]
+
+
+def decode_bench(torch, dev, n_new: int = 256, prompt_len: int = 128, seed: int = 1) -> dict:
+    """The device decoder on Qwen3-1.7B W4A16-g128: prefill, then n_new - 1
+    graph-replayed decode steps timed between HIP events on the replay stream
+    (wall clock beside them)."""
+    from pilm_amd import qwen3 as Q
+    from pilm_amd import synth_model as SM
+    cfg = Q.QWEN3_1P7B
+    t0 = time.perf_counter()
+    w = Q.Qwen3Weights.synthetic(cfg, seed, 0.02, device=dev)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    dec = Q.Qwen3Decoder(w, max_positions=prompt_len + n_new + 1, max_new_tokens=n_new)
+    prompt = SM.token_ids(seed, prompt_len, cfg.vocab).tolist()
+    dec.prefill(prompt)
+    dec.capture()
+    s = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.prefill(prompt)
+    torch.cuda.synchronize()
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(n_new - 1):
+        dec.graph.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu = e0.elapsed_time(e1) / 1e3
+    tokens = dec.tokens[:n_new].tolist()
+    fx_path = ROOT / "tests" / "golden" / "decode_qwen3_1p7b.json"
+    match = None
+    if fx_path.exists():
+        fx = json.loads(fx_path.read_text())
+        if fx["prompt"] == prompt and fx["config"]["seed"] == seed:
+            match = tokens == fx["tokens"][:n_new]
+    steps = n_new - 1
+    return {"decode_tok_s": round(steps / wall, 1), "ms_per_token": round(wall / steps * 1e3, 4),
+            "gpu_ms_per_token": round(gpu / steps * 1e3, 4), "prefill_ms": round(prefill_ms, 2),
+            "prompt_tokens": prompt_len, "new_tokens": n_new, "tokens_match_reference": match,
+            "linear_bytes_per_token": w.linear_bytes_per_token(), "weights_build_s": round(build_s, 2),
+            "launch": "one HIP graph per decode token (state word advanced on device)"}
 
 
 def make_weights(torch, dev, n: int, k: int, gen):
@@ -645,7 +705,12 @@ def main(argv=None) -> int:
     ap.add_argument("--stats-summary", metavar="STATS_CSV")
     ap.add_argument("--attn-pmc-pass", action="store_true")
     ap.add_argument("--attn-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--layout", choices=("fused", "separate"), default="fused",
+                    help="q/k/v and gate/up as one matrix each (the decoder's layout) or one call per projection")
+    ap.add_argument("--no-decode", action="store_true", help="skip the whole-decoder tok/s measurement")
     args = ap.parse_args(argv)
+    global LAYER_SHAPES
+    LAYER_SHAPES = LAYER_SHAPES_FUSED if args.layout == "fused" else LAYER_SHAPES_SEPARATE
     if args.traffic:
         rec = traffic_summary(*args.traffic)
         TRAFFIC_FILE.parent.mkdir(exist_ok=True)
@@ -716,7 +781,8 @@ def main(argv=None) -> int:
         "vs_baseline": None,
         "dtype": "int4 weights x bf16 activations, fp32 accumulate (bit-exact reference order)",
         "data": "synthetic (seeded torch RNG on device), weights resident in HBM",
-        "config": {"workload": "Qwen3-1.7B W4A16-g128 decode linears, one token (28 layers x 7 + lm_head)",
+        "config": {"workload": "Qwen3-1.7B W4A16-g128 decode linears, one token (28 layers x "
+                               f"{len(LAYER_SHAPES)} + lm_head, {args.layout} q/k/v and gate/up)",
                    "M": m, "calls_per_step": len(calls), "alg_bytes_per_step": step_bytes,
                    "entry_point": "ekernel_linear_w4a16g128_bf16", "launch": "HIP graph replay"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
@@ -726,6 +792,14 @@ def main(argv=None) -> int:
         "eager_ms_per_step": round(eager_ms, 3),
         "roofline": roof,
     }
+    if not args.no_decode:
+        del calls, xs, run
+        torch.cuda.empty_cache()
+        print("[bench] whole decoder: Qwen3-1.7B W4A16-g128, 128-token prompt, 256 greedy tokens", flush=True)
+        dec = decode_bench(torch, dev)
+        out["decode_tok_s"] = dec["decode_tok_s"]
+        out["decode"] = dec
+        calls = xs = run = None
     if args.sweep:
         sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "attention", "load") if args.sweep == "all" \
             else tuple(args.sweep.split(","))
