@@ -74,65 +74,64 @@ __device__ __forceinline__ float sleef_expf(float d) {
     return u;
 }
 
-// torch's sum of the squares of n contiguous fp32 values (n >= 32; the
-// squares of bf16 values are exact, as x.pow(2) stores them): chain t (t < 32) of a
-// workgroup's first wave owns lane l = t & 7 of the vectors v = 4r + k, k =
-// t >> 3, accumulated through the 16-row level cascade; the 32 chain values,
-// the vectors left over by the four-way interleave and the scalar tail are
-// then folded by one lane in torch's order.  `x` is in LDS; `tmp` holds 32
-// floats of LDS.  Every thread of the workgroup calls it (it synchronizes)
-// and gets the sum.
-__device__ float torch_row_sumsq(const float *x, int n, float *tmp, float *result) {
-    const int t = threadIdx.x;
+// One chain of torch's row sum of squares (x.pow(2).sum(-1) over n >= 32
+// contiguous fp32 values in LDS; the squares of bf16 values are exact, as
+// x.pow(2) stores them).  Chain t (t < 32) owns lane l = t & 7 of the
+// eight-float vectors v = 4r + k, k = t >> 3, accumulated through the cascade
+// of 16-row levels; the vectors the four-way interleave leaves over go to
+// chain group k = 0.  Loads are issued 16 at a time ahead of their sums.
+__device__ float chain_sumsq(const float *x, int n, int t) {
+    const int k = t >> 3, l = t & 7;
     const int nvec = n / 8, size_ilp = nvec / 4;
-    if (t < 32) {
-        const int k = t >> 3, l = t & 7;
-        int clog = 0;
-        while ((1 << clog) < size_ilp) ++clog;
-        const int level_power = max(4, clog / 4);
-        const int step = 1 << level_power, mask = step - 1;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int r = 0;
-        while (r + step <= size_ilp) {
-            for (int j = 0; j < step; ++j, ++r) acc[0] = acc[0] + sq(x[8 * (4 * r + k) + l]);
-            for (int j = 1; j < 4; ++j) {
-                acc[j] = acc[j] + acc[j - 1];
-                acc[j - 1] = 0.0f;
-                if ((r & (mask << (j * level_power))) != 0) break;
-            }
+    int clog = 0;
+    while ((1 << clog) < size_ilp) ++clog;
+    const int level_power = max(4, clog / 4);
+    const int step = 1 << level_power, mask = step - 1;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int r = 0;
+    while (r + step <= size_ilp) {
+        for (int j0 = 0; j0 < step; j0 += 16) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = x[8 * (4 * (r + j) + k) + l];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[0] = acc[0] + sq(v[j]);
+            r += 16;
         }
-        for (; r < size_ilp; ++r) acc[0] = acc[0] + sq(x[8 * (4 * r + k) + l]);
-        float a = acc[0];
-        for (int j = 1; j < 4; ++j) a = a + acc[j];
-        if (k == 0)
-            for (int v = 4 * size_ilp; v < nvec; ++v) a = a + sq(x[8 * v + l]);
-        tmp[t] = a;
+        for (int j = 1; j < 4; ++j) {
+            acc[j] = acc[j] + acc[j - 1];
+            acc[j - 1] = 0.0f;
+            if ((r & (mask << (j * level_power))) != 0) break;
+        }
     }
-    __syncthreads();
-    if (t == 0) {
-        float fin = 0.0f;
-        for (int i = 8 * nvec; i < n; ++i) fin = fin + sq(x[i]);
-        for (int l = 0; l < 8; ++l) fin = fin + (((tmp[l] + tmp[8 + l]) + tmp[16 + l]) + tmp[24 + l]);
-        *result = fin;
-    }
-    __syncthreads();
-    return *result;
+    for (; r < size_ilp; ++r) acc[0] = acc[0] + sq(x[8 * (4 * r + k) + l]);
+    float a = acc[0];
+    for (int j = 1; j < 4; ++j) a = a + acc[j];
+    if (k == 0)
+        for (int v = 4 * size_ilp; v < nvec; ++v) a = a + sq(x[8 * v + l]);
+    return a;
 }
 
-// GemmaRMSNorm (layers.py:130-147) of one row held in LDS as fp32 values:
-// bf16((w + 1) * bf16(x * rsqrt(mean(x^2) + eps))).
-__device__ void gemma_norm_row(float *xs, int n, const uint16_t *__restrict__ w, float eps, float *tmp,
-                               float *result, uint16_t *__restrict__ out) {
-    const float sum = torch_row_sumsq(xs, n, tmp, result);
-    const float r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sum, (float)n) + eps));
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float y = bfr(xs[i] * r);
-        const float wp = bfr(bf(w[i]) + 1.0f);
-        const uint16_t o = f32_to_bf16(wp * y);
-        if (out) out[i] = o;
-        xs[i] = bf(o);
-    }
-    __syncthreads();
+// 1 / sqrt(mean(x^2) + eps) of a row in LDS, computed by one whole wave
+// (every lane gets it): the 32 chains, their lanes folded
+// ((c0 + c1) + c2) + c3 across the four chain groups, then the scalar tail and
+// the eight lanes added to 0 in order -- torch's sum -- divided by n.
+__device__ float wave_row_rsqrt(const float *x, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    const float c = lane < 32 ? chain_sumsq(x, n, lane) : 0.0f;
+    const int l = lane & 7;
+    const float p = ((c + __shfl(c, l + 8)) + __shfl(c, l + 16)) + __shfl(c, l + 24);
+    float fin = 0.0f;
+    for (int i = (n / 8) * 8; i < n; ++i) fin = fin + sq(x[i]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fin = fin + __shfl(p, j);
+    return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(fin, (float)n) + eps));
+}
+
+// GemmaRMSNorm (layers.py:130-147) output of one element: bf16((w + 1) *
+// bf16(h * r)).
+__device__ __forceinline__ uint16_t gemma_out(float h, float r, uint16_t w) {
+    return f32_to_bf16(bfr(bf(w) + 1.0f) * bfr(h * r));
 }
 
 // ---- residual add + GemmaRMSNorm ------------------------------------------
@@ -142,7 +141,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
                                                       const uint16_t *__restrict__ w, uint16_t *__restrict__ out,
                                                       uint16_t *__restrict__ res_out, int n, float eps) {
     extern __shared__ float lds[];
-    float *xs = lds, *tmp = lds + n, *result = tmp + 32;
+    float *xs = lds, *rsh = lds + n;
     const size_t row = (size_t)blockIdx.x * n;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         float h = bf(x[row + i]);
@@ -153,32 +152,41 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
         xs[i] = h;
     }
     __syncthreads();
-    gemma_norm_row(xs, n, w, eps, tmp, result, out + row);
+    if (threadIdx.x < 64) {
+        const float r = wave_row_rsqrt(xs, n, eps);
+        if (threadIdx.x == 0) *rsh = r;
+    }
+    __syncthreads();
+    const float r = *rsh;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[row + i] = gemma_out(xs[i], r, w[i]);
 }
 
 // ---- q/k GemmaRMSNorm + rope + cache write ---------------------------------
-// Workgroup (s, head): head < H normalizes q (the first D of the head's 2D
+// One wave per (s, head): head < H normalizes q (the first D of the head's 2D
 // q_proj outputs) into q_out[s, head, :]; head >= H normalizes k of kv head
 // head - H and stores it, with v, into the cache at position pos0 + s.  Rope
 // (layers.py:150-195, NeoX halves) on the first rot dims: with c, s the fp32
 // tables at the position, (a, b) = (x[f], x[f + rot/2]) becomes
 // (a c - b s, a s + b c), each product and sum rounded, then bf16.
-__global__ __launch_bounds__(128) void qk_rope_kernel(
+__global__ __launch_bounds__(64) void qk_rope_kernel(
     const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
     size_t q_stride, size_t kv_stride, const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
     const float *__restrict__ cos_t, const float *__restrict__ sin_t, int max_pos, const int32_t *__restrict__ step,
     int pos0_host, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
     const int32_t *__restrict__ block_ids, int n_block_ids, int block_size, int num_blocks, int H, int Hkv, int D,
     int rot, float eps) {
-    extern __shared__ float lds[];
-    float *xs = lds, *tmp = lds + D, *result = tmp + 32;
+    __shared__ float xs[256];
     const int s = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
     const bool is_q = head < H;
     const int hk = is_q ? head : head - H;
     const uint16_t *src = is_q ? qg + (size_t)s * q_stride + (size_t)hk * 2 * D : kin + (size_t)s * kv_stride + (size_t)hk * D;
-    for (int i = t; i < D; i += blockDim.x) xs[i] = bf(src[i]);
+    for (int i = t; i < D; i += 64) xs[i] = bf(src[i]);
     __syncthreads();
-    gemma_norm_row(xs, D, is_q ? qw : kw, eps, tmp, result, nullptr);
+    const float r = wave_row_rsqrt(xs, D, eps);
+    const uint16_t *nw = is_q ? qw : kw;
+    __syncthreads();
+    for (int i = t; i < D; i += 64) xs[i] = bf(gemma_out(xs[i], r, nw[i]));
+    __syncthreads();
     const int pos = (step ? step[0] : pos0_host) + s;
     const int pc = min(max(pos, 0), max_pos - 1);
     const int nf = rot / 2;
@@ -191,9 +199,9 @@ __global__ __launch_bounds__(128) void qk_rope_kernel(
         const size_t row = (((size_t)blk * block_size + pos % block_size) * Hkv + hk) * D;
         dst = k_cache + row;
         const uint16_t *vs = vin + (size_t)s * kv_stride + (size_t)hk * D;
-        for (int i = t; i < D; i += blockDim.x) v_cache[row + i] = vs[i];
+        for (int i = t; i < D; i += 64) v_cache[row + i] = vs[i];
     }
-    for (int i = t; i < D; i += blockDim.x) {
+    for (int i = t; i < D; i += 64) {
         float o = xs[i];
         if (i < rot) {
             const int f = i < nf ? i : i - nf;
@@ -208,25 +216,62 @@ __global__ __launch_bounds__(128) void qk_rope_kernel(
 // ---- attention in torch's CPU order ----------------------------------------
 // Workgroup (kv head, query row s, column slice z) computes the rep = H / Hkv
 // heads that read this kv head, for head dimensions [z * DS, z * DS + DS).
-// Scores of the visible positions j <= cache_len - S + s go to LDS (bf16
-// values as fp32) and become softmax weights per head; then thread
-// (head, column, chain k) sums its chain of P.V (positions j = k mod 4; the
-// tail beyond the last multiple of four on chain 0) from value rows staged in
-// LDS 64 positions at a time, and chain 0's thread folds the four chains in
-// order and applies the gate.  naive: torch's small product kernel
+// The slice of every visible value row (64 bytes each) is copied into LDS by
+// DMA at the start, up to vcap positions per pass, so the copy overlaps the
+// scores and the softmax.  Scores of the visible positions j <= cache_len -
+// S + s go to LDS (bf16 values as fp32) and become softmax weights per head;
+// then thread (head, column, chain k) sums its chain of P.V (positions
+// j = k mod 4; the tail beyond the last multiple of four on chain 0) from the
+// staged rows, and chain 0's thread folds the four chains in order and
+// applies the gate.  naive: torch's small product kernel
 // (S * cache_len * D < 400) sums both dots in plain order.
-constexpr int kChunk = 64;     // positions per staged value chunk
-constexpr int kDS = 32;        // head dimensions per workgroup
+constexpr int kDS = 32;        // head dimensions per workgroup (64-byte value rows)
+
+template <int D>
+__device__ __forceinline__ float score_dot(const float *qr, const uint32_t (&kv)[D / 2], bool naive) {
+    if (naive) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D; ++i) dot = dot + qr[i] * (i & 1 ? bf16_hi(kv[i / 2]) : bf16_lo(kv[i / 2]));
+        return dot;
+    }
+    float p[D / 2];
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i) {
+        const int i2 = i + D / 2;
+        const float ka = i & 1 ? bf16_hi(kv[i / 2]) : bf16_lo(kv[i / 2]);
+        const float kb = i2 & 1 ? bf16_hi(kv[i2 / 2]) : bf16_lo(kv[i2 / 2]);
+        p[i] = __builtin_fmaf(qr[i], ka, qr[i2] * kb);
+    }
+#pragma unroll
+    for (int w = D / 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
+    return p[0];
+}
+
+template <int D>
+__device__ __forceinline__ void load_krow(const uint16_t *kr, uint32_t (&kv)[D / 2]) {
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        const u32x4 c = ((const u32x4 *)kr)[i];
+        kv[4 * i] = c[0];
+        kv[4 * i + 1] = c[1];
+        kv[4 * i + 2] = c[2];
+        kv[4 * i + 3] = c[3];
+    }
+}
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_exact_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache,
     const int32_t *__restrict__ block_ids, int n_block_ids, int num_blocks, int block_size,
     const uint16_t *__restrict__ gate, size_t gate_row_stride, size_t gate_head_stride,
-    const int32_t *__restrict__ step, int cache_len_host, int S, int H, int Hkv, int max_len, float scale,
+    const int32_t *__restrict__ step, int cache_len_host, int S, int H, int Hkv, int max_len, int vcap, float scale,
     uint16_t *__restrict__ out) {
     extern __shared__ float lds[];
     const int kh = blockIdx.x, s = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
     const int rep = H / Hkv;
     int cache_len = step ? step[1] : cache_len_host;
     cache_len = min(max(cache_len, S), max_len);
@@ -237,61 +282,51 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
     float *sc = qs + rep * D;                                  // [rep][scs]
     float *part = sc + (size_t)rep * scs;                      // [rep][kDS][4] chain sums
     int *bids = (int *)(part + rep * kDS * 4);                 // [n_block_ids]
-    uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [2][kChunk][kDS]
+    uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [vcap][kDS]
+    const int d0 = z * kDS;
+    for (int i = t; i < n_block_ids; i += blockDim.x) bids[i] = min(max(block_ids[i], 0), num_blocks - 1);
     for (int i = t; i < rep * D; i += blockDim.x) {
         const int r = i / D, d = i % D;
         qs[i] = bf(q[((size_t)s * H + kh * rep + r) * D + d]);
     }
-    for (int i = t; i < n_block_ids; i += blockDim.x) bids[i] = min(max(block_ids[i], 0), num_blocks - 1);
     __syncthreads();
 
     auto row_of = [&](int j) -> size_t {
         const int blk = bids[min(j / block_size, n_block_ids - 1)];
         return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
     };
-
-    // scores
-    for (int j = t; j < vis; j += blockDim.x) {
-        const u32x4 *kr = (const u32x4 *)(k_cache + row_of(j));
-        uint32_t kv[D / 2];
-#pragma unroll
-        for (int i = 0; i < D / 8; ++i) {
-            const u32x4 c = kr[i];
-            kv[4 * i] = c[0];
-            kv[4 * i + 1] = c[1];
-            kv[4 * i + 2] = c[2];
-            kv[4 * i + 3] = c[3];
+    // value rows [j0, j0 + vcap) of this slice into vs: 16 bytes per lane,
+    // four lanes per row; rows past the visible ones repeat the last visible
+    // row (never read).
+    auto stage_v = [&](int j0) {
+        const int nrows = min(vcap, vis - j0);
+        const int pieces = ((nrows * 4 + 255) / 256) * 256;   // whole instructions of every wave
+        for (int base = 0; base < pieces; base += 256) {
+            const int idx = base + t;
+            const int j = j0 + min(idx >> 2, nrows - 1);
+            const uint16_t *src = v_cache + row_of(j) + d0 + 8 * (idx & 3);
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(vs + (size_t)(base + wave * 64) * 8), 16,
+                                             0, 0);
         }
+    };
+    stage_v(0);
+
+    // scores: two positions per thread in flight (one for 256-wide heads)
+    constexpr int kPer = D <= 128 ? 2 : 1;
+    for (int j = t; j < vis; j += kPer * blockDim.x) {
+        const int j2 = kPer == 2 ? j + blockDim.x : vis;
+        uint32_t ka[D / 2], kb[D / 2];
+        load_krow<D>(k_cache + row_of(j), ka);
+        if (j2 < vis) load_krow<D>(k_cache + row_of(j2), kb);
         for (int r = 0; r < rep; ++r) {
             const float *qr = qs + r * D;
-            float dot;
-            if (naive) {
-                dot = 0.0f;
-#pragma unroll
-                for (int i = 0; i < D; ++i)
-                    dot = dot + qr[i] * (i & 1 ? bf16_hi(kv[i / 2]) : bf16_lo(kv[i / 2]));
-            } else {
-                float p[D / 2];
-#pragma unroll
-                for (int i = 0; i < D / 2; ++i) {
-                    const int i2 = i + D / 2;
-                    const float ka = i & 1 ? bf16_hi(kv[i / 2]) : bf16_lo(kv[i / 2]);
-                    const float kb = i2 & 1 ? bf16_hi(kv[i2 / 2]) : bf16_lo(kv[i2 / 2]);
-                    p[i] = __builtin_fmaf(qr[i], ka, qr[i2] * kb);
-                }
-#pragma unroll
-                for (int w = D / 4; w >= 1; w >>= 1)
-#pragma unroll
-                    for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
-                dot = p[0];
-            }
-            sc[(size_t)r * scs + j] = bfr(bfr(dot) * scale);
+            sc[(size_t)r * scs + j] = bfr(bfr(score_dot<D>(qr, ka, naive)) * scale);
+            if (j2 < vis) sc[(size_t)r * scs + j2] = bfr(bfr(score_dot<D>(qr, kb, naive)) * scale);
         }
     }
     __syncthreads();
 
     // softmax per head: wave r (looping when rep exceeds the wave count)
-    const int wave = t >> 6, lane = t & 63;
     for (int r = wave; r < rep; r += blockDim.x / 64) {
         float *x = sc + (size_t)r * scs;
         float mx = -__builtin_inff();
@@ -304,10 +339,19 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float sum = 0.0f;
         if (cache_len >= 8) {
+            // lane c < 8: chain c = positions j = c mod 8, in order from x[c]
             float a = 0.0f;
             if (lane < 8) {
                 a = lane < vis ? x[lane] : 0.0f;
-                for (int j = lane + 8; j < vis; j += 8) a = a + x[j];
+                int j = lane + 8;
+                for (; j + 56 < vis; j += 64) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = x[j + 8 * u];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) a = a + v[u];
+                }
+                for (; j < vis; j += 8) a = a + x[j];
             }
             const float b = a + __shfl_xor(a, 4);    // lanes c < 4: (c) + (c + 4)
             const float c = b + __shfl_xor(b, 2);    // ((0+4) + (2+6)), ((1+5) + (3+7))
@@ -318,50 +362,48 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
         const float inv = __fdiv_rn(1.0f, sum);
         for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
     }
-    __syncthreads();
 
-    // P.V: thread (r, column c, chain k); value rows of this slice staged in LDS
+    // P.V: thread (r, column c, chain k) over the staged value rows
     const int main_len = naive ? 0 : (cache_len / 4) * 4;
     const int nthr = rep * kDS * 4;
-    const int d0 = z * kDS;
-    auto stage = [&](int ch, int buf) {
-        // kChunk rows x kDS columns of bf16 = kChunk x 64 bytes, 16 bytes per thread
-        uint16_t *dst = vs + (size_t)buf * kChunk * kDS;
-        for (int i = t; i < kChunk * (kDS / 8); i += blockDim.x) {
-            const int jj = i / (kDS / 8), piece = i % (kDS / 8);
-            const int j = ch * kChunk + jj;
-            u32x4 val = {0u, 0u, 0u, 0u};
-            if (j < vis) val = *(const u32x4 *)(v_cache + row_of(j) + d0 + 8 * piece);
-            *(u32x4 *)(dst + jj * kDS + 8 * piece) = val;
-        }
-    };
-    const int nch = (vis + kChunk - 1) / kChunk;
     for (int base = 0; base < nthr; base += blockDim.x) {
         const int i = base + t;
         const bool active = i < nthr;
         const int r = active ? i / (kDS * 4) : 0, c = (i / 4) % kDS, k = i & 3;
         const float *w = sc + (size_t)r * scs;
         float acc = 0.0f;
-        stage(0, 0);
-        __syncthreads();
-        for (int ch = 0; ch < nch; ++ch) {
-            if (ch + 1 < nch) stage(ch + 1, (ch + 1) & 1);
-            const uint16_t *vb = vs + (size_t)(ch & 1) * kChunk * kDS;
-            const int j0 = ch * kChunk, j1 = min(vis, j0 + kChunk);
+        for (int j0 = 0; j0 < vis; j0 += vcap) {
+            if (j0 > 0 || base > 0) {
+                __syncthreads();          // the previous rows have been read
+                stage_v(j0);
+            }
+            wait_vmcnt<0>();
+            __syncthreads();              // every wave's copies (and the weights) are in
+            const int j1 = min(vis, j0 + vcap);
             if (active) {
                 if (naive) {
                     if (k == 0)
-                        for (int j = j0; j < j1; ++j) acc = __builtin_fmaf(w[j], bf(vb[(j - j0) * kDS + c]), acc);
+                        for (int j = j0; j < j1; ++j) acc = __builtin_fmaf(w[j], bf(vs[(j - j0) * kDS + c]), acc);
                 } else {
                     // chain k: positions j = k mod 4 below main_len; chain 0 also takes the tail
-                    for (int j = j0 + k; j < min(j1, main_len); j += 4)
-                        acc = __builtin_fmaf(w[j], bf(vb[(j - j0) * kDS + c]), acc);
+                    int j = j0 + ((k - j0) & 3);
+                    const int jm = min(j1, main_len);
+                    for (; j + 12 < jm; j += 16) {
+                        float wv[4], vv[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            wv[u] = w[j + 4 * u];
+                            vv[u] = bf(vs[(j + 4 * u - j0) * kDS + c]);
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) acc = __builtin_fmaf(wv[u], vv[u], acc);
+                    }
+                    for (; j < jm; j += 4) acc = __builtin_fmaf(w[j], bf(vs[(j - j0) * kDS + c]), acc);
                     if (k == 0)
-                        for (int j = max(j0, main_len); j < j1; ++j)
-                            acc = __builtin_fmaf(w[j], bf(vb[(j - j0) * kDS + c]), acc);
+                        for (j = max(j0, main_len); j < j1; ++j)
+                            acc = __builtin_fmaf(w[j], bf(vs[(j - j0) * kDS + c]), acc);
                 }
             }
-            __syncthreads();
         }
         if (active) part[i - base] = acc;
         __syncthreads();
@@ -376,7 +418,6 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
             }
             out[((size_t)s * H + h) * D + d] = f32_to_bf16(o);
         }
-        __syncthreads();
     }
 }
 
@@ -394,54 +435,60 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 }
 
 // ---- greedy step ------------------------------------------------------------
-// argmax of bf16 logits (first index of the largest value: torch.argmax on
-// the fp32 copy for finite logits), then the decode state advances:
-// tokens[count] = id, next_id = id, pos0 = cache_len, cache_len += 1, count += 1.
-__global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t *__restrict__ logits, int n,
-                                                      int32_t *__restrict__ state, int32_t *__restrict__ tokens,
-                                                      int64_t *__restrict__ next_id, int max_tokens) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    const int t = threadIdx.x;
-    float bv = -__builtin_inff();
-    int bi = 0x7FFFFFFF;
-    for (int i = t; i < n; i += 1024) {
-        const float v = bf(logits[i]);
-        if (v > bv || (v == bv && i < bi)) {
-            bv = v;
-            bi = i;
+// argmax of bf16 logits as the first index of the largest value (torch.argmax
+// on the fp32 copy, for finite logits): every position becomes the 64-bit key
+// (order-preserving bits of the value) << 32 | (2^32 - 1 - index), whose
+// maximum is that position; workgroups fold 16-byte loads of logits into a
+// key and atomically raise one shared key.  The advance kernel reads it,
+// clears it for the next call and moves the decode state on:
+// tokens[count] = id, next_id = id, pos0 = cache_len, cache_len += 1,
+// count += 1.
+__device__ __forceinline__ unsigned long long arg_key(float v, uint32_t idx) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)o << 32) | (0xFFFFFFFFu - idx);
+}
+
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) {
+    return a > b ? a : b;
+}
+
+__global__ __launch_bounds__(256) void argmax_key_kernel(const uint16_t *__restrict__ logits, int n,
+                                                         unsigned long long *__restrict__ key) {
+    const int chunks = n / 8;
+    unsigned long long best = 0;
+    for (int c = blockIdx.x * 256 + threadIdx.x; c < chunks; c += gridDim.x * 256) {
+        const u32x4 v = ((const u32x4 *)logits)[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            best = max_u64(best, arg_key(bf16_lo(v[e]), (uint32_t)(8 * c + 2 * e)));
+            best = max_u64(best, arg_key(bf16_hi(v[e]), (uint32_t)(8 * c + 2 * e + 1)));
         }
     }
+    if (blockIdx.x == 0)
+        for (int i = chunks * 8 + threadIdx.x; i < n; i += 256) best = max_u64(best, arg_key(bf(logits[i]), (uint32_t)i));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-        }
+        const unsigned long long o = ((unsigned long long)(uint32_t)__shfl_xor((int)(best >> 32), off) << 32) |
+                                     (uint32_t)__shfl_xor((int)(uint32_t)best, off);
+        best = max_u64(best, o);
     }
-    if ((t & 63) == 0) {
-        sv[t >> 6] = bv;
-        si[t >> 6] = bi;
-    }
-    __syncthreads();
-    if (t == 0) {
-        bv = sv[0];
-        bi = si[0];
-        for (int w = 1; w < 16; ++w)
-            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
-                bv = sv[w];
-                bi = si[w];
-            }
-        if (bi == 0x7FFFFFFF) bi = 0;
-        const int count = state[2];
-        if (count < max_tokens) tokens[count] = bi;
-        state[2] = count + 1;
-        next_id[0] = bi;
-        state[0] = state[1];
-        state[1] = state[1] + 1;
-    }
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_max(key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(64) void greedy_advance_kernel(unsigned long long *__restrict__ key,
+                                                            int32_t *__restrict__ state, int32_t *__restrict__ tokens,
+                                                            int64_t *__restrict__ next_id, int max_tokens) {
+    if (threadIdx.x != 0) return;
+    const unsigned long long k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int id = k ? (int)(0xFFFFFFFFu - (uint32_t)k) : 0;
+    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int count = state[2];
+    if (count < max_tokens) tokens[count] = id;
+    state[2] = count + 1;
+    next_id[0] = id;
+    state[0] = state[1];
+    state[1] = state[1] + 1;
 }
 
 }  // namespace
@@ -466,7 +513,7 @@ int ekernel_rmsnorm_gemma_bf16(const ekernel_rmsnorm_desc_t *desc, const uint16_
     if (rc == ECPU_OK) rc = check_device_buffer(out, bytes, "out", fn);
     if (rc == ECPU_OK && residual_out) rc = check_device_buffer(residual_out, bytes, "residual_out", fn);
     if (rc != ECPU_OK) return rc;
-    const size_t lds = (n + 64) * sizeof(float);
+    const size_t lds = (n + 4) * sizeof(float);
     rmsnorm_kernel<<<(unsigned)M, 256, lds, current_stream()>>>(x, residual, weight, out, residual_out, (int)n,
                                                                 desc->eps);
     return check_launch(fn);
@@ -497,8 +544,7 @@ int ekernel_qk_norm_rope_bf16(const ekernel_qk_rope_desc_t *desc, const uint16_t
     if (rc == ECPU_OK) rc = check_device_buffer(sin_table, d.max_positions * (d.rot_dim / 2) * 4, "sin_table", fn);
     if (rc != ECPU_OK) return rc;
     const dim3 grid((unsigned)d.S, (unsigned)(d.n_heads + d.n_kv_heads));
-    const size_t lds = (D + 64) * sizeof(float);
-    qk_rope_kernel<<<grid, 128, lds, current_stream()>>>(
+    qk_rope_kernel<<<grid, 64, 0, current_stream()>>>(
         qg, k, v, d.q_stride, d.kv_stride, q_norm_w, k_norm_w, cos_table, sin_table, (int)d.max_positions, step, (int)d.pos0,
         q_out, k_cache, v_cache, block_ids, (int)d.n_block_ids, (int)d.block_size, (int)d.num_blocks,
         (int)d.n_heads, (int)d.n_kv_heads, (int)D, (int)d.rot_dim, d.eps);
@@ -521,10 +567,14 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
     if (!step && (d.cache_len < d.S || d.cache_len > max_len))
         return fail(ECPU_ERR_PARAM, "%s: cache_len %zu outside [S, %zu]", fn, d.cache_len, max_len);
     const size_t rep = d.n_heads / d.n_kv_heads, D = d.head_dim;
-    const size_t lds = (rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * kDS * 4 + ((d.n_block_ids + 3) & ~(size_t)3)) * 4 +
-                       2 * kChunk * kDS * 2;
-    if (lds > 64 * 1024)
+    const size_t fixed = (rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * kDS * 4 +
+                          ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
+    // value rows staged per pass: all of them when they fit, in 64-row steps
+    const size_t room = fixed < 64 * 1024 ? (64 * 1024 - fixed) / (kDS * 2) : 0;
+    const size_t vcap = std::min<size_t>(room / 64 * 64, (max_len + 63) / 64 * 64);
+    if (vcap < 64)
         return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu positions x %zu heads per kv head exceed LDS", fn, max_len, rep);
+    const size_t lds = fixed + vcap * kDS * 2;
     const size_t cache_bytes = d.num_blocks * d.block_size * d.n_kv_heads * D * 2;
     int rc = check_device_buffer(q, d.S * d.n_heads * D * 2, "q", fn);
     if (rc == ECPU_OK) rc = check_device_buffer(k_cache, cache_bytes, "k_cache", fn);
@@ -539,7 +589,8 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
     attn_exact_kernel<DD><<<grid, 256, lds, st>>>(q, k_cache, v_cache, block_ids, (int)d.n_block_ids,             \
                                                   (int)d.num_blocks, (int)d.block_size, gate, d.gate_row_stride,    \
                                                   d.gate_head_stride, step, (int)d.cache_len, (int)d.S,             \
-                                                  (int)d.n_heads, (int)d.n_kv_heads, (int)max_len, scale, out)
+                                                  (int)d.n_heads, (int)d.n_kv_heads, (int)max_len, (int)vcap, scale, \
+                                                  out)
     if (D == 64) PILM_ATTN_EXACT(64);
     else if (D == 128) PILM_ATTN_EXACT(128);
     else PILM_ATTN_EXACT(256);
@@ -568,12 +619,24 @@ int ekernel_greedy_step_bf16(const uint16_t *logits, size_t n, int32_t *state, i
                              int64_t *next_id) {
     static const char *fn = "ekernel_greedy_step_bf16";
     if (!logits || !state || !tokens || !next_id || n == 0) return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    if (n >= 0x7FFFFFFFu) return fail(ECPU_ERR_PARAM, "%s: %zu logits", fn, n);
     int rc = check_device_buffer(logits, n * 2, "logits", fn);
     if (rc == ECPU_OK) rc = check_device_buffer(state, 3 * 4, "state", fn);
     if (rc == ECPU_OK) rc = check_device_buffer(tokens, max_tokens * 4, "tokens", fn);
     if (rc == ECPU_OK) rc = check_device_buffer(next_id, 8, "next_id", fn);
     if (rc != ECPU_OK) return rc;
-    greedy_kernel<<<1, 1024, 0, current_stream()>>>(logits, (int)n, state, tokens, next_id, (int)max_tokens);
+    if (((uintptr_t)logits & 15) != 0) return fail(ECPU_ERR_PARAM, "%s: logits not 16-byte aligned", fn);
+    hipStream_t st = current_stream();
+    // the shared key: tickets 4092-4093 of the per-device split-K set (zero
+    // between calls; the K-split kernels use tickets below 4092)
+    float *P = nullptr;
+    int *T = nullptr;
+    rc = split_scratch(st, 0, 4096, &P, &T, fn);
+    if (rc != ECPU_OK) return rc;
+    unsigned long long *key = (unsigned long long *)(T + 4092);
+    const unsigned blocks = (unsigned)std::min<size_t>(256, std::max<size_t>(1, (n / 8 + 255) / 256));
+    argmax_key_kernel<<<blocks, 256, 0, st>>>(logits, (int)n, key);
+    greedy_advance_kernel<<<1, 64, 0, st>>>(key, state, tokens, next_id, (int)max_tokens);
     return check_launch(fn);
 }
 
