@@ -191,6 +191,17 @@ int ekernel_linear_w8a16_bf16_argmax(const ekernel_linear_w8a32_desc_t *desc, co
                                      const int8_t *W, const float *scales, size_t *out_index,
                                      float *out_value, ekernel_isa_t isa);
 
+/* The same result with no allocation at all: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * intermediates (the bf16 logits, per-workgroup partials, result, ticket)
+ * live in a file-scope device array of about 0.5 MB that each GPU keeps until
+ * the process ends, so N is limited to 262144 (larger N: ECPU_ERR_UNSUPPORTED).
+ * Calls that overlap in time on one GPU share that array and race. */
+int ekernel_linear_w8a16_bf16_argmax_noalloc(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                                             const int8_t *W, const float *scales, size_t *out_index,
+                                             float *out_value, ekernel_isa_t isa);
+
 /*                                                          kernel/api.h:44-50 */
 typedef struct {
     size_t M;

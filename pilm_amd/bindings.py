@@ -212,6 +212,9 @@ def _configure(lib):
             ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
         lib.ekernel_linear_w8a16_bf16_argmax.restype = ctypes.c_int
+    if hasattr(lib, "ekernel_linear_w8a16_bf16_argmax_noalloc"):
+        lib.ekernel_linear_w8a16_bf16_argmax_noalloc.argtypes = lib.ekernel_linear_w8a16_bf16_argmax.argtypes
+        lib.ekernel_linear_w8a16_bf16_argmax_noalloc.restype = ctypes.c_int
     if hasattr(lib, "ekernel_swiglu_w4a16_bf16"):
         lib.ekernel_swiglu_w4a16_bf16.argtypes = [
             ctypes.POINTER(EkernelW4A16SwiGLUDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,

@@ -99,6 +99,15 @@ int run_linear_argmax_w8a16(size_t N, size_t K, const uint16_t *A, const uint8_t
                             size_t *out_index, float *out_value, bool index_on_device, bool value_on_device,
                             const char *fn);
 
+// The same with every intermediate (logits, parked pairs, result, ticket) in
+// a file-scope device array instead of allocated scratch: no allocation at
+// all; N <= kStaticArgmaxMaxN (else ECPU_ERR_UNSUPPORTED); overlapping calls
+// on one GPU race on the array.
+constexpr size_t kStaticArgmaxMaxN = 262144;
+int run_linear_argmax_w8a16_static(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S,
+                                   size_t *out_index, float *out_value, bool index_on_device, bool value_on_device,
+                                   const char *fn);
+
 // The W4 SwiGLU MLP of one token: C[H] = down(bf16(silu(g) * u)) with g, u
 // the first and second I rows of the gate/up GEMV over K inputs.
 int run_swiglu_w4(size_t H, size_t I, size_t K, const uint16_t *A, const uint8_t *Wgu, const float *Sgu,

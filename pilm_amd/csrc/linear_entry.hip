@@ -185,6 +185,33 @@ int ekernel_linear_w8a16_bf16_argmax(const ekernel_linear_w8a32_desc_t *desc, co
     return run_linear_argmax_w8a16(N, K, A, (const uint8_t *)W, scales, out_index, out_value, idx_dev, val_dev, fn);
 }
 
+int ekernel_linear_w8a16_bf16_argmax_noalloc(const ekernel_linear_w8a32_desc_t *desc, const uint16_t *A,
+                                             const int8_t *W, const float *scales, size_t *out_index,
+                                             float *out_value, ekernel_isa_t isa) {
+    const char *fn = "ekernel_linear_w8a16_bf16_argmax_noalloc";
+    (void)isa;
+    if (!desc || !A || !W || !scales || !out_index || !out_value) return fail(ECPU_ERR_PARAM, "%s: NULL argument", fn);
+    if (desc->M != 1 || desc->N == 0 || desc->K == 0)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: needs M == 1 and N, K > 0 (got M=%zu N=%zu K=%zu)", fn, desc->M,
+                    desc->N, desc->K);
+    const size_t N = desc->N, K = desc->K;
+    if (N > kStaticArgmaxMaxN)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: N = %zu exceeds the %zu logits its static scratch holds", fn, N,
+                    kStaticArgmaxMaxN);
+    if (K >= ((size_t)1 << 31)) return fail(ECPU_ERR_PARAM, "%s: K must be < 2^31", fn);
+    size_t w_bytes;
+    if (!mul_ok(N, K, &w_bytes)) return fail(ECPU_ERR_PARAM, "%s: shape overflows size_t", fn);
+    int rc;
+    if ((rc = check_buf(A, 2 * K, "A", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(W, w_bytes, "W", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(scales, 4 * N, "scales", fn)) != ECPU_OK) return rc;
+    const bool idx_dev = is_device_pointer(out_index), val_dev = is_device_pointer(out_value);
+    if (idx_dev && (rc = check_buf(out_index, sizeof(size_t), "out_index", fn)) != ECPU_OK) return rc;
+    if (val_dev && (rc = check_buf(out_value, sizeof(float), "out_value", fn)) != ECPU_OK) return rc;
+    return run_linear_argmax_w8a16_static(N, K, A, (const uint8_t *)W, scales, out_index, out_value, idx_dev, val_dev,
+                                          fn);
+}
+
 int ekernel_swiglu_w4a16_bf16(const ekernel_w4a16_swiglu_desc_t *desc, const uint16_t *A, const uint8_t *gate_up_W,
                               const float *gate_up_scales, const uint8_t *down_W, const float *down_scales,
                               uint16_t *C, ekernel_isa_t isa) {

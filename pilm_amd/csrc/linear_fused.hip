@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 
 #include "gemv_device.h"
 #include "internal.h"
@@ -134,6 +135,10 @@ __global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t *__rest
 
 constexpr size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+__global__ void clear_int_kernel(int *p) {
+    if (threadIdx.x == 0) *p = 0;
+}
+
 }  // namespace
 
 int run_swiglu_bf16(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t st, const char *fn) {
@@ -142,32 +147,22 @@ int run_swiglu_bf16(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t 
     return check_launch(fn);
 }
 
-int run_linear_argmax_w8a16(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S,
-                            size_t *out_index, float *out_value, bool index_on_device, bool value_on_device,
-                            const char *fn) {
-    hipStream_t st = current_stream();
-    const size_t logit_bytes = round_up(N * 2, 256);
-    const size_t part_bytes = (size_t)kArgMaxBlocks * 8;
-    void *Y = nullptr;
-    int rc = aux_scratch(logit_bytes + part_bytes + 256, &Y, fn);
-    if (rc != ECPU_OK) return rc;
-    float *P = nullptr;
-    int *T = nullptr;
-    // Ticket 4095 of the split-K set: the K-split GEMV takes ticket t for
-    // tile t of grids below 256 tiles, and every kernel leaves its tickets
-    // at zero, so calls ordered on one stream never share a live ticket.
-    rc = split_scratch(st, 0, 4096, &P, &T, fn);
-    if (rc != ECPU_OK) return rc;
-    uint16_t *logits = (uint16_t *)Y;
-    uint32_t *part = (uint32_t *)((char *)Y + logit_bytes);
-    uint32_t *result = (uint32_t *)((char *)Y + logit_bytes + part_bytes);
+namespace {
 
-    rc = run_linear(F_W8A16, 1, N, K, A, W, S, logits, fn);
+// The W8A16 GEMV into `logits`, then the argmax kernel with its parked pairs
+// in `part`, its ticket and its result word pair; host outputs wait for the
+// result.  clear_ticket: a one-thread kernel zeroes the ticket first.
+int linear_argmax_core(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *logits,
+                       uint32_t *part, uint32_t *result, int *ticket, bool clear_ticket, size_t *out_index,
+                       float *out_value, bool index_on_device, bool value_on_device, const char *fn) {
+    hipStream_t st = current_stream();
+    int rc = run_linear(F_W8A16, 1, N, K, A, W, S, logits, fn);
     if (rc != ECPU_OK) return rc;
     hipEvent_t ev0 = prof_begin(st);
+    if (clear_ticket) clear_int_kernel<<<1, 64, 0, st>>>(ticket);
     const uint32_t nblk = (uint32_t)std::min<size_t>(kArgMaxBlocks, (N + kArgStep - 1) / kArgStep);
     const uint32_t per_block = (uint32_t)round_up((N + nblk - 1) / nblk, 8);
-    argmax_bf16_kernel<<<nblk, kArgThreads, 0, st>>>(logits, (uint32_t)N, per_block, part, T + 4095, result,
+    argmax_bf16_kernel<<<nblk, kArgThreads, 0, st>>>(logits, (uint32_t)N, per_block, part, ticket, result,
                                                      index_on_device ? out_index : nullptr,
                                                      value_on_device ? out_value : nullptr);
     rc = check_launch(fn);
@@ -185,6 +180,77 @@ int run_linear_argmax_w8a16(size_t N, size_t K, const uint16_t *A, const uint8_t
     if (!index_on_device) *out_index = (size_t)host[1];
     if (!value_on_device) memcpy(out_value, &host[0], sizeof(float));
     return ECPU_OK;
+}
+
+// Scratch of the entry point that allocates nothing: the logits of up to
+// kStaticArgmaxMaxN rows, the parked pairs, the result and the ticket, in one
+// file-scope device array.  Each GPU holds its own copy (its address comes
+// from hipGetSymbolAddress with that device current) for the whole process;
+// calls that overlap in time on one GPU share it and race.
+constexpr size_t kStaticLogitBytes = round_up(kStaticArgmaxMaxN * 2, 256);
+constexpr size_t kStaticPartBytes = (size_t)kArgMaxBlocks * 8;
+constexpr size_t kStaticBytes = kStaticLogitBytes + kStaticPartBytes + 256 + 256;
+__device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+std::mutex g_static_mu;
+void *g_static_ptr[64];
+
+int static_scratch(void **p, const char *fn) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(ECPU_ERR_DEVICE, "%s: no current HIP device", fn);
+    if (dev < 0 || dev >= 64) return fail(ECPU_ERR_DEVICE, "%s: device %d beyond the 64 this library tracks", fn, dev);
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void *q = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !q) {
+            (void)hipGetLastError();
+            return fail(ECPU_ERR_DEVICE, "%s: hipGetSymbolAddress of the static scratch failed: %s", fn,
+                        hipGetErrorString(e));
+        }
+        g_static_ptr[dev] = q;
+    }
+    *p = g_static_ptr[dev];
+    return ECPU_OK;
+}
+
+}  // namespace
+
+int run_linear_argmax_w8a16(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S,
+                            size_t *out_index, float *out_value, bool index_on_device, bool value_on_device,
+                            const char *fn) {
+    hipStream_t st = current_stream();
+    const size_t logit_bytes = round_up(N * 2, 256);
+    const size_t part_bytes = (size_t)kArgMaxBlocks * 8;
+    void *Y = nullptr;
+    int rc = aux_scratch(logit_bytes + part_bytes + 256, &Y, fn);
+    if (rc != ECPU_OK) return rc;
+    float *P = nullptr;
+    int *T = nullptr;
+    // Ticket 4095 of the split-K set: the K-split GEMV takes ticket t for
+    // tile t of grids below 256 tiles, and every kernel leaves its tickets
+    // at zero, so calls ordered on one stream never share a live ticket.
+    rc = split_scratch(st, 0, 4096, &P, &T, fn);
+    if (rc != ECPU_OK) return rc;
+    return linear_argmax_core(N, K, A, W, S, (uint16_t *)Y, (uint32_t *)((char *)Y + logit_bytes),
+                              (uint32_t *)((char *)Y + logit_bytes + part_bytes), T + 4095, false, out_index,
+                              out_value, index_on_device, value_on_device, fn);
+}
+
+int run_linear_argmax_w8a16_static(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S,
+                                   size_t *out_index, float *out_value, bool index_on_device, bool value_on_device,
+                                   const char *fn) {
+    if (N > kStaticArgmaxMaxN)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: N = %zu exceeds the static scratch's %zu logits", fn, N,
+                    kStaticArgmaxMaxN);
+    void *base = nullptr;
+    const int rc = static_scratch(&base, fn);
+    if (rc != ECPU_OK) return rc;
+    char *b = (char *)base;
+    return linear_argmax_core(N, K, A, W, S, (uint16_t *)b, (uint32_t *)(b + kStaticLogitBytes),
+                              (uint32_t *)(b + kStaticLogitBytes + kStaticPartBytes),
+                              (int *)(b + kStaticLogitBytes + kStaticPartBytes + 256), true, out_index, out_value,
+                              index_on_device, value_on_device, fn);
 }
 
 int run_swiglu_w4(size_t H, size_t I, size_t K, const uint16_t *A, const uint8_t *Wgu, const float *Sgu,
