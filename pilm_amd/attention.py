@@ -32,11 +32,23 @@ def _check_dev(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be bfloat16")
 
 
-def _block_table(block_ids, device) -> torch.Tensor:
+def _block_table(block_ids, device, num_blocks: int, needed: int) -> torch.Tensor:
+    """int32 device table.  A host list is checked like the reference's
+    indexing (IndexError for ids outside [0, num_blocks), and for a table
+    shorter than the cache_len positions need); a device table is not read
+    back -- the kernels clamp its ids into [0, num_blocks), so an invalid id
+    reads and writes another block instead of faulting, and callers with
+    device tables own their validity."""
     if isinstance(block_ids, torch.Tensor):
         t = block_ids.to(device=device, dtype=torch.int32)
     else:
-        t = torch.tensor(list(block_ids), dtype=torch.int32).to(device)
+        ids = [int(b) for b in block_ids]
+        bad = [b for b in ids[:needed] if not 0 <= b < num_blocks]
+        if bad:
+            raise IndexError(f"block id {bad[0]} is out of bounds for a cache of {num_blocks} blocks")
+        if len(ids) < needed:
+            raise IndexError(f"{needed} blocks are needed for the positions, the table has {len(ids)}")
+        t = torch.tensor(ids, dtype=torch.int32).to(device)
     return t.contiguous()
 
 
@@ -76,8 +88,8 @@ def paged_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
             raise ValueError("caches must be contiguous")
         if cache_len is None:
             raise ValueError("cache_len is required with a cache")
-        table = _block_table(block_ids, q.device)
         num_blocks, block_size = k_cache.shape[0], k_cache.shape[1]
+        table = _block_table(block_ids, q.device, num_blocks, -(-int(cache_len) // block_size))
     else:
         cache_len = seq if cache_len is None else cache_len
         table = None
@@ -151,7 +163,8 @@ class PagedKVCache:
                v_new: torch.Tensor, gate: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The attention step of one sequence on this layer's blocks (the new
         rows are written at positions cache_len - S ..)."""
-        table = _block_table(block_ids, self.k_cache[layer_idx].device)
+        kc = self.k_cache[layer_idx]
+        table = _block_table(block_ids, kc.device, kc.shape[0], -(-int(cache_len) // kc.shape[1]))
         if not isinstance(block_ids, torch.Tensor):   # (a device table is not read back)
             needed = (int(cache_len) + self.block_size - 1) // self.block_size
             self.used.update(int(x) for x in list(block_ids)[:needed])

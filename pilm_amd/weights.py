@@ -123,6 +123,9 @@ def load_quantized_linear_cache(cache_file, out_features: int, in_features: int,
         t = torch.empty(shape, dtype=dtype, device=device)
         tensors[name] = t
         ranges.append((off, nbytes, t.data_ptr()))
+    # the upload runs on the library's own copy stream: order it after the
+    # work torch's stream has queued on memory these fresh tensors may reuse
+    torch.cuda.current_stream(device).synchronize()
     rc = abi.eram_load_file(str(cache_file), ranges)
     if rc != 0:
         raise RuntimeError(f"eram_hip_load_file failed: rc={rc} ({abi.last_error()})")
@@ -154,6 +157,9 @@ class QuantBundle:
                 total += -(-header[name][3] // _ALIGN) * _ALIGN
             plan.append((src, path, header))
         self.arena = torch.empty((max(total, 1),), dtype=torch.uint8, device=device)
+        # uploads run on the library's copy stream: order them after torch's
+        # queued work on memory the fresh arena may reuse
+        torch.cuda.current_stream(self.arena.device).synchronize()
         self.linears = {}
         off = 0
         t0 = time.perf_counter()

@@ -24,10 +24,23 @@ def test_wrong_dtype_rejected():
 
 
 def test_block_table_from_list_and_tensor():
-    t = A._block_table([3, 1, 2], "cpu")
+    t = A._block_table([3, 1, 2], "cpu", 4, 3)
     assert t.dtype == torch.int32 and t.tolist() == [3, 1, 2]
-    t2 = A._block_table(torch.tensor([5, 4], dtype=torch.int64), "cpu")
+    t2 = A._block_table(torch.tensor([5, 4], dtype=torch.int64), "cpu", 8, 2)
     assert t2.dtype == torch.int32 and t2.is_contiguous() and t2.tolist() == [5, 4]
+
+
+def test_block_table_rejects_invalid_ids():
+    """As the reference's cache indexing does (physical_kv.py, attention.py:
+    98-112): an id outside the cache raises IndexError, as does a table too
+    short for the positions; ids past the needed blocks are not looked at."""
+    with pytest.raises(IndexError, match="out of bounds"):
+        A._block_table([0, 4], "cpu", 4, 2)
+    with pytest.raises(IndexError, match="out of bounds"):
+        A._block_table([-1], "cpu", 4, 1)
+    with pytest.raises(IndexError, match="needed"):
+        A._block_table([0], "cpu", 4, 2)
+    assert A._block_table([0, 1, 99], "cpu", 4, 2).tolist() == [0, 1, 99]
 
 
 def test_cache_bookkeeping_without_gpu():
