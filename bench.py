@@ -495,38 +495,92 @@ def sweep_fused(torch, dev, reps: int = 20) -> dict:
     return out
 
 
-def cpu_baseline(budget_s: float = 12.0) -> dict | None:
-    """The reference's ekernel_linear_w4a16g128_bf16 (kernels.c compiled from
-    source into oracle/_ref, OpenMP over rows) on this host.  Sample: one
-    layer's seven linears plus lm_head at M = 1, repeated for ~budget_s."""
+def cpu_host() -> dict:
+    """CPU model, sockets, physical cores and logical CPUs among the CPUs this
+    process may run on (SMT siblings share a core id within a package)."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores, packages = set(), set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            pkg = open(base + "physical_package_id").read().strip()
+            core = open(base + "core_id").read().strip()
+        except OSError:
+            pkg, core = "0", str(c)
+        packages.add(pkg)
+        cores.add((pkg, core))
+    return {"model": _cpu_model(), "sockets": len(packages), "physical_cores": len(cores),
+            "logical_cpus": len(cpus)}
+
+
+def cpu_child(threads: int) -> dict:
+    """One thread count (OMP_NUM_THREADS / OMP_PROC_BIND / OMP_PLACES set by
+    the parent before this process loaded OpenMP): per shape of one decode
+    layer's W4A16-g128 linears plus lm_head (M = 1), 5 warm-up calls and the
+    median of >= 20 calls timed with the monotonic clock around the C call."""
     import numpy as np
     from oracle import oracle as O
     from pilm_amd import synth as S
     kind = "reference" if O.ref_available() else "port"
-    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    shapes = LAYER_SHAPES + [LM_HEAD]
-    data = []
-    for i, (name, n, k) in enumerate(shapes):
+    lib = O.ref_lib() if kind == "reference" else O.oracle_lib()
+    fn = lib.ekernel_linear_w4a16g128_bf16 if kind == "reference" else None
+    per_shape, tot_bytes, tot_sec = [], 0, 0.0
+    for i, (name, n, k) in enumerate(LAYER_SHAPES + [LM_HEAD]):
         x = S.activations_bf16(100 + i, 1, k)
-        rng = np.random.default_rng(i)
-        w = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
-        s = S.scales_uniform(200 + i, (n, k // 128))
-        data.append((x, w, s, n, k))
-    impl = "ref" if kind == "reference" else "oracle"
-    O.linear_w4a16g_bf16(data[0][0], data[0][1], data[0][2], 128, impl=impl)   # warm (OpenMP pool)
-    done_bytes, reps = 0, 0
+        w = np.random.default_rng(i).integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+        sc = S.scales_uniform(200 + i, (n, k // 128))
+        out = np.empty((1, n), np.uint16)
+        if fn is not None:
+            desc = O._Desc(1, n, k)
+            args = (ctypes.byref(desc), x.ctypes.data, w.ctypes.data, sc.ctypes.data, out.ctypes.data, 1)
+            call = lambda: fn(*args)       # noqa: E731
+        else:
+            call = lambda: O.linear_w4a16g_bf16(x, w, sc, 128, impl="oracle")   # noqa: E731
+        for _ in range(5):
+            call()
+        times = []
+        for _ in range(20):
+            t0 = time.clock_gettime(time.CLOCK_MONOTONIC)
+            call()
+            times.append(time.clock_gettime(time.CLOCK_MONOTONIC) - t0)
+        med = float(np.median(times))
+        b = alg_bytes(1, n, k)
+        per_shape.append({"shape": f"{name} {n}x{k}", "median_ms": round(med * 1e3, 4), "GBps": round(b / med / 1e9, 2)})
+        tot_bytes += b
+        tot_sec += med
+    return {"threads": threads, "kind": kind, "GBps": round(tot_bytes / tot_sec / 1e9, 2), "shapes": per_shape}
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict | None:
+    """The reference's ekernel_linear_w4a16g128_bf16 (kernels.c compiled from
+    its source into oracle/_ref by oracle/Makefile, x86-64-v3 + OpenMP) on this
+    host, swept over 1, half and all of the physical cores this process may
+    use, each in a child process with OMP_PROC_BIND=close and
+    OMP_PLACES=cores.  value: the rate at all physical cores, GB/s of the
+    per-shape medians summed over one layer's linears plus lm_head."""
+    import subprocess
+    host = cpu_host()
+    phys = max(1, min(host["physical_cores"], int(os.environ.get("OMP_NUM_THREADS") or host["physical_cores"])))
+    sweep = sorted({1, max(1, phys // 2), phys})
+    runs = []
     t0 = time.perf_counter()
-    while True:
-        for (x, w, s, n, k) in data:
-            O.linear_w4a16g_bf16(x, w, s, 128, impl=impl)
-            done_bytes += alg_bytes(1, n, k)
-        reps += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    sec = time.perf_counter() - t0
-    return {"value": round(done_bytes / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{reps} passes over one layer's 7 W4A16-g128 linears + lm_head (M=1) in {sec:.1f} s",
-            "cpu": _cpu_model()}
+    for t in sweep:
+        env = dict(os.environ, OMP_NUM_THREADS=str(t), OMP_PROC_BIND="close", OMP_PLACES="cores")
+        r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-child", str(t)], env=env,
+                           capture_output=True, text=True, timeout=max(60.0, 10 * budget_s))
+        if r.returncode != 0:
+            print(r.stderr[-2000:], file=sys.stderr)
+            return None
+        runs.append(json.loads(r.stdout.strip().splitlines()[-1]))
+    top = runs[-1]
+    return {"value": top["GBps"], "unit": "GB/s", "cores": top["threads"], "kind": top["kind"],
+            "sample": (f"median of 20 calls (after 5 warm-ups) per shape of one Qwen3-1.7B layer's W4A16-g128 "
+                       f"linears + lm_head, M=1; threads swept {sweep} in {time.perf_counter() - t0:.1f} s"),
+            "cpu": host["model"], "sockets": host["sockets"], "physical_cores": host["physical_cores"],
+            "logical_cpus": host["logical_cpus"], "omp": "OMP_PROC_BIND=close OMP_PLACES=cores",
+            "build": "kernels.c, gcc -O3 -march=x86-64-v3 -fopenmp (the reference's sources are not on this "
+                     "host, so no -march=native build here)",
+            "sweep": [{"threads": r["threads"], "GBps": r["GBps"]} for r in runs], "per_shape": top["shapes"]}
 
 
 def pmc_pass(torch, dev, steps: int) -> None:
@@ -708,9 +762,13 @@ def main(argv=None) -> int:
     ap.add_argument("--layout", choices=("fused", "separate"), default="fused",
                     help="q/k/v and gate/up as one matrix each (the decoder's layout) or one call per projection")
     ap.add_argument("--no-decode", action="store_true", help="skip the whole-decoder tok/s measurement")
+    ap.add_argument("--cpu-child", type=int, metavar="THREADS", help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
     global LAYER_SHAPES
     LAYER_SHAPES = LAYER_SHAPES_FUSED if args.layout == "fused" else LAYER_SHAPES_SEPARATE
+    if args.cpu_child:
+        print(json.dumps(cpu_child(args.cpu_child)))
+        return 0
     if args.traffic:
         rec = traffic_summary(*args.traffic)
         TRAFFIC_FILE.parent.mkdir(exist_ok=True)

@@ -239,3 +239,87 @@ def test_matrix_core_threshold_setter(fmt, dev):
         abi.set_matrix_core_min_rows(-1)
     assert abi.matrix_core_min_rows() == 64
     check_close(fmt, run_gpu(fmt, x, w, s, dev), ref, f"{fmt} default threshold")
+
+
+# ------------------------------------------------- configuration 3 at full size
+
+CONFIG3_SHAPES = [(8192, 4096), (24576, 4096), (4096, 12288), (151936, 4096)]   # Qwen3-8B q / gate_up / down / lm_head
+CONFIG3_M = [64, 256, 1024, 2048]
+_C3_CACHE: dict = {}
+
+
+def _c3_weights(fmt, n, k, dev):
+    """Seeded device weights of the configuration's distributions (int8
+    uniform in [-127, 127] or packed int4 bytes uniform; scales ~U(0.001,
+    0.02), group scales rounded through fp16), kept across the M values."""
+    key = (fmt, n, k)
+    if key not in _C3_CACHE:
+        _C3_CACHE.clear()
+        torch.cuda.empty_cache()
+        g = torch.Generator(device=dev)
+        g.manual_seed(n * 7 + k)
+        if fmt == "w8a32":
+            w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+            s = torch.rand((n,), device=dev, generator=g) * 0.019 + 0.001
+        else:
+            w = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=g)
+            s = (torch.rand((n, k // 128), device=dev, generator=g) * 0.019 + 0.001).half().float()
+        _C3_CACHE[key] = (w, s)
+    return _C3_CACHE[key]
+
+
+def _c3_run(fmt, x, w, s, k):
+    from pilm_amd import ckernel as ck
+    if fmt == "w8a32":
+        return ck.linear_w8a32(x, w, s)
+    return ck.linear_w4a16g128_bf16(x, w, s, k)
+
+
+@pytest.mark.parametrize("m", CONFIG3_M)
+@pytest.mark.parametrize("n,k", CONFIG3_SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("fmt", ["w8a32", "w4g128"])
+def test_config3_full_shapes(fmt, n, k, m, dev):
+    """The prefill / verify GEMM at the Qwen3-8B shapes and M of the
+    configuration: 128 sampled weight rows (every activation row) against the
+    oracle on the sliced weights, within the matrix-core tolerance; over the
+    whole output, doubling every scale doubles every output exactly (a power
+    of two passes through the fp16 operands and the epilogue unchanged)."""
+    w, s = _c3_weights(fmt, n, k, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(m)
+    x = torch.randn((m, k), device=dev, generator=g)
+    if fmt != "w8a32":
+        x = x.to(torch.bfloat16)
+    _say(f"[gpu] config3 {fmt} M={m} N={n} K={k}")
+    y = _c3_run(fmt, x, w, s, k)
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(n + m))[:128].sort().values
+    xs = x.cpu().numpy() if fmt == "w8a32" else x.view(torch.int16).cpu().numpy().view(np.uint16)
+    ws, ss = w[rows.to(dev)].cpu().numpy(), s[rows.to(dev)].cpu().numpy()
+    gen = GV._gen()
+    ref = gen.run(fmt, xs, ws, ss, "oracle")
+    yr = y[:, rows.to(dev)]
+    got = yr.cpu().numpy() if fmt == "w8a32" else yr.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    check_close(fmt, got, ref, f"{fmt} {m}x{n}x{k} sampled rows")
+    y2 = _c3_run(fmt, x, w, s * 2, k)
+    if fmt == "w8a32":
+        assert torch.equal(y2, y * 2)
+    else:
+        assert torch.equal(y2.float(), y.float() * 2)
+    del y, y2
+
+
+@pytest.mark.parametrize("fmt", ["w8a32", "w4g128"])
+def test_config3_zero_rows(fmt, dev):
+    """Zero weight rows give exactly zero outputs in a full-size call."""
+    n, k, m = 24576, 4096, 256
+    w, s = _c3_weights(fmt, n, k, dev)
+    w = w.clone()
+    zero = torch.arange(0, n, 997, device=dev)
+    w[zero] = 0 if fmt == "w8a32" else 0x00
+    x = torch.randn((m, k), device=dev)
+    if fmt != "w8a32":
+        x = x.to(torch.bfloat16)
+    _say(f"[gpu] config3 zero rows {fmt}")
+    y = _c3_run(fmt, x, w, s, k).float()
+    assert torch.all(y[:, zero] == 0)
+    assert torch.count_nonzero(y) > 0.99 * (y.numel() - m * zero.numel())
