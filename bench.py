@@ -38,7 +38,7 @@ Printed JSON line:
                on a bounded sample of the same workload on this host
   sweep        per-shape times with --sweep [sections]: g128 (default),
                w4row, w8a32, w8a16, gemm, fused, attention, load (bundle ->
-               HBM), or all
+               HBM), verify (16-sequence MTP verify, M = 80), or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -340,7 +340,10 @@ def sweep(torch, dev, sections) -> dict:
       fused  W4 SwiGLU MLP and W8A16 lm_head argmax vs their unfused calls
       attention  paged attention of one sequence (decode and MTP verify) at
              the 1.7B and 8B head layouts, 384 .. 131072 positions (K+V GB/s)
-      load   a 1.7B W4 bundle uploaded to HBM (GB/s)."""
+      load   a 1.7B W4 bundle uploaded to HBM (GB/s)
+      verify MTP verify of 16 sequences x (1 + 4 drafts) at the 8B shapes,
+             W8A16 and W4A16 g128: one M = 80 call on the exact kernels,
+             the same on the matrix cores, and 16 per-sequence M = 5 calls."""
     res = {}
     if "g128" in sections:
         res["g128_1p7b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4g128", n, k, (1, 4, 16))}
@@ -365,6 +368,32 @@ def sweep(torch, dev, sections) -> dict:
         res["attention"] = sweep_attention(torch, dev)
     if "load" in sections:
         res["load"] = sweep_load(torch, dev)
+    if "verify" in sections:
+        res["verify_8b"] = sweep_verify(torch, dev)
+    return res
+
+
+def sweep_verify(torch, dev, n_seq: int = 16, drafts: int = 4) -> dict:
+    """Batched MTP verify: M = n_seq * (1 + drafts) rows per linear."""
+    from pilm_amd import bindings as abi
+    m1 = 1 + drafts
+    m = n_seq * m1
+    res = {}
+    for fmt in ("w8a16", "w4g128"):
+        for name, n, k in SHAPES_8B:
+            prev = abi.matrix_core_min_rows()
+            abi.set_matrix_core_min_rows(0)
+            try:
+                exact = time_linear(torch, dev, fmt, n, k, (m1, m), reps=5, min_bytes=256 << 20)
+            finally:
+                abi.set_matrix_core_min_rows(prev)
+            mc = time_linear(torch, dev, fmt, n, k, (m,), reps=5, min_bytes=256 << 20)
+            res[f"{fmt}_{name}"] = {"N": n, "K": k,
+                                    f"exact_M{m}_us": exact[f"M{m}"]["us"],
+                                    f"matrix_M{m}_us": mc[f"M{m}"]["us"],
+                                    f"per_seq_{n_seq}xM{m1}_us": round(n_seq * exact[f"M{m1}"]["us"], 2),
+                                    f"exact_M{m}_GBps": exact[f"M{m}"]["GBps"]}
+            print(f"[bench] verify {fmt} {name}: {res[f'{fmt}_{name}']}", file=sys.stderr, flush=True)
     return res
 
 
@@ -859,7 +888,8 @@ def main(argv=None) -> int:
         out["decode"] = dec
         calls = xs = run = None
     if args.sweep:
-        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "attention", "load") if args.sweep == "all" \
+        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "attention", "load", "verify") \
+            if args.sweep == "all" \
             else tuple(args.sweep.split(","))
         print(f"[bench] sweeps: {', '.join(sections)}", flush=True)
         del calls, xs, run

@@ -390,6 +390,20 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
                                  const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *block_ids,
                                  const uint16_t *gate, const int32_t *step, uint16_t *out);
 
+/* One decode row (S = 1) of FullAttention.forward (attention.py:82-139) in
+ * one launch: ekernel_qk_norm_rope_bf16 followed by
+ * ekernel_attention_exact_bf16 with the gate inside qg (gate_row_stride
+ * n_heads*2*head_dim, gate_head_stride 2*head_dim), bit-identical to them,
+ * the roped q kept on chip.  desc as for ekernel_qk_norm_rope_bf16 with
+ * S = 1; the cache holds pos0 + 1 positions after the call (step: step[0]
+ * the position, step[1] the cached length, as the two calls read them).
+ * head_dim 64 or 128, 1, 2 or 4 q heads per kv head, the visible value
+ * rows staged in LDS in passes.  out [n_heads * head_dim] bf16. */
+int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint16_t *qg, const uint16_t *k,
+                                  const uint16_t *v, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                                  const float *cos_table, const float *sin_table, const int32_t *step,
+                                  uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids, uint16_t *out);
+
 /* out[m, i] = bf16(bf16(silu(gate[m*in_stride + i])) * up[m*in_stride + i])
  * (F.silu(gate(x)) * up(x), layers.py:188-193), m < rows, i < n. */
 int ekernel_silu_mul_bf16(const uint16_t *gate, const uint16_t *up, size_t rows, size_t n, size_t in_stride,

@@ -221,8 +221,10 @@ class OracleDecoder:
         q, s = qs
         return O.linear_w4a16g_bf16(x, q, s, self.cfg["group_size"])
 
-    def forward(self, ids, pos0):
-        """bf16 logits of the last of the S tokens at positions pos0.. ."""
+    def forward(self, ids, pos0, all_rows=False):
+        """bf16 logits of the last of the S tokens at positions pos0.., or of
+        every row (all_rows: the speculative verify of src/engine.py:462-476,
+        lm_head over the whole normed output)."""
         c = self.cfg
         D, Hq, Hkv, I, eps = c["head_dim"], c["heads"], c["kv_heads"], c["intermediate"], c["eps"]
         S = len(ids)
@@ -251,6 +253,9 @@ class OracleDecoder:
             u = self._lin(h, Lw["up"])
             act = silu_mul_bf16(g, u, S, I, I)
             x = self._lin(act, Lw["down"])
+        if all_rows:
+            hN, _ = rmsnorm_gemma_bf16(x, res, self.norm, eps)
+            return self._lin(hN, self.lm_head)
         hN, _ = rmsnorm_gemma_bf16(x[-1:], res[-1:], self.norm, eps)
         return self._lin(hN, self.lm_head)[0]
 

@@ -46,6 +46,7 @@ _OPTIONAL_KERNEL_SYMBOLS = [
     "ekernel_rmsnorm_gemma_bf16",
     "ekernel_qk_norm_rope_bf16",
     "ekernel_attention_exact_bf16",
+    "ekernel_decode_attention_bf16",
     "ekernel_silu_mul_bf16",
     "ekernel_greedy_step_bf16",
 ]
@@ -253,6 +254,8 @@ def _configure(lib):
         lib.ekernel_attention_exact_bf16.argtypes = [ctypes.POINTER(EkernelAttentionExactDesc)] + \
             [ctypes.c_void_p] * 7
         lib.ekernel_attention_exact_bf16.restype = ctypes.c_int
+        lib.ekernel_decode_attention_bf16.argtypes = [ctypes.POINTER(EkernelQkRopeDesc)] + [ctypes.c_void_p] * 12
+        lib.ekernel_decode_attention_bf16.restype = ctypes.c_int
         lib.ekernel_silu_mul_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
                                               ctypes.c_size_t, ctypes.c_void_p]
         lib.ekernel_silu_mul_bf16.restype = ctypes.c_int

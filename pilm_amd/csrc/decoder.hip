@@ -161,6 +161,79 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[row + i] = gemma_out(xs[i], r, w[i]);
 }
 
+// The same with every load of the row issued at once: thread t owns the
+// eight-element chunks t, t + 256, ... (CPT of them; 16-byte loads of x, the
+// residual and the weight), so the row costs one memory round trip.  Needs
+// n % 8 == 0 and 16-byte aligned rows.  residual and residual_out may be the
+// same buffer (each chunk is read before it is written).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+template <int CPT>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t *__restrict__ x, const uint16_t *res,
+                                                          const uint16_t *__restrict__ w, uint16_t *__restrict__ out,
+                                                          uint16_t *res_out, int n, float eps) {
+    extern __shared__ float lds[];
+    float *xs = lds, *rsh = lds + n;
+    const size_t row = (size_t)blockIdx.x * n;
+    const int nc = n / 8, t = threadIdx.x;
+    u32x4 xv[CPT], rv[CPT], wv[CPT];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = t + 256 * u;
+        if (c < nc) {
+            xv[u] = ((const u32x4 *)(x + row))[c];
+            if (res) rv[u] = ((const u32x4 *)(res + row))[c];
+            wv[u] = ((const u32x4 *)w)[c];
+        }
+    }
+    float h[CPT][8];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = t + 256 * u;
+        if (c < nc) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float a = bf16_lo(xv[u][e]), b = bf16_hi(xv[u][e]);
+                if (res) {
+                    a = bfr(a + bf16_lo(rv[u][e]));
+                    b = bfr(b + bf16_hi(rv[u][e]));
+                }
+                h[u][2 * e] = a;
+                h[u][2 * e + 1] = b;
+            }
+            if (res && res_out) {
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = pack_bf16(h[u][2 * e], h[u][2 * e + 1]);
+                ((u32x4 *)(res_out + row))[c] = o;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xs[8 * c + e] = h[u][e];
+        }
+    }
+    __syncthreads();
+    if (t < 64) {
+        const float r = wave_row_rsqrt(xs, n, eps);
+        if (t == 0) *rsh = r;
+    }
+    __syncthreads();
+    const float r = *rsh;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = t + 256 * u;
+        if (c < nc) {
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = (uint32_t)gemma_out(h[u][2 * e], r, (uint16_t)(wv[u][e] & 0xFFFFu)) |
+                       ((uint32_t)gemma_out(h[u][2 * e + 1], r, (uint16_t)(wv[u][e] >> 16)) << 16);
+            ((u32x4 *)(out + row))[c] = o;
+        }
+    }
+}
+
 // ---- q/k GemmaRMSNorm + rope + cache write ---------------------------------
 // One wave per (s, head): head < H normalizes q (the first D of the head's 2D
 // q_proj outputs) into q_out[s, head, :]; head >= H normalizes k of kv head
@@ -176,40 +249,74 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(
     const int32_t *__restrict__ block_ids, int n_block_ids, int block_size, int num_blocks, int H, int Hkv, int D,
     int rot, float eps) {
     __shared__ float xs[256];
+    constexpr int kPer = 4;                  // elements per lane (D <= 256)
     const int s = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
     const bool is_q = head < H;
     const int hk = is_q ? head : head - H;
     const uint16_t *src = is_q ? qg + (size_t)s * q_stride + (size_t)hk * 2 * D : kin + (size_t)s * kv_stride + (size_t)hk * D;
-    for (int i = t; i < D; i += 64) xs[i] = bf(src[i]);
-    __syncthreads();
-    const float r = wave_row_rsqrt(xs, D, eps);
     const uint16_t *nw = is_q ? qw : kw;
-    __syncthreads();
-    for (int i = t; i < D; i += 64) xs[i] = bf(gemma_out(xs[i], r, nw[i]));
-    __syncthreads();
+    const uint16_t *vsrc = vin + (size_t)s * kv_stride + (size_t)hk * D;
+    // every load issued before the arithmetic: the head's values, the norm
+    // weight, v; then (once the position is known) the rope table entries and
+    // the cache block
     const int pos = (step ? step[0] : pos0_host) + s;
+    float xr[kPer];
+    uint16_t wr[kPer], vr[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = t + 64 * u;
+        if (i < D) {
+            xr[u] = bf(src[i]);
+            wr[u] = nw[i];
+            if (!is_q) vr[u] = vsrc[i];
+        }
+    }
     const int pc = min(max(pos, 0), max_pos - 1);
     const int nf = rot / 2;
+    float cr[kPer], sr[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = t + 64 * u;
+        if (i < rot) {
+            const int f = i < nf ? i : i - nf;
+            cr[u] = cos_t[(size_t)pc * nf + f];
+            sr[u] = sin_t[(size_t)pc * nf + f];
+        }
+    }
+    int blk = 0;
+    if (!is_q) blk = min(max(block_ids[min(max(pos / block_size, 0), n_block_ids - 1)], 0), num_blocks - 1);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+        if (t + 64 * u < D) xs[t + 64 * u] = xr[u];
+    __syncthreads();
+    const float r = wave_row_rsqrt(xs, D, eps);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+        if (t + 64 * u < D) xs[t + 64 * u] = bf(gemma_out(xr[u], r, wr[u]));
+    __syncthreads();
     uint16_t *dst;
     if (is_q) {
         dst = q_out + ((size_t)s * H + hk) * D;
     } else {
-        const int bi = min(max(pos / block_size, 0), n_block_ids - 1);
-        const int blk = min(max(block_ids[bi], 0), num_blocks - 1);
         const size_t row = (((size_t)blk * block_size + pos % block_size) * Hkv + hk) * D;
         dst = k_cache + row;
-        const uint16_t *vs = vin + (size_t)s * kv_stride + (size_t)hk * D;
-        for (int i = t; i < D; i += 64) v_cache[row + i] = vs[i];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+            if (t + 64 * u < D) v_cache[row + t + 64 * u] = vr[u];
     }
-    for (int i = t; i < D; i += 64) {
-        float o = xs[i];
-        if (i < rot) {
-            const int f = i < nf ? i : i - nf;
-            const float c = cos_t[(size_t)pc * nf + f], sn = sin_t[(size_t)pc * nf + f];
-            const float a = xs[f], b = xs[f + nf];
-            o = i < nf ? (a * c) - (b * sn) : (a * sn) + (b * c);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = t + 64 * u;
+        if (i < D) {
+            float o = xs[i];
+            if (i < rot) {
+                const int f = i < nf ? i : i - nf;
+                const float a = xs[f], b = xs[f + nf];
+                o = i < nf ? (a * cr[u]) - (b * sr[u]) : (a * sr[u]) + (b * cr[u]);
+            }
+            dst[i] = f32_to_bf16(o);
         }
-        dst[i] = f32_to_bf16(o);
     }
 }
 
@@ -289,6 +396,20 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
         const int r = i / D, d = i % D;
         qs[i] = bf(q[((size_t)s * H + kh * rep + r) * D + d]);
     }
+    // the gate values of this thread's outputs (P.V pass it, chain 0), fetched
+    // with q rather than after the sums; passes beyond kGatePre load theirs late
+    constexpr int kGatePre = 4;
+    const int nthr = rep * kDS * 4;
+    float gpre[kGatePre];
+#pragma unroll
+    for (int it = 0; it < kGatePre; ++it) {
+        const int i = it * (int)blockDim.x + t;
+        gpre[it] = 0.0f;
+        if (gate && i < nthr && (i & 3) == 0) {
+            const int h = kh * rep + i / (kDS * 4), dd = d0 + (i / 4) % kDS;
+            gpre[it] = bf(gate[(size_t)s * gate_row_stride + (size_t)h * gate_head_stride + dd]);
+        }
+    }
     __syncthreads();
 
     auto row_of = [&](int j) -> size_t {
@@ -365,7 +486,6 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
 
     // P.V: thread (r, column c, chain k) over the staged value rows
     const int main_len = naive ? 0 : (cache_len / 4) * 4;
-    const int nthr = rep * kDS * 4;
     for (int base = 0; base < nthr; base += blockDim.x) {
         const int i = base + t;
         const bool active = i < nthr;
@@ -413,11 +533,310 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
             o = bfr(o);
             const int h = kh * rep + r, d = d0 + c;
             if (gate) {
-                const float g = bf(gate[(size_t)s * gate_row_stride + (size_t)h * gate_head_stride + d]);
+                const int it = base / (int)blockDim.x;
+                const float g = it == 0 ? gpre[0] : it == 1 ? gpre[1] : it == 2 ? gpre[2] : it == 3 ? gpre[3]
+                              : bf(gate[(size_t)s * gate_row_stride + (size_t)h * gate_head_stride + d]);
                 o = o * bfr(__fdiv_rn(1.0f, 1.0f + sleef_expf(-g)));
             }
             out[((size_t)s * H + h) * D + d] = f32_to_bf16(o);
         }
+    }
+}
+
+// ---- one decode row: q/k norm + rope + cache write + attention ---------------
+// The steps of qk_rope_kernel and attn_exact_kernel for S = 1 in one launch,
+// one 512-thread workgroup per kv head: waves 0 .. rep-1 normalize and rotate
+// the rep q heads that read this kv head, wave rep the k head (and write the
+// k and v rows into the cache).  The scores are computed once per kv head, one
+// position per thread, the new position from the k row just made.  The value
+// rows are staged whole in LDS (the new one from registers), and thread
+// (chain k, column c), c fastest, sums P.V for every head of the kv head, so
+// a wave reads one value row contiguously and each weight by broadcast.
+// Every sum keeps the order of the two-kernel path above.
+constexpr int kDecodeThreads = 512;
+
+template <int D, int REP>
+__global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
+    const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
+    const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, int max_pos, const int32_t *__restrict__ step, int pos0_host,
+    uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache, const int32_t *__restrict__ block_ids,
+    int n_block_ids, int block_size, int num_blocks, int H, int Hkv, int rot, float eps, int max_len, int vcap,
+    float scale, uint16_t *__restrict__ out) {
+    constexpr int kPer = D / 64;          // elements per lane of one head
+    constexpr int nthreads = kDecodeThreads;
+    constexpr int rep = REP;              // q heads per kv head (H / Hkv)
+    extern __shared__ float lds[];
+    const int kh = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int scs = (max_len + 3) & ~3;
+    float *xn = lds;                                           // [rep + 1][D] normalized heads
+    float *qs = xn + (rep + 1) * D;                            // [rep][D] roped q
+    float *sc = qs + rep * D;                                  // [rep][scs]
+    float *part = sc + (size_t)rep * scs;                      // [rep][4][D] chain sums
+    int *bids = (int *)(part + rep * 4 * D);                   // [n_block_ids]
+    uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [vcap][D]
+
+    const int pos = step ? step[0] : pos0_host;
+    int cache_len = step ? step[1] : pos0_host + 1;
+    cache_len = min(max(cache_len, 1), max_len);
+    const int vis = cache_len;
+    const bool naive = (long long)cache_len * D < 400;
+    const bool pos_ok = pos >= 0 && pos < max_len;
+    for (int i = t; i < n_block_ids; i += nthreads) bids[i] = min(max(block_ids[i], 0), num_blocks - 1);
+
+    // the head this wave normalizes: q head kh * rep + wave, or the k head
+    const bool head_wave = wave <= rep;
+    const bool is_k = wave == rep;
+    float xr[kPer];
+    uint16_t wr[kPer], vr[kPer], kb[kPer];
+    if (head_wave) {
+        const uint16_t *src = is_k ? kin + (size_t)kh * D : qg + (size_t)(kh * rep + wave) * 2 * D;
+        const uint16_t *nw = is_k ? kw : qw;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            xr[u] = bf(src[lane + 64 * u]);
+            wr[u] = nw[lane + 64 * u];
+            if (is_k) vr[u] = vin[(size_t)kh * D + lane + 64 * u];
+        }
+    }
+    const int pc = min(max(pos, 0), max_pos - 1);
+    const int nf = rot / 2;
+    float cr[kPer], sr[kPer];
+    if (head_wave) {
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = lane + 64 * u;
+            if (i < rot) {
+                const int f = i < nf ? i : i - nf;
+                cr[u] = cos_t[(size_t)pc * nf + f];
+                sr[u] = sin_t[(size_t)pc * nf + f];
+            }
+        }
+    }
+    // the gate values of the outputs this thread folds: (head r, column c) for
+    // r * D + c = t + nthreads * it
+    constexpr int kGatePre = 2;
+    float gpre[kGatePre];
+#pragma unroll
+    for (int it = 0; it < kGatePre; ++it) {
+        const int o = t + nthreads * it;
+        gpre[it] = o < rep * D ? bf(qg[(size_t)(kh * rep + o / D) * 2 * D + D + o % D]) : 0.0f;
+    }
+    if (head_wave) {
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) xn[wave * D + lane + 64 * u] = xr[u];
+    }
+    __syncthreads();                      // block ids and the raw heads are in
+
+    auto row_of = [&](int j) -> size_t {
+        const int blk = bids[min(j / block_size, n_block_ids - 1)];
+        return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
+    };
+    // rows [j0, j0 + vcap) of a cache into the staging region: 16 bytes per
+    // lane, D / 8 lanes per row, one DMA instruction per 64 pieces; rows past
+    // the visible ones repeat the last visible row.  Key rows are stored with
+    // their 16-byte chunks XOR-swizzled by the row index (chunk u of row j at
+    // slot u ^ (j mod D/8)), so that one thread per row reads them from LDS
+    // without bank conflicts; value rows are stored plainly.
+    constexpr int per_row = D / 8;
+    auto stage = [&](const uint16_t *cache, int j0, bool swizzle) {
+        const int nrows = min(vcap, vis - j0);
+        const int pieces = ((nrows * per_row + nthreads - 1) / nthreads) * nthreads;
+        for (int base = 0; base < pieces; base += nthreads) {
+            const int idx = base + t;
+            const int jr = min(idx / per_row, nrows - 1);
+            const int slot = idx % per_row;
+            const int u = swizzle ? (slot ^ (jr & (per_row - 1))) : slot;
+            const uint16_t *src = cache + row_of(j0 + jr) + 8 * u;
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(vs + (size_t)(base + wave * 64) * 8), 16,
+                                             0, 0);
+        }
+    };
+    stage(k_cache, 0, true);
+
+    if (head_wave) {
+        const float r = wave_row_rsqrt(xn + wave * D, D, eps);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) xn[wave * D + lane + 64 * u] = bf(gemma_out(xr[u], r, wr[u]));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float *x = xn + wave * D;
+        float *dst = qs + wave * D;       // roped q
+        const size_t crow = (is_k && pos_ok) ? row_of(pos) : 0;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = lane + 64 * u;
+            float o = x[i];
+            if (i < rot) {
+                const int f = i < nf ? i : i - nf;
+                const float a = x[f], b = x[f + nf];
+                o = i < nf ? (a * cr[u]) - (b * sr[u]) : (a * sr[u]) + (b * cr[u]);
+            }
+            const uint16_t ob = f32_to_bf16(o);
+            if (!is_k) dst[i] = bf(ob);
+            kb[u] = ob;
+            if (is_k && pos_ok) {
+                k_cache[crow + i] = ob;
+                v_cache[crow + i] = vr[u];
+            }
+        }
+    }
+
+    // scores from the staged key rows, one position per thread; the new
+    // position's row is written into the staging from registers (the copy the
+    // DMA brought may predate the cache write)
+    for (int j0 = 0; j0 < vis; j0 += vcap) {
+        if (j0 > 0) {
+            __syncthreads();              // the previous rows have been read
+            stage(k_cache, j0, true);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();                  // the key rows (and the roped q and k) are in
+        const int j1 = min(vis, j0 + vcap);
+        if (is_k && pos >= j0 && pos < j1) {
+            const int jr = pos - j0;
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int i = lane + 64 * u;
+                vs[(size_t)jr * D + 8 * ((i / 8) ^ (jr & (per_row - 1))) + i % 8] = kb[u];
+            }
+        }
+        __syncthreads();
+        for (int j = j0 + t; j < j1; j += nthreads) {
+            uint32_t ka[D / 2];
+            const int jr = j - j0;
+            const uint16_t *row = vs + (size_t)jr * D;
+#pragma unroll
+            for (int u = 0; u < per_row; ++u) {
+                const u32x4 c = *(const u32x4 *)(row + 8 * (u ^ (jr & (per_row - 1))));
+                ka[4 * u] = c[0];
+                ka[4 * u + 1] = c[1];
+                ka[4 * u + 2] = c[2];
+                ka[4 * u + 3] = c[3];
+            }
+#pragma unroll
+            for (int r = 0; r < rep; ++r)
+                sc[(size_t)r * scs + j] = bfr(bfr(score_dot<D>(qs + r * D, ka, naive)) * scale);
+        }
+    }
+    __syncthreads();                      // every score is in; the staged key rows are free
+    stage(v_cache, 0, false);             // value rows arrive during the softmax
+
+    // softmax per head: wave r
+    for (int r = wave; r < rep; r += nthreads / 64) {
+        float *x = sc + (size_t)r * scs;
+        float mx = -__builtin_inff();
+        for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float sum = 0.0f;
+        if (cache_len >= 8) {
+            float a = 0.0f;
+            if (lane < 8) {
+                a = lane < vis ? x[lane] : 0.0f;
+                int j = lane + 8;
+                for (; j + 56 < vis; j += 64) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = x[j + 8 * u];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) a = a + v[u];
+                }
+                for (; j < vis; j += 8) a = a + x[j];
+            }
+            const float b = a + __shfl_xor(a, 4);
+            const float c = b + __shfl_xor(b, 2);
+            sum = __shfl(c + __shfl_xor(c, 1), 0);
+        } else {
+            for (int j = 0; j < vis; ++j) sum = sum + x[j];
+        }
+        const float inv = __fdiv_rn(1.0f, sum);
+        for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
+    }
+
+    // P.V: thread (chain k, column c), every head of this kv head at once;
+    // eight positions of a chain (their value and rep weights) loaded ahead
+    const int main_len = naive ? 0 : (cache_len / 4) * 4;
+    constexpr int nthr = 4 * D;
+    for (int base = 0; base < nthr; base += nthreads) {
+        const int i = base + t;
+        const bool active = i < nthr;
+        const int k = (i / D) & 3, c = i % D;
+        float acc[rep];
+#pragma unroll
+        for (int r = 0; r < rep; ++r) acc[r] = 0.0f;
+        for (int j0 = 0; j0 < vis; j0 += vcap) {
+            if (j0 > 0) {
+                __syncthreads();          // the previous rows have been read
+                stage(v_cache, j0, false);
+            }
+            if (j0 > 0 || base == 0 || vis > vcap) {
+                wait_vmcnt<0>();
+                __syncthreads();          // every wave's copies (and the weights) are in
+                if (is_k && pos >= j0 && pos < min(vis, j0 + vcap)) {
+#pragma unroll
+                    for (int u = 0; u < kPer; ++u) vs[(size_t)(pos - j0) * D + lane + 64 * u] = vr[u];
+                }
+                __syncthreads();          // the new value row replaces the staged copy
+            }
+            const int j1 = min(vis, j0 + vcap);
+            if (active) {
+                const uint16_t *vc = vs + c - (size_t)j0 * D;     // vc[j * D]: column c of position j
+                auto fma_row = [&](int j) {
+                    const float vv = bf(vc[(size_t)j * D]);
+#pragma unroll
+                    for (int r = 0; r < rep; ++r) acc[r] = __builtin_fmaf(sc[(size_t)r * scs + j], vv, acc[r]);
+                };
+                if (naive) {
+                    if (k == 0)
+                        for (int j = j0; j < j1; ++j) fma_row(j);
+                } else {
+                    int j = j0 + ((k - j0) & 3);
+                    const int jm = min(j1, main_len);
+                    for (; j + 28 < jm; j += 32) {
+                        float vv[8], wv[8][rep];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            vv[u] = bf(vc[(size_t)(j + 4 * u) * D]);
+#pragma unroll
+                            for (int r = 0; r < rep; ++r) wv[u][r] = sc[(size_t)r * scs + j + 4 * u];
+                        }
+#pragma unroll
+                        for (int u = 0; u < 8; ++u)
+#pragma unroll
+                            for (int r = 0; r < rep; ++r) acc[r] = __builtin_fmaf(wv[u][r], vv[u], acc[r]);
+                    }
+                    for (; j < jm; j += 4) fma_row(j);
+                    if (k == 0)
+                        for (j = max(j0, main_len); j < j1; ++j) fma_row(j);
+                }
+            }
+            if (vis > vcap && j0 + vcap >= vis && base + nthreads < nthr) {
+                __syncthreads();          // the next pass stages from row 0 again
+                stage(v_cache, 0, false);
+            }
+        }
+        if (active)
+            for (int r = 0; r < rep; ++r) part[(size_t)r * 4 * D + i] = acc[r];
+    }
+    __syncthreads();
+    // fold: output (head r, column c) for r * D + c = t + nthreads * it
+    for (int o = t, it = 0; o < rep * D; o += nthreads, ++it) {
+        const int r = o / D, c = o % D;
+        const float *pp = part + (size_t)r * 4 * D + c;
+        float v = naive ? pp[0] : ((pp[0] + pp[D]) + pp[2 * D]) + pp[3 * D];
+        v = bfr(v);
+        const float g = it == 0 ? gpre[0] : it == 1 ? gpre[1] : bf(qg[(size_t)(kh * rep + r) * 2 * D + D + c]);
+        v = v * bfr(__fdiv_rn(1.0f, 1.0f + sleef_expf(-g)));
+        out[(size_t)(kh * rep + r) * D + c] = f32_to_bf16(v);
     }
 }
 
@@ -514,8 +933,22 @@ int ekernel_rmsnorm_gemma_bf16(const ekernel_rmsnorm_desc_t *desc, const uint16_
     if (rc == ECPU_OK && residual_out) rc = check_device_buffer(residual_out, bytes, "residual_out", fn);
     if (rc != ECPU_OK) return rc;
     const size_t lds = (n + 4) * sizeof(float);
-    rmsnorm_kernel<<<(unsigned)M, 256, lds, current_stream()>>>(x, residual, weight, out, residual_out, (int)n,
-                                                                desc->eps);
+    const uintptr_t ptrs = (uintptr_t)x | (uintptr_t)residual | (uintptr_t)weight | (uintptr_t)out |
+                           (uintptr_t)residual_out;
+    hipStream_t st = current_stream();
+    if (n % 8 == 0 && (ptrs & 15) == 0) {
+        if (n <= 2048)
+            rmsnorm_vec_kernel<1><<<(unsigned)M, 256, lds, st>>>(x, residual, weight, out, residual_out, (int)n,
+                                                                 desc->eps);
+        else if (n <= 4096)
+            rmsnorm_vec_kernel<2><<<(unsigned)M, 256, lds, st>>>(x, residual, weight, out, residual_out, (int)n,
+                                                                 desc->eps);
+        else
+            rmsnorm_vec_kernel<4><<<(unsigned)M, 256, lds, st>>>(x, residual, weight, out, residual_out, (int)n,
+                                                                 desc->eps);
+    } else {
+        rmsnorm_kernel<<<(unsigned)M, 256, lds, st>>>(x, residual, weight, out, residual_out, (int)n, desc->eps);
+    }
     return check_launch(fn);
 }
 
@@ -595,6 +1028,80 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
     else if (D == 128) PILM_ATTN_EXACT(128);
     else PILM_ATTN_EXACT(256);
 #undef PILM_ATTN_EXACT
+    return check_launch(fn);
+}
+
+// LDS a workgroup may hold on the current device (gfx950: 160 KB).
+static size_t lds_limit() {
+    static size_t cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+    if (!cached[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 64 * 1024;
+        cached[dev] = std::min<size_t>((size_t)v, 160 * 1024);
+    }
+    return cached[dev];
+}
+
+int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint16_t *qg, const uint16_t *k,
+                                  const uint16_t *v, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                                  const float *cos_table, const float *sin_table, const int32_t *step,
+                                  uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids, uint16_t *out) {
+    static const char *fn = "ekernel_decode_attention_bf16";
+    if (!desc || !qg || !k || !v || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !k_cache || !v_cache ||
+        !block_ids || !out)
+        return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    const ekernel_qk_rope_desc_t &d = *desc;
+    if (d.S != 1) return fail(ECPU_ERR_UNSUPPORTED, "%s: one decode row per call (S = %zu)", fn, d.S);
+    // 256-wide heads would hold a whole key row and its products beyond the
+    // registers a 512-thread workgroup has: the two-call path serves them
+    if (d.head_dim != 64 && d.head_dim != 128)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: head_dim %zu (64 or 128)", fn, d.head_dim);
+    if (d.rot_dim > d.head_dim || d.rot_dim % 2 || d.n_kv_heads == 0 || d.n_heads % d.n_kv_heads ||
+        d.block_size == 0 || d.n_block_ids == 0 || d.max_positions == 0)
+        return fail(ECPU_ERR_PARAM, "%s: inconsistent descriptor", fn);
+    const size_t rep = d.n_heads / d.n_kv_heads, D = d.head_dim;
+    if (rep != 1 && rep != 2 && rep != 4)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu q heads per kv head (1, 2 or 4)", fn, rep);
+    const size_t max_len = d.n_block_ids * d.block_size;
+    if (!step && (d.pos0 + 1 > d.max_positions || d.pos0 + 1 > max_len))
+        return fail(ECPU_ERR_PARAM, "%s: position %zu beyond the tables", fn, d.pos0);
+    const size_t fixed = ((rep + 1) * D + rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * 4 * D +
+                          ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
+    const size_t budget = lds_limit();
+    const size_t room = fixed < budget ? (budget - fixed) / (D * 2) : 0;
+    const size_t vcap = std::min<size_t>(room / 64 * 64, (max_len + 63) / 64 * 64);
+    if (vcap < 64)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu positions x %zu heads per kv head exceed LDS", fn, max_len, rep);
+    const size_t lds = fixed + vcap * D * 2;
+    const size_t cache_bytes = d.num_blocks * d.block_size * d.n_kv_heads * D * 2;
+    int rc = check_device_buffer(qg, d.n_heads * 2 * D * 2, "qg", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(k_cache, cache_bytes, "k_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(v_cache, cache_bytes, "v_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(block_ids, d.n_block_ids * 4, "block_ids", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(cos_table, d.max_positions * (d.rot_dim / 2) * 4, "cos_table", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(sin_table, d.max_positions * (d.rot_dim / 2) * 4, "sin_table", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(out, d.n_heads * D * 2, "out", fn);
+    if (rc != ECPU_OK) return rc;
+    const float scale = (float)(1.0 / __builtin_sqrt((double)D));
+    hipStream_t st = current_stream();
+#define PILM_DECODE_ATTN(DD, RR)                                                                                     \
+    decode_attn_kernel<DD, RR><<<(unsigned)d.n_kv_heads, kDecodeThreads, lds, st>>>(                                \
+        qg, k, v, q_norm_w, k_norm_w, cos_table, sin_table, (int)d.max_positions, step, (int)d.pos0, k_cache,       \
+        v_cache, block_ids, (int)d.n_block_ids, (int)d.block_size, (int)d.num_blocks, (int)d.n_heads,              \
+        (int)d.n_kv_heads, (int)d.rot_dim, d.eps, (int)max_len, (int)vcap, scale, out)
+    if (D == 64) {
+        if (rep == 1) PILM_DECODE_ATTN(64, 1);
+        else if (rep == 2) PILM_DECODE_ATTN(64, 2);
+        else PILM_DECODE_ATTN(64, 4);
+    } else {
+        if (rep == 1) PILM_DECODE_ATTN(128, 1);
+        else if (rep == 2) PILM_DECODE_ATTN(128, 2);
+        else PILM_DECODE_ATTN(128, 4);
+    }
+#undef PILM_DECODE_ATTN
     return check_launch(fn);
 }
 

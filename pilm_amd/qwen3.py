@@ -146,7 +146,8 @@ class Qwen3Decoder:
     """One sequence's decode state: paged KV caches, rope tables, the device
     state word {pos0, cache_len, count} and the step buffers."""
 
-    def __init__(self, weights: Qwen3Weights, max_positions: int, max_new_tokens: int = 1024):
+    def __init__(self, weights: Qwen3Weights, max_positions: int, max_new_tokens: int = 1024,
+                 max_rows: int | None = None, pool_blocks: int | None = None):
         self.w = w = weights
         self.cfg = c = weights.cfg
         dev = w.embed.device
@@ -154,15 +155,17 @@ class Qwen3Decoder:
         self.lib = abi._load_lib()
         bs = c.block_size
         self.max_pos = max_positions
-        self.nblocks = (max_positions + bs - 1) // bs
-        kv_shape = (self.nblocks, bs, c.kv_heads, c.head_dim)
+        self.nblocks = (max_positions + bs - 1) // bs          # blocks one sequence can use
+        self.pool = pool_blocks or self.nblocks                  # blocks in each layer's cache
+        kv_shape = (self.pool, bs, c.kv_heads, c.head_dim)
         self.k_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.layers)]
         self.v_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.layers)]
         # the reference's block manager hands out block ids; any assignment gives the same arithmetic
         self.block_ids = torch.arange(self.nblocks, dtype=torch.int32, device=dev)
         cos, sin = rope_tables(c.rope_theta, c.rot_dim, max_positions)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
-        S, H, D, Hq, I = bs, c.hidden, c.head_dim, c.heads, c.intermediate
+        S, H, D, Hq, I = max_rows or bs, c.hidden, c.head_dim, c.heads, c.intermediate
+        self.max_rows = S
         e = dict(dtype=torch.bfloat16, device=dev)
         self.nqkv = w.layers[0]["qkv"][0].shape[0]
         self.x = torch.empty((S, H), **e)
@@ -176,12 +179,15 @@ class Qwen3Decoder:
         self.act = torch.empty((S, I), **e)
         self.mlp = torch.empty((S, H), **e)
         self.logits = torch.empty((c.vocab,), **e)
+        self.logits_rows = torch.empty((S, c.vocab), **e) if max_rows else None
         self.state = torch.zeros(4, dtype=torch.int32, device=dev)      # pos0, cache_len, count
         self.max_new = max_new_tokens
         self.tokens = torch.zeros(max_new_tokens, dtype=torch.int32, device=dev)
         self.next_id = torch.zeros(1, dtype=torch.int64, device=dev)
         self.graph = None
         self._descs = {}
+        # the one-launch decode attention serves 64- and 128-wide heads, 1, 2 or 4 q heads per kv head
+        self.fused_decode = c.head_dim in (64, 128) and c.heads // c.kv_heads in (1, 2, 4)
 
     # ---------------------------------------------------------------- calls
     def _check(self, rc: int, name: str) -> None:
@@ -206,18 +212,21 @@ class Qwen3Decoder:
         self._check(self.lib.ekernel_rmsnorm_gemma_bf16(ctypes.byref(d), _vp(x), _vp(res), _vp(weight), _vp(out),
                                                         _vp(res_out)), "ekernel_rmsnorm_gemma_bf16")
 
-    def _forward(self, m: int, with_logits: bool):
-        """The model over the m tokens in self.x at the positions the state
-        word names; with_logits: final norm + lm_head of the last token."""
+    def _forward(self, m: int, with_logits: bool, groups=None):
+        """The model over the m tokens in self.x.  groups None: one sequence at
+        the positions the state word names (graph-capturable); with_logits:
+        final norm + lm_head of the last token and the greedy step.  groups:
+        [(row0, rows, pos0, block table)] -- several sequences' rows in one
+        batch, positions from the host; the linears take all m rows at once
+        and with_logits gives the logits of every row (self.logits_rows)."""
         c, L = self.cfg, self.lib
         D, Hq, Hkv, I = c.head_dim, c.heads, c.kv_heads, c.intermediate
-        rope = self._desc(("rope", m), lambda: abi.EkernelQkRopeDesc(
-            m, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, 0, self.max_pos, c.block_size, self.nblocks,
-            self.nblocks, c.eps))
-        att = self._desc(("attn", m), lambda: abi.EkernelAttentionExactDesc(
-            m, Hq, Hkv, D, m, c.block_size, self.nblocks, self.nblocks, self.nqkv, 2 * D))
         qkv_p = self.qkv.data_ptr()
         k_off, v_off = 2 * Hq * D * 2, (2 * Hq * D + Hkv * D) * 2
+        if groups is None:
+            groups_run = [(0, m, None, self.block_ids)]
+        else:
+            groups_run = groups
         res_in = None
         for li, Lw in enumerate(self.w.layers):
             if li == 0:
@@ -227,14 +236,36 @@ class Qwen3Decoder:
                 self._norm(self.mlp, self.res, Lw["in_norm"], self.h, self.res, m)
                 res_in = self.res
             self._linear(self.h, Lw["qkv"], self.qkv, m)
-            self._check(L.ekernel_qk_norm_rope_bf16(
-                ctypes.byref(rope), ctypes.c_void_p(qkv_p), ctypes.c_void_p(qkv_p + k_off),
-                ctypes.c_void_p(qkv_p + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos), _vp(self.sin),
-                _vp(self.state), _vp(self.q), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(self.block_ids)),
-                "ekernel_qk_norm_rope_bf16")
-            self._check(L.ekernel_attention_exact_bf16(
-                ctypes.byref(att), _vp(self.q), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(self.block_ids),
-                ctypes.c_void_p(qkv_p + D * 2), _vp(self.state), _vp(self.attn)), "ekernel_attention_exact_bf16")
+            for (r0, n, pos0, table) in groups_run:
+                def mk_rope():
+                    return abi.EkernelQkRopeDesc(n, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, pos0 or 0,
+                                                 self.max_pos, c.block_size, self.pool, table.numel(), c.eps)
+
+                def mk_att():
+                    return abi.EkernelAttentionExactDesc(n, Hq, Hkv, D, (pos0 or 0) + n, c.block_size, self.pool,
+                                                         table.numel(), self.nqkv, 2 * D)
+                # one sequence's descriptors are reused; batch positions change every step
+                rope = self._desc(("rope", n), mk_rope) if pos0 is None else mk_rope()
+                att = self._desc(("attn", n), mk_att) if pos0 is None else mk_att()
+                step = self.state if pos0 is None else None
+                rp = qkv_p + r0 * self.nqkv * 2
+                if n == 1 and self.fused_decode:
+                    # one decode row: norm, rope, cache write and attention in one launch
+                    self._check(L.ekernel_decode_attention_bf16(
+                        ctypes.byref(rope), ctypes.c_void_p(rp), ctypes.c_void_p(rp + k_off),
+                        ctypes.c_void_p(rp + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos),
+                        _vp(self.sin), _vp(step), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(table),
+                        ctypes.c_void_p(self.attn.data_ptr() + r0 * Hq * D * 2)), "ekernel_decode_attention_bf16")
+                    continue
+                self._check(L.ekernel_qk_norm_rope_bf16(
+                    ctypes.byref(rope), ctypes.c_void_p(rp), ctypes.c_void_p(rp + k_off), ctypes.c_void_p(rp + v_off),
+                    _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos), _vp(self.sin), _vp(step),
+                    ctypes.c_void_p(self.q.data_ptr() + r0 * Hq * D * 2), _vp(self.k_cache[li]),
+                    _vp(self.v_cache[li]), _vp(table)), "ekernel_qk_norm_rope_bf16")
+                self._check(L.ekernel_attention_exact_bf16(
+                    ctypes.byref(att), ctypes.c_void_p(self.q.data_ptr() + r0 * Hq * D * 2), _vp(self.k_cache[li]),
+                    _vp(self.v_cache[li]), _vp(table), ctypes.c_void_p(rp + D * 2), _vp(step),
+                    ctypes.c_void_p(self.attn.data_ptr() + r0 * Hq * D * 2)), "ekernel_attention_exact_bf16")
             self._linear(self.attn, Lw["o"], self.o, m)
             self._norm(self.o, res_in, Lw["post_norm"], self.h, self.res, m)
             self._linear(self.h, Lw["gate_up"], self.gu, m)
@@ -242,12 +273,15 @@ class Qwen3Decoder:
             self._check(L.ekernel_silu_mul_bf16(ctypes.c_void_p(gp), ctypes.c_void_p(gp + I * 2), m, I, 2 * I,
                                                 _vp(self.act)), "ekernel_silu_mul_bf16")
             self._linear(self.act, Lw["down"], self.mlp, m)
-        if with_logits:
+        if with_logits and groups is None:
             last = m - 1
             self._norm(self.mlp[last:m], self.res[last:m], self.w.norm, self.h, None, 1)
             self._linear(self.h[:1], self.w.lm_head, self.logits.view(1, -1), 1)
             self._check(L.ekernel_greedy_step_bf16(_vp(self.logits), c.vocab, _vp(self.state), _vp(self.tokens),
                                                    self.max_new, _vp(self.next_id)), "ekernel_greedy_step_bf16")
+        elif with_logits:
+            self._norm(self.mlp, self.res, self.w.norm, self.h, None, m)
+            self._linear(self.h, self.w.lm_head, self.logits_rows, m)
 
     def _bind(self):
         abi.set_stream(torch.cuda.current_stream(self.dev).cuda_stream)
@@ -324,3 +358,122 @@ class Qwen3Decoder:
                     on_logits(i, self.logits)
         torch.cuda.synchronize(self.dev)
         return self.tokens[:n_new].tolist()
+
+
+def accept_drafts(logits_rows: torch.Tensor, drafts: list) -> tuple:
+    """Greedy MTP verification of one sequence (src/engine.py:467-545): row i
+    of the logits (rows 0 .. len(drafts)) is what the model predicts after the
+    sequence's last token and drafts[:i]; drafts are accepted while each
+    equals the argmax of the row before it; the first mismatch's argmax, or
+    when all are accepted the argmax of the last row, is the next token.
+    Returns (accepted drafts, next token).  Argmax as torch.argmax on the
+    fp32 copy: the first index of the largest value."""
+    ids = torch.argmax(logits_rows.to(torch.float32), dim=-1).tolist()
+    acc = []
+    for i, d in enumerate(drafts):
+        if ids[i] != int(d):
+            return acc, ids[i]
+        acc.append(int(d))
+    return acc, ids[len(drafts)]
+
+
+class Qwen3Batch(Qwen3Decoder):
+    """Several sequences decoding together (continuous batching,
+    src/runtime/scheduler/scheduler.py:70-178): one paged KV pool per layer,
+    one block table per sequence, and steps that pass every sequence's rows
+    as one M to the linears -- an MTP verify step of 16 sequences x (1 + 4
+    drafts) is one M = 80 call per linear.  The linears run on the bit-exact
+    kernels at every M (the matrix-core threshold is raised above the batch
+    for the step), so each sequence's logits are bit-identical to its own
+    per-sequence run, as the reference verifies each sequence by itself
+    (src/engine.py:416-459)."""
+
+    def __init__(self, weights: Qwen3Weights, n_seqs: int, max_positions: int, max_rows: int = 96):
+        bs = weights.cfg.block_size
+        per_seq = (max_positions + bs - 1) // bs
+        super().__init__(weights, max_positions, max_new_tokens=1, max_rows=max_rows,
+                         pool_blocks=per_seq * n_seqs)
+        self.tables = [torch.arange(i * per_seq, (i + 1) * per_seq, dtype=torch.int32, device=self.dev)
+                       for i in range(n_seqs)]
+        self.cache_len = [0] * n_seqs
+
+    def _run(self, groups_tokens, with_logits: bool):
+        rows = sum(len(t) for _, t in groups_tokens)
+        if rows > self.max_rows:
+            raise ValueError(f"{rows} rows exceed the batch buffers ({self.max_rows})")
+        ids = torch.tensor([t for _, toks in groups_tokens for t in toks], dtype=torch.int64, device=self.dev)
+        torch.index_select(self.w.embed, 0, ids, out=self.x[:rows])
+        groups, r0 = [], 0
+        for seq, toks in groups_tokens:
+            pos0 = self.cache_len[seq]
+            if pos0 + len(toks) > self.max_pos:
+                raise ValueError(f"sequence {seq} would exceed {self.max_pos} positions")
+            groups.append((r0, len(toks), pos0, self.tables[seq]))
+            r0 += len(toks)
+        prev = abi.matrix_core_min_rows()
+        abi.set_matrix_core_min_rows(0)          # 0: exact kernels at every M
+        try:
+            self._bind()
+            self._forward(rows, with_logits, groups=groups)
+        finally:
+            abi.set_matrix_core_min_rows(prev)
+        return rows
+
+    def prefill_seq(self, seq: int, prompt: list) -> int:
+        """One sequence's prompt in the engine's block-aligned chunks; returns
+        the greedy first token."""
+        bs = self.cfg.block_size
+        self.cache_len[seq] = 0
+        pos = 0
+        while pos < len(prompt):
+            n = min(len(prompt) - pos, bs - pos % bs)
+            rows = self._run([(seq, prompt[pos:pos + n])], with_logits=pos + n == len(prompt))
+            self.cache_len[seq] += n
+            pos += n
+        return int(torch.argmax(self.logits_rows[rows - 1].to(torch.float32)).item())
+
+    def prefill_seqs(self, seqs: list, prompts: list) -> list:
+        """Several sequences' prompts together: each step packs the next
+        block-aligned chunk of every unfinished sequence into one batch of at
+        most max_rows rows.  Returns each sequence's greedy first token."""
+        bs = self.cfg.block_size
+        pos = {s: 0 for s in seqs}
+        for s in seqs:
+            self.cache_len[s] = 0
+        first = {}
+        while len(first) < len(seqs):
+            groups, rows, final = [], 0, []
+            for s, p in zip(seqs, prompts):
+                if s in first:
+                    continue
+                n = min(len(p) - pos[s], bs - pos[s] % bs)
+                if rows + n > self.max_rows:
+                    break
+                groups.append((s, p[pos[s]:pos[s] + n]))
+                if pos[s] + n == len(p):
+                    final.append((s, rows + n - 1))
+                rows += n
+            if not groups:
+                raise ValueError(f"a chunk of {bs} rows exceeds the batch buffers ({self.max_rows})")
+            self._run(groups, with_logits=bool(final))
+            for s, toks in groups:
+                self.cache_len[s] += len(toks)
+                pos[s] += len(toks)
+            for s, r in final:
+                first[s] = int(torch.argmax(self.logits_rows[r].to(torch.float32)).item())
+        return [first[s] for s in seqs]
+
+    def verify(self, last_tokens: list, drafts: list) -> list:
+        """One verify step for every sequence: sequence i feeds
+        [last_tokens[i]] + drafts[i] (its positions follow its cache); all rows
+        go through the model as one batch; returns [(accepted, next token)]
+        per sequence and advances each cache past the accepted tokens."""
+        groups = [(i, [int(last_tokens[i])] + [int(d) for d in drafts[i]]) for i in range(len(drafts))]
+        self._run(groups, with_logits=True)
+        out, r0 = [], 0
+        for (i, toks) in groups:
+            acc, nxt = accept_drafts(self.logits_rows[r0:r0 + len(toks)], drafts[i])
+            out.append((acc, nxt))
+            self.cache_len[i] += 1 + len(acc)
+            r0 += len(toks)
+        return out

@@ -62,7 +62,8 @@ def _vp(t):
 
 # --------------------------------------------------------------- rmsnorm
 
-@pytest.mark.parametrize("rows,n", [(1, 2048), (16, 2048), (3, 4096), (2, 128), (5, 296), (1, 8192)])
+@pytest.mark.parametrize("rows,n", [(1, 2048), (16, 2048), (3, 4096), (2, 128), (5, 296), (1, 8192), (2, 6144),
+                                    (2, 100)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_rmsnorm_kernel(lib, dev, rows, n, with_res):
     import ctypes
@@ -97,6 +98,24 @@ def test_rmsnorm_in_place_residual(lib, dev):
                                         _vp(wd), _vp(out), _vp(rd))
     assert rc == 0
     assert np.array_equal(_bits(out), want) and np.array_equal(_bits(rd), want_res)
+
+
+def test_rmsnorm_unaligned_rows(lib, dev):
+    """Rows that are not 16-byte aligned take the element-wise kernel."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(9)
+    x, r, w = _rand16(rng, (3, 2048)), _rand16(rng, (3, 2048)), _rand16(rng, (2048,), 0.02)
+    want, want_res = OD.rmsnorm_gemma_bf16(x, r, w, 1e-6)
+    xd = torch.empty(3 * 2048 + 1, dtype=torch.bfloat16, device=dev)
+    xd[1:].copy_(_dev16(x, dev).reshape(-1))
+    rd, wd = _dev16(r, dev), _dev16(w, dev)
+    out, res_out = torch.empty((3, 2048), dtype=torch.bfloat16, device=dev), torch.empty_like(rd)
+    _bind()
+    rc = lib.ekernel_rmsnorm_gemma_bf16(ctypes.byref(abi.EkernelRmsnormDesc(3, 2048, 1e-6)), _vp(xd[1:]), _vp(rd),
+                                        _vp(wd), _vp(out), _vp(res_out))
+    assert rc == 0, abi.last_error()
+    assert np.array_equal(_bits(out), want) and np.array_equal(_bits(res_out), want_res)
 
 
 # ----------------------------------------------------- q/k norm + rope + attention
@@ -160,6 +179,72 @@ def test_qk_rope_then_attention(lib, dev, S, H, Hkv, D, pos0):
         got = _bits(out_d)
         bad = np.argwhere(got != want)
         assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()} (step={use_step})"
+
+
+@pytest.mark.parametrize("H,Hkv,D,pos0", [(16, 8, 128, 383), (16, 8, 128, 0), (16, 8, 128, 1), (16, 8, 128, 2),
+                                          (16, 8, 128, 3), (16, 8, 128, 7), (16, 8, 128, 64), (32, 8, 128, 2043),
+                                          (4, 2, 128, 0), (8, 8, 64, 17), (16, 4, 128, 100), (16, 8, 128, 4000),
+                                          (32, 8, 64, 515)])
+def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0):
+    """ekernel_decode_attention_bf16 (one launch) against the oracle's two
+    steps: the same output bits and the same cache rows, with the position
+    from the host and from the device state word.  Cases: lengths 1-4
+    (torch's small-matrix kernel below 4), 8 and 65 (tails of the four- and
+    eight-way sums), 1, 2 and 4 q heads per kv head, value rows staged in one
+    pass and in several (2044 and 4001 positions)."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(pos0 * 31 + H + D)
+    bs, S = 16, 1
+    L, block_ids, kc, vc, qkv, qw, kw = _attn_case(rng, S, H, Hkv, D, pos0, bs)
+    cos, sin = OD.rope_tables(1e6, D, L + 1)
+    stride = qkv.shape[1]
+    qg, k, v = qkv[:, :2 * H * D], qkv[:, 2 * H * D:2 * H * D + Hkv * D], qkv[:, 2 * H * D + Hkv * D:]
+    kc_o, vc_o = kc.copy(), vc.copy()
+    q_want = OD.qk_norm_rope_bf16(qg, k, v, qw, kw, cos, sin, pos0, kc_o, vc_o, block_ids, n_heads=H, n_kv_heads=Hkv,
+                                  head_dim=D, rot_dim=D, eps=1e-6, block_size=bs)
+    want = OD.attention_exact_bf16(q_want, kc_o, vc_o, block_ids, L, qkv.reshape(-1)[D:], stride, 2 * D,
+                                   block_size=bs)
+    qkv_d, kc_d, vc_d = _dev16(qkv, dev), _dev16(kc, dev), _dev16(vc, dev)
+    bid_d = torch.from_numpy(block_ids).to(dev)
+    cos_d, sin_d = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    qw_d, kw_d = _dev16(qw, dev), _dev16(kw, dev)
+    out_d = torch.empty((1, H * D), dtype=torch.bfloat16, device=dev)
+    step = torch.tensor([pos0, L, 0, 0], dtype=torch.int32, device=dev)
+    _say(f"[gpu] fused decode attention H={H} Hkv={Hkv} D={D} pos0={pos0}")
+    _bind()
+    p = qkv_d.data_ptr()
+    for use_step in (False, True):
+        kc_d.copy_(_dev16(kc, dev))
+        vc_d.copy_(_dev16(vc, dev))
+        out_d.zero_()
+        rd = abi.EkernelQkRopeDesc(1, H, Hkv, D, D, stride, stride, pos0, L + 1, bs, kc.shape[0], len(block_ids), 1e-6)
+        rc = lib.ekernel_decode_attention_bf16(ctypes.byref(rd), ctypes.c_void_p(p),
+                                               ctypes.c_void_p(p + 2 * H * D * 2),
+                                               ctypes.c_void_p(p + (2 * H * D + Hkv * D) * 2), _vp(qw_d), _vp(kw_d),
+                                               _vp(cos_d), _vp(sin_d), _vp(step if use_step else None), _vp(kc_d),
+                                               _vp(vc_d), _vp(bid_d), _vp(out_d))
+        assert rc == 0, abi.last_error()
+        assert np.array_equal(_bits(kc_d), kc_o) and np.array_equal(_bits(vc_d), vc_o)
+        got = _bits(out_d)
+        bad = np.argwhere(got != want)
+        assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()} (step={use_step})"
+
+
+def test_decode_attention_fused_refuses_unsupported(lib, dev):
+    """Other than 1, 2 or 4 q heads per kv head, 256-wide heads and S > 1 are
+    refused (the two-call path serves them)."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    buf = torch.zeros(1 << 20, dtype=torch.bfloat16, device=dev)
+    cs = torch.zeros(1 << 16, dtype=torch.float32, device=dev)
+    bid = torch.zeros(4, dtype=torch.int32, device=dev)
+    _bind()
+    for S, H, Hkv, D in ((1, 16, 2, 128), (1, 6, 2, 128), (1, 4, 2, 256), (2, 4, 2, 128)):
+        rd = abi.EkernelQkRopeDesc(S, H, Hkv, D, D, 0, 0, 0, 16, 16, 4, 4, 1e-6)
+        rc = lib.ekernel_decode_attention_bf16(ctypes.byref(rd), _vp(buf), _vp(buf), _vp(buf), _vp(buf), _vp(buf),
+                                               _vp(cs), _vp(cs), None, _vp(buf), _vp(buf), _vp(bid), _vp(buf))
+        assert rc == abi.ECPU_ERR_UNSUPPORTED, (S, H, Hkv, D, rc)
 
 
 @pytest.mark.parametrize("L", [1, 2, 3, 4, 5, 8, 9, 64, 65, 129, 512])
@@ -285,6 +370,10 @@ def test_decoder_tiny_matches_reference(dev):
     assert dec2.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
     # a second sequence on the same decoder (graph already captured) starts clean
     assert dec2.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
+    _say("[gpu] decoder, two-layer model: the two-call attention path")
+    dec3 = Q.Qwen3Decoder(w, max_positions=dec.max_pos, max_new_tokens=dec.max_new)
+    dec3.fused_decode = False
+    assert dec3.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
 
 
 def test_decoder_qwen3_1p7b_matches_reference(dev):

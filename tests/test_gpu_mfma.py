@@ -126,22 +126,31 @@ def test_mfma_split_k(splits, dev, monkeypatch):
 @pytest.mark.parametrize("fmt", ["w8a16", "w4g128", "w4"])
 @pytest.mark.parametrize("nseq", [12, 16])
 def test_continuous_batching_verify(fmt, nseq, dev):
-    """MTP verify under continuous batching (src/engine.py:374-570,
+    """MTP verify under continuous batching (src/engine.py:416-545,
     scheduler.py:70-178): every sequence's 1 + 4 draft rows go into one call,
-    M = 5 * nseq.  Each sequence's rows must come out as its own M = 5 call
-    gives them: bit-identical below the matrix-core threshold (12 sequences,
-    M = 60), within the matrix-core tolerance from it on (16 sequences,
-    M = 80)."""
+    M = 5 * nseq, compared with the oracle.  Below the matrix-core threshold
+    (12 sequences, M = 60) the call is bit-identical to it; from the threshold
+    on (16 sequences, M = 80) the matrix-core call is within its tolerance and
+    the same call forced onto the exact kernels (threshold 0, what the batched
+    decoder's verify step does) is bit-identical again."""
+    from pilm_amd import bindings as abi
     gen = GV._gen()
     n, k = 1024, 4096          # Qwen3-8B k_proj
     x, w, s = gen.make_inputs(fmt, 5 * nseq, n, k, 9500 + nseq)
     _say(f"[gpu] batched verify {fmt} sequences={nseq} M={5 * nseq}")
     y = run_gpu(fmt, x, w, s, dev)
-    per = np.concatenate([run_gpu(fmt, x[5 * i:5 * i + 5], w, s, dev) for i in range(nseq)])
+    ref = gen.run(fmt, x, w, s, "oracle")
     if 5 * nseq < 64:
-        assert np.array_equal(y.view(np.uint8), per.view(np.uint8)), fmt
-    else:
-        check_close(fmt, y, per, f"{fmt} batched M={5 * nseq}")
+        assert np.array_equal(y.view(np.uint8), ref.view(np.uint8)), fmt
+        return
+    check_close(fmt, y, ref, f"{fmt} batched M={5 * nseq}")
+    prev = abi.matrix_core_min_rows()
+    abi.set_matrix_core_min_rows(0)
+    try:
+        y0 = run_gpu(fmt, x, w, s, dev)
+    finally:
+        abi.set_matrix_core_min_rows(prev)
+    assert np.array_equal(y0.view(np.uint8), ref.view(np.uint8)), f"{fmt} exact kernels at M={5 * nseq}"
 
 
 @pytest.mark.parametrize("bm,wm", [("64", "1"), ("64", "2"), ("128", "1"), ("128", "2"), ("256", "2")])

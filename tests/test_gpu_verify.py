@@ -1,0 +1,167 @@
+"""GPU: speculative (MTP) verify under continuous batching, against the oracle.
+
+The reference verifies one sequence's last token and its drafts as one
+model call over 1 + k rows, lm_head over every row, and accepts the drafts
+while each equals the argmax of the row before it (src/engine.py:416-545).
+Under continuous batching (src/runtime/scheduler/scheduler.py:70-178) the
+device takes every running sequence's rows as one M: 16 sequences x
+(1 + 4 drafts) is an M = 80 call per linear, attention per sequence on its
+own block table in a shared KV pool.
+
+Checked here:
+  * the two-layer model: every verify row's bf16 logits bit-identical to the
+    oracle's per-sequence model call (oracle/decoder.py), the accepted drafts
+    and next token per sequence equal to the oracle's, and the emitted tokens
+    equal to plain greedy decoding (what greedy speculation must give);
+  * Qwen3-1.7B W4A16 g128: 16 sequences on the 128-token prompt of the
+    reference's fixture, speculating with drafts taken from the reference's
+    own greedy tokens and corrupted at varying positions; every verify row's
+    logits, accepted drafts and next token equal to the oracle's (a fixture:
+    the oracle needs minutes per sequence at this size).  A verify row is not
+    always bit-identical to the one-row decode step at its position (torch's
+    P.V partial sums depend on the masked row length), so these tokens may
+    leave the plain greedy ones at a near tie, in the reference too.
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import decoder as OD
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _fixture(name):
+    return json.loads((GOLDEN / f"decode_{name}.json").read_text())
+
+
+def _corrupt(tok, vocab, salt):
+    return (tok + 1 + salt) % vocab
+
+
+def _drafts(greedy, start, n, bad, vocab, salt):
+    """n drafts following greedy[start - 1]; draft `bad` (if < n) is wrong."""
+    d = list(greedy[start:start + n])
+    if bad < n:
+        d[bad] = _corrupt(d[bad], vocab, salt)
+        assert d[bad] != greedy[start + bad]
+    return d
+
+
+def test_batched_verify_two_layer_matches_oracle(dev):
+    from pilm_amd import qwen3 as Q
+    from pilm_amd import synth_model as SM
+    fx = _fixture("tiny")
+    c = dict(fx["config"])
+    n_seq, n_greedy = 16, 12
+    prompts = [SM.token_ids(200 + i, 3 + 7 * i, c["vocab"]) for i in range(n_seq)]
+    c["prompt"], c["new_tokens"] = max(len(p) for p in prompts), n_greedy + 4
+    V = c["vocab"]
+
+    # Two verify steps per sequence.  Step 1: 4 drafts, the j-th wrong
+    # (j = i % 5; 4 means all right).  Step 2: 0 .. 4 drafts, one maybe wrong.
+    plan = []
+    for i in range(n_seq):
+        j1 = i % 5
+        n2, j2 = i % 5, (3 * i + 1) % 5
+        plan.append((j1, n2, j2))
+
+    _say("[gpu] batched verify, two-layer model: oracle greedy and verify rows (CPU)")
+    od = OD.OracleDecoder(c)
+    greedy, want = [], []
+    for i in range(n_seq):
+        g = od.generate(prompts[i], n_greedy)
+        greedy.append(g)
+        j1, n2, j2 = plan[i]
+        p = len(prompts[i])
+        d1 = _drafts(g, 1, 4, j1, V, i)
+        rows1 = od.forward([g[0]] + d1, p, all_rows=True)
+        a1 = min(j1, 4)
+        d2 = _drafts(g, 2 + a1, n2, j2, V, i + 7)
+        rows2 = od.forward([g[1 + a1]] + d2, p + 1 + a1, all_rows=True)
+        want.append(((d1, rows1), (d2, rows2)))
+
+    _say("[gpu] batched verify, two-layer model: weights, prefill")
+    w = Q.Qwen3Weights.synthetic(Q.Qwen3Config.from_dict(c), c["seed"], c["std"], device=dev)
+    b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=c["prompt"] + c["new_tokens"] + 1, max_rows=96)
+    first = [b.prefill_seq(i, prompts[i]) for i in range(n_seq)]
+    assert first == [g[0] for g in greedy]
+
+    last = first
+    for step in range(2):
+        drafts = [want[i][step][0] for i in range(n_seq)]
+        rows = sum(1 + len(d) for d in drafts)
+        _say(f"[gpu] batched verify, two-layer model: step {step + 1}, M = {rows}")
+        out = b.verify(last, drafts)
+        r0 = 0
+        for i in range(n_seq):
+            d, ref_rows = want[i][step]
+            got = _bits(b.logits_rows[r0:r0 + 1 + len(d)])
+            assert np.array_equal(got, ref_rows), f"sequence {i} step {step + 1}: logits differ from the oracle"
+            r0 += 1 + len(d)
+            ids = [OD.argmax_bf16(r) for r in ref_rows]
+            acc = []
+            for k, t in enumerate(d):
+                if ids[k] != t:
+                    break
+                acc.append(t)
+            nxt = ids[len(acc)]
+            assert out[i] == (acc, nxt), f"sequence {i} step {step + 1}"
+            emitted = [last[i]] + acc + [nxt]
+            pos = b.cache_len[i] - len(prompts[i])           # tokens of the sequence now in the cache
+            assert emitted == greedy[i][pos - 1 - len(acc):pos + 1], f"sequence {i}: not the greedy tokens"
+        last = [o[1] for o in out]
+
+
+def test_batched_speculation_qwen3_1p7b_matches_oracle(dev):
+    """Qwen3-1.7B W4A16 g128: 16 sequences on the reference fixture's prompt,
+    8 verify steps of M = 80, all on the exact kernels.  Each step's drafts,
+    accepted drafts, next token and the sha256 of the five verify rows' bf16
+    logits must equal what the oracle computed for that sequence alone
+    (tests/golden/verify_qwen3_1p7b.json, written by gen_verify_fixture.py)."""
+    from pilm_amd import qwen3 as Q
+    fx = _fixture("qwen3_1p7b")
+    path = GOLDEN / "verify_qwen3_1p7b.json"
+    if not path.exists():
+        pytest.skip("tests/golden/verify_qwen3_1p7b.json not generated (gen_verify_fixture.py)")
+    sv = json.loads(path.read_text())
+    c = fx["config"]
+    n_seq, steps = sv["n_seq"], sv["steps"]
+    _say("[gpu] batched speculation Qwen3-1.7B: weights")
+    w = Q.Qwen3Weights.synthetic(Q.Qwen3Config.from_dict(c), c["seed"], c["std"], device=dev)
+    b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=c["prompt"] + 5 * steps + 8, max_rows=96)
+    _say(f"[gpu] batched speculation Qwen3-1.7B: prefill {n_seq} x {len(fx['prompt'])} tokens")
+    first = b.prefill_seqs(list(range(n_seq)), [fx["prompt"]] * n_seq)
+    assert first == [q["first"] for q in sv["sequences"]]
+    last = first
+    for step in range(steps):
+        want = [q["steps"][step] for q in sv["sequences"]]
+        _say(f"[gpu] batched speculation Qwen3-1.7B: verify step {step + 1}, M = {sum(1 + len(x['drafts']) for x in want)}")
+        out = b.verify(last, [x["drafts"] for x in want])
+        r0 = 0
+        for i, x in enumerate(want):
+            rows = 1 + len(x["drafts"])
+            assert OD.sha_u16(_bits(b.logits_rows[r0:r0 + rows])) == x["rows_sha"], \
+                f"sequence {i} step {step + 1}: verify logits differ from the oracle"
+            assert out[i] == (x["accepted"], x["next"]), f"sequence {i} step {step + 1}"
+            r0 += rows
+        last = [o[1] for o in out]
+    for i, q in enumerate(sv["sequences"]):
+        assert b.cache_len[i] == len(fx["prompt"]) + len(q["emitted"]) - 1
