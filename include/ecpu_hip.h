@@ -390,6 +390,30 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
                                  const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *block_ids,
                                  const uint16_t *gate, const int32_t *step, uint16_t *out);
 
+typedef struct {
+    size_t rows;      /* activation rows: 1 (one decode token) */
+    size_t N;         /* rows of W (with swiglu: gate rows then as many up rows) */
+    size_t K;         /* hidden size, a multiple of 256 up to 16384 */
+    float eps;        /* GemmaRMSNorm eps */
+    int swiglu;       /* 1: out[i] = bf16(bf16(silu(gate_i)) * up_i), N / 2 outputs */
+} ekernel_norm_linear_desc_t;
+
+/* The residual add + GemmaRMSNorm before a Linear of TransformerBlock
+ * (model.py:63-69: input_layernorm before q/k/v, post_attention_layernorm
+ * before gate/up) and that W4A16 g128 Linear, for one token in one launch:
+ * h = bf16(x + residual) (x when residual is NULL), residual_out = h (when
+ * not NULL), a = GemmaRMSNorm(h) as ekernel_rmsnorm_gemma_bf16 computes it,
+ * out = a @ W^T as ekernel_linear_w4a16g128_bf16 computes it; with swiglu
+ * the SwiGLU product F.silu(gate) * up of the two halves of W
+ * (layers.py:188-193) as ekernel_silu_mul_bf16 computes it.  Bit-identical
+ * to those calls in sequence.  All pointers 16-byte aligned (scales 4);
+ * residual_out and out must not overlap x or residual.  No counterpart in
+ * the reference, which runs these steps one after another. */
+int ekernel_rmsnorm_linear_w4a16g128_bf16(const ekernel_norm_linear_desc_t *desc, const uint16_t *x,
+                                          const uint16_t *residual, const uint16_t *norm_weight,
+                                          uint16_t *residual_out, const uint8_t *W, const float *scales,
+                                          uint16_t *out);
+
 /* One decode row (S = 1) of FullAttention.forward (attention.py:82-139) in
  * one launch: ekernel_qk_norm_rope_bf16 followed by
  * ekernel_attention_exact_bf16 with the gate inside qg (gate_row_stride

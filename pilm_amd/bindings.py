@@ -47,6 +47,7 @@ _OPTIONAL_KERNEL_SYMBOLS = [
     "ekernel_qk_norm_rope_bf16",
     "ekernel_attention_exact_bf16",
     "ekernel_decode_attention_bf16",
+    "ekernel_rmsnorm_linear_w4a16g128_bf16",
     "ekernel_silu_mul_bf16",
     "ekernel_greedy_step_bf16",
 ]
@@ -163,6 +164,13 @@ class EkernelRmsnormDesc(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_size_t), ("hidden", ctypes.c_size_t), ("eps", ctypes.c_float)]
 
 
+class EkernelNormLinearDesc(ctypes.Structure):
+    """ekernel_norm_linear_desc_t (GemmaRMSNorm, layers.py:130-147, fused into
+    the following W4A16 g128 Linear; with swiglu the SwiGLU product too)."""
+    _fields_ = [("rows", ctypes.c_size_t), ("N", ctypes.c_size_t), ("K", ctypes.c_size_t),
+                ("eps", ctypes.c_float), ("swiglu", ctypes.c_int)]
+
+
 class EkernelQkRopeDesc(ctypes.Structure):
     """ekernel_qk_rope_desc_t (attention.py:82-97)."""
     _fields_ = [(n, ctypes.c_size_t) for n in ("S", "n_heads", "n_kv_heads", "head_dim", "rot_dim", "q_stride",
@@ -256,6 +264,9 @@ def _configure(lib):
         lib.ekernel_attention_exact_bf16.restype = ctypes.c_int
         lib.ekernel_decode_attention_bf16.argtypes = [ctypes.POINTER(EkernelQkRopeDesc)] + [ctypes.c_void_p] * 12
         lib.ekernel_decode_attention_bf16.restype = ctypes.c_int
+        lib.ekernel_rmsnorm_linear_w4a16g128_bf16.argtypes = [ctypes.POINTER(EkernelNormLinearDesc)] + \
+            [ctypes.c_void_p] * 7
+        lib.ekernel_rmsnorm_linear_w4a16g128_bf16.restype = ctypes.c_int
         lib.ekernel_silu_mul_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
                                               ctypes.c_size_t, ctypes.c_void_p]
         lib.ekernel_silu_mul_bf16.restype = ctypes.c_int

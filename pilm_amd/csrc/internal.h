@@ -78,6 +78,13 @@ int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
 int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
                    hipStream_t st, const char *fn);
 
+// One activation row of W4A16 g128 through a GemmaRMSNorm prologue
+// (h = x + res, res_out = h, a = norm(h)) computed by every workgroup, then
+// the group-quad GEMV of a; with swiglu, W = [gate; up] (N/2 rows each) and
+// C[i] = bf16(bf16(silu(gate_i)) * up_i).  K a multiple of 256; enqueued on st.
+int run_gq_norm(bool swiglu, size_t N, size_t K, const uint16_t *x, const uint16_t *res, const uint16_t *norm_w,
+                uint16_t *res_out, float eps, const uint8_t *W, const float *S, uint16_t *C, hipStream_t st);
+
 // Fused W4 SwiGLU gate/up pass (one launch) for M = 1; ECPU_ERR_UNSUPPORTED
 // when the shape or alignment does not suit the stripe kernel.
 int run_swiglu_gate_up(size_t I, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *hidden,

@@ -60,6 +60,54 @@ static int linear_common(int fmt, const ekernel_linear_w8a32_desc_t *desc, const
     return run_linear(fmt, M, N, K, A, (const uint8_t *)W, S, C, fn);
 }
 
+// ------------------------------------------------------------ norm + linear
+static bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
+    if (!a || !b) return false;
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + bn && y < x + an;
+}
+
+extern "C" int ekernel_rmsnorm_linear_w4a16g128_bf16(const ekernel_norm_linear_desc_t *desc, const uint16_t *x,
+                                                     const uint16_t *residual, const uint16_t *norm_weight,
+                                                     uint16_t *residual_out, const uint8_t *W, const float *scales,
+                                                     uint16_t *out) {
+    static const char *fn = "ekernel_rmsnorm_linear_w4a16g128_bf16";
+    if (!desc || !x || !norm_weight || !W || !scales || !out) return fail(ECPU_ERR_PARAM, "%s: NULL argument", fn);
+    const size_t M = desc->rows, N = desc->N, K = desc->K;
+    if (M == 0 || N == 0) return ECPU_OK;
+    if (M != 1) return fail(ECPU_ERR_UNSUPPORTED, "%s: one activation row per call (rows = %zu)", fn, M);
+    if (K == 0 || K % 256 || K > 16384)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: K = %zu (a multiple of 256 up to 16384)", fn, K);
+    if (N >= ((size_t)1 << 31)) return fail(ECPU_ERR_PARAM, "%s: N must be < 2^31", fn);
+    if (desc->swiglu && N % 16)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: SwiGLU needs N (gate + up rows) a multiple of 16, got %zu", fn, N);
+    const uintptr_t al = (uintptr_t)x | (uintptr_t)residual | (uintptr_t)norm_weight | (uintptr_t)residual_out |
+                         (uintptr_t)W;
+    if ((al & 15) || ((uintptr_t)scales & 3))
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: x, residual, norm weight, residual_out and W must be 16-byte aligned",
+                    fn);
+    const size_t row = K * 2, n_out = desc->swiglu ? N / 2 : N;
+    // every workgroup reads x and residual while workgroup 0 writes
+    // residual_out and all write out
+    if (overlaps(residual_out, row, x, row) || overlaps(residual_out, row, residual, row) ||
+        overlaps(out, n_out * 2, x, row) || overlaps(out, n_out * 2, residual, row) ||
+        overlaps(out, n_out * 2, residual_out, row))
+        return fail(ECPU_ERR_PARAM, "%s: out / residual_out overlap the inputs", fn);
+    int rc;
+    if ((rc = check_buf(x, row, "x", fn)) != ECPU_OK) return rc;
+    if (residual && (rc = check_buf(residual, row, "residual", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(norm_weight, row, "norm_weight", fn)) != ECPU_OK) return rc;
+    if (residual_out && (rc = check_buf(residual_out, row, "residual_out", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(W, N * (K / 2), "W", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(scales, N * (K / 128) * 4, "scales", fn)) != ECPU_OK) return rc;
+    if ((rc = check_buf(out, n_out * 2, "out", fn)) != ECPU_OK) return rc;
+    rc = run_gq_norm(desc->swiglu != 0, N, K, x, residual, norm_weight, residual_out, desc->eps, W, scales, out,
+                     current_stream());
+    if (rc == ECPU_ERR_DEVICE) return fail(rc, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+    if (rc != ECPU_OK) return fail(rc, "%s: shape does not fit the kernel (N = %zu, K = %zu)", fn, N, K);
+    return check_launch(fn);
+}
+
 // ------------------------------------------------------------ f32 GEMM
 // kernels.c:396-435: 8-lane FMA dot when !transpose_a && transpose_b (and the
 // caller's isa is AVX2 or above), otherwise a sequential FMA loop.

@@ -31,6 +31,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "cpu_order.h"
 #include "gemv_device.h"
 #include "internal.h"
 
@@ -1588,11 +1589,26 @@ int run_rbc(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t 
 // waves without changing a bit.  The row scales of the tile are copied to
 // LDS at the start (DMA, behind the activations), so the fold waits for
 // nothing.
-template <int FMT, int MT, int D, int P>
+// Optional GemmaRMSNorm prologue of the group-quad kernel (one activation
+// row): h = bf16(x + res) (or x), res_out = h (workgroup 0), and the
+// activation row a = bf16(bf16(w + 1) * bf16(h * r)), r = 1 / sqrt(mean(h^2)
+// + eps) in torch's CPU order, computed by every workgroup into its LDS copy
+// of the activations.
+struct GqNorm {
+    const uint16_t *x = nullptr;
+    const uint16_t *res = nullptr;
+    const uint16_t *w = nullptr;
+    uint16_t *res_out = nullptr;
+    float eps = 0.0f;
+};
+constexpr int kGqNormChunks = 4;   // eight-element chunks of the row per thread
+
+template <int FMT, int MT, int D, int P, bool NORM = false, bool SW = false>
 __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restrict__ A, const uint8_t *__restrict__ W,
                                                      const float *__restrict__ S, uint16_t *__restrict__ C, int N,
-                                                     int K, int m0) {
+                                                     int K, int m0, GqNorm na) {
     using Q = QuadFmt<F_W4ROW>;
+    static_assert(!(NORM || SW) || MT == 1, "norm prologue / SwiGLU epilogue: one activation row");
     constexpr int GS = FMT == F_W4G128 ? 128 : 32;   // group size
     constexpr int GPS = 256 / GS;                    // groups per stripe: 2 or 8
     constexpr int WPG = 16 / GPS;                    // lane words per group: 8 or 2
@@ -1601,6 +1617,14 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
     const int lane = threadIdx.x & 63;
     const int r = lane >> 2, c = lane & 3, par = c >> 1;
     const int row0 = blockIdx.x * 16;
+    // weight row of tile row rr: SW pairs gate rows 8t..8t+7 (tile rows 0-7)
+    // with their up rows N/2 + 8t.. (tile rows 8-15)
+    auto wrow = [&](int rr) -> size_t {
+        if constexpr (SW)
+            return rr < 8 ? (size_t)blockIdx.x * 8 + rr : (size_t)(N / 2) + blockIdx.x * 8 + (rr - 8);
+        else
+            return (size_t)min(row0 + rr, N - 1);
+    };
     const size_t row_bytes = (size_t)K / 2;
     const int ns = (int)(row_bytes / kStripe);
     const int G = K / GS;
@@ -1612,19 +1636,22 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
     float *scl = (float *)(act + (size_t)MT * rdw * 4);   // [16][G]
     float *blk = scl + 16 * G;                             // [MT][16][G]
 
-    // Activation rows (16-byte DMA, 256 dwords per instruction) and the
-    // tile's scales (4-byte DMA, 64 per instruction), dealt round-robin.
+    // Activation rows (16-byte DMA, 256 dwords per instruction; NORM: computed
+    // below instead) and the tile's scales (4-byte DMA, 64 per instruction),
+    // dealt round-robin.
     {
         int issued = 0;
-        const int total = MT * rdw;
-        const uint32_t *a = (const uint32_t *)A + (size_t)m0 * rdw;
+        if constexpr (!NORM) {
+            const int total = MT * rdw;
+            const uint32_t *a = (const uint32_t *)A + (size_t)m0 * rdw;
 #pragma unroll 1
-        for (int q = wave; q * 256 < total; q += P) {
-            const int g = q * 256 + 4 * lane;
-            if (g < total)
-                __builtin_amdgcn_global_load_lds((const void *)(a + g), (lds_void *)(act + (size_t)q * 1024), 16, 0,
-                                                 0);
-            if ((++issued & 15) == 0) wait_vmcnt<16>();
+            for (int q = wave; q * 256 < total; q += P) {
+                const int g = q * 256 + 4 * lane;
+                if (g < total)
+                    __builtin_amdgcn_global_load_lds((const void *)(a + g), (lds_void *)(act + (size_t)q * 1024), 16,
+                                                     0, 0);
+                if ((++issued & 15) == 0) wait_vmcnt<16>();
+            }
         }
         const int nscl = 16 * G;
 #pragma unroll 1
@@ -1632,8 +1659,8 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
             const int i = q * 64 + lane;
             if (i < nscl) {
                 const int rr = i / G, g = i - rr * G;
-                __builtin_amdgcn_global_load_lds((const void *)(S + (size_t)min(row0 + rr, N - 1) * G + g),
-                                                 (lds_void *)(scl + q * 64), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)(S + wrow(rr) * G + g), (lds_void *)(scl + q * 64), 4,
+                                                 0, 0);
             }
             if ((++issued & 15) == 0) wait_vmcnt<16>();
         }
@@ -1645,7 +1672,7 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
     for (int i = 0; i < 2; ++i) {
         const int rr = 8 * i + (lane >> 3);
         const int q = (lane & 7) ^ ((rr >> 1) & 7);
-        src[i] = W + (size_t)min(row0 + rr, N - 1) * row_bytes + q * 16;
+        src[i] = W + wrow(rr) * row_bytes + q * 16;
     }
     unsigned char *ring = lds + (size_t)wave * D * kQuadSlotBytes;
     auto issue = [&](int t) {   // t: index within this wave's range
@@ -1658,6 +1685,68 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
 #pragma unroll
     for (int t = 0; t < D - 2; ++t)
         if (t < nsw) issue(t);
+    if constexpr (NORM) {
+        // the row, its residual and the norm weight in 16-byte chunks (the
+        // first stripes are already on their way), then the norm into act
+        float *xs = blk + 16 * G;                  // [K + 4]: h as fp32, then r
+        const int nc = K / 8, t = threadIdx.x;
+        u32x4 xv[kGqNormChunks], rv[kGqNormChunks], wv[kGqNormChunks];
+#pragma unroll
+        for (int u = 0; u < kGqNormChunks; ++u) {
+            const int ch = t + 64 * P * u;
+            if (ch < nc) {
+                xv[u] = ((const u32x4 *)na.x)[ch];
+                if (na.res) rv[u] = ((const u32x4 *)na.res)[ch];
+                wv[u] = ((const u32x4 *)na.w)[ch];
+            }
+        }
+        float h[kGqNormChunks][8];
+#pragma unroll
+        for (int u = 0; u < kGqNormChunks; ++u) {
+            const int ch = t + 64 * P * u;
+            if (ch < nc) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float lo = bf16_lo(xv[u][e]), hi = bf16_hi(xv[u][e]);
+                    if (na.res) {
+                        lo = bfr(lo + bf16_lo(rv[u][e]));
+                        hi = bfr(hi + bf16_hi(rv[u][e]));
+                    }
+                    h[u][2 * e] = lo;
+                    h[u][2 * e + 1] = hi;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xs[8 * ch + e] = h[u][e];
+                if (na.res_out && blockIdx.x == 0) {
+                    u32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        o[e] = (uint32_t)f32_to_bf16(h[u][2 * e]) | ((uint32_t)f32_to_bf16(h[u][2 * e + 1]) << 16);
+                    ((u32x4 *)na.res_out)[ch] = o;
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float rs = wave_row_rsqrt(xs, K, na.eps);
+            if (lane == 0) xs[K] = rs;
+        }
+        __syncthreads();
+        const float rs = xs[K];
+#pragma unroll
+        for (int u = 0; u < kGqNormChunks; ++u) {
+            const int ch = t + 64 * P * u;
+            if (ch < nc) {
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    o[e] = (uint32_t)gemma_out(h[u][2 * e], rs, (uint16_t)(wv[u][e] & 0xFFFFu)) |
+                           ((uint32_t)gemma_out(h[u][2 * e + 1], rs, (uint16_t)(wv[u][e] >> 16)) << 16);
+                ((u32x4 *)act)[ch] = o;
+            }
+        }
+        __syncthreads();                           // the activation row is in
+    }
     if (nsw >= D - 2)
         wait_vmcnt<2 * (D - 2)>();   // activation and scale copies, older than the stripes
     else
@@ -1764,6 +1853,24 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
 
     // Fold: row r's blocks in group order (kernels.c:1141-1150), by lane 4r of wave 0.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (SW) {
+        // gate row r < 8 and up row r + 8 (lane 4r + 32): C[8t + r] =
+        // bf16(bf16(silu(g)) * u), F.silu(gate(x)) * up(x) on the bf16 outputs
+        if (wave != 0) return;
+        float a = 0.0f;
+        if (c == 0) {
+            const float *sr = scl + r * G, *br = blk + r * G;
+#pragma unroll 8
+            for (int g = 0; g < G; ++g) a = __builtin_fmaf(br[g], sr[g], a);
+        }
+        const float v = bfr(a);
+        const float u = __shfl(v, lane + 32);
+        if (c == 0 && r < 8) {
+            const float sl = bfr(__fdiv_rn(v, 1.0f + sleef_expf(-v)));
+            C[(size_t)blockIdx.x * 8 + r] = f32_to_bf16(sl * u);
+        }
+        return;
+    }
     const int n = row0 + r;
     if (wave != 0 || c != 0 || n >= N) return;
     const float *sr = scl + r * G;
@@ -1777,10 +1884,11 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
     }
 }
 
-template <int FMT, int MT, int D, int P>
+template <int FMT, int MT, int D, int P, bool NORM = false>
 size_t gq_lds_bytes(int K) {
     const size_t G = (size_t)K / (FMT == F_W4G128 ? 128 : 32);
-    return (size_t)P * D * kQuadSlotBytes + (size_t)MT * K * 2 + 16 * G * 4 + (size_t)MT * 16 * G * 4;
+    return (size_t)P * D * kQuadSlotBytes + (size_t)MT * K * 2 + 16 * G * 4 + (size_t)MT * 16 * G * 4 +
+           (NORM ? ((size_t)K + 4) * 4 : 0);
 }
 
 template <int FMT, int MT, int D, int P>
@@ -1795,9 +1903,30 @@ int launch_gq_one(int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
     const size_t lds = gq_lds_bytes<FMT, MT, D, P>(K);
     if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
-    gemv_gq_kernel<FMT, MT, D, P><<<ntiles, 64 * P, lds, st>>>(A, W, S, C, N, K, m0);
+    gemv_gq_kernel<FMT, MT, D, P><<<ntiles, 64 * P, lds, st>>>(A, W, S, C, N, K, m0, GqNorm{});
     return ECPU_OK;
 }
+
+// One activation row through a GemmaRMSNorm prologue (and with sw, the
+// SwiGLU epilogue over gate/up row pairs): eight waves, rings of four slots,
+// as run_group_quad takes for one row.
+template <bool SW>
+static int launch_gq_norm(int ntiles, hipStream_t st, const uint8_t *W, const float *S, uint16_t *C, int N, int K,
+                          const GqNorm &na) {
+    constexpr int D = 4, P = 8;
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_gq_kernel<F_W4G128, 1, D, P, true, SW>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = gq_lds_bytes<F_W4G128, 1, D, P, true>(K);
+    if (lds > kRowMaxLds) return ECPU_ERR_UNSUPPORTED;
+    gemv_gq_kernel<F_W4G128, 1, D, P, true, SW><<<ntiles, 64 * P, lds, st>>>(nullptr, W, S, C, N, K, 0, na);
+    return ECPU_OK;
+}
+
 
 template <int FMT, int D, int P>
 int launch_gq_mt(int mt, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S,
@@ -2084,6 +2213,22 @@ int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16
 }
 
 }  // namespace
+
+int run_gq_norm(bool swiglu, size_t N, size_t K, const uint16_t *x, const uint16_t *res, const uint16_t *norm_w,
+                uint16_t *res_out, float eps, const uint8_t *W, const float *S, uint16_t *C, hipStream_t st) {
+    GqNorm na;
+    na.x = x;
+    na.res = res;
+    na.w = norm_w;
+    na.res_out = res_out;
+    na.eps = eps;
+    if (K == 0 || K % 256 || K / 8 > (size_t)kGqNormChunks * 64 * 8) return ECPU_ERR_UNSUPPORTED;
+    if (swiglu) {
+        if (N % 16) return ECPU_ERR_UNSUPPORTED;
+        return launch_gq_norm<true>((int)(N / 16), st, W, S, C, (int)N, (int)K, na);
+    }
+    return launch_gq_norm<false>((int)((N + 15) / 16), st, W, S, C, (int)N, (int)K, na);
+}
 
 // Per-row formats on the stripe path: K a multiple of the stripe (128 int8
 // or 256 int4 weights), 16-byte aligned weights and activations.

@@ -178,6 +178,8 @@ class Qwen3Decoder:
         self.gu = torch.empty((S, 2 * I), **e)
         self.act = torch.empty((S, I), **e)
         self.mlp = torch.empty((S, H), **e)
+        # residual rows of the fused decode step, alternating (a launch reads one, writes the other)
+        self.res_pp = (torch.empty((1, H), **e), torch.empty((1, H), **e))
         self.logits = torch.empty((c.vocab,), **e)
         self.logits_rows = torch.empty((S, c.vocab), **e) if max_rows else None
         self.state = torch.zeros(4, dtype=torch.int32, device=dev)      # pos0, cache_len, count
@@ -188,6 +190,8 @@ class Qwen3Decoder:
         self._descs = {}
         # the one-launch decode attention serves 64- and 128-wide heads, 1, 2 or 4 q heads per kv head
         self.fused_decode = c.head_dim in (64, 128) and c.heads // c.kv_heads in (1, 2, 4)
+        # decode tokens: each GemmaRMSNorm inside the launch of the linear after it, SwiGLU inside gate_up
+        self.fused_norm = self.fused_decode and c.hidden % 256 == 0 and c.hidden <= 16384
 
     # ---------------------------------------------------------------- calls
     def _check(self, rc: int, name: str) -> None:
@@ -211,6 +215,48 @@ class Qwen3Decoder:
         d = self._desc(("norm", m), lambda: abi.EkernelRmsnormDesc(m, self.cfg.hidden, self.cfg.eps))
         self._check(self.lib.ekernel_rmsnorm_gemma_bf16(ctypes.byref(d), _vp(x), _vp(res), _vp(weight), _vp(out),
                                                         _vp(res_out)), "ekernel_rmsnorm_gemma_bf16")
+
+    def _norm_linear(self, x, res, weight, res_out, wq, out, swiglu):
+        q, s = wq
+        d = self._desc(("normlin", q.shape[0], swiglu),
+                       lambda: abi.EkernelNormLinearDesc(1, q.shape[0], self.cfg.hidden, self.cfg.eps, int(swiglu)))
+        self._check(self.lib.ekernel_rmsnorm_linear_w4a16g128_bf16(ctypes.byref(d), _vp(x), _vp(res), _vp(weight),
+                                                                  _vp(res_out), _vp(q), _vp(s), _vp(out)),
+                    "ekernel_rmsnorm_linear_w4a16g128_bf16")
+
+    def _forward_decode(self):
+        """One decode token (self.x[0]) with five launches per layer: input
+        norm + qkv, attention, o, post-attention norm + gate_up + SwiGLU,
+        down; the residual rows alternate between two buffers."""
+        c, L = self.cfg, self.lib
+        D, Hq, Hkv = c.head_dim, c.heads, c.kv_heads
+        qkv_p = self.qkv.data_ptr()
+        k_off, v_off = 2 * Hq * D * 2, (2 * Hq * D + Hkv * D) * 2
+        rope = self._desc(("rope", 1), lambda: abi.EkernelQkRopeDesc(
+            1, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, 0, self.max_pos, c.block_size, self.pool,
+            self.block_ids.numel(), c.eps))
+        r0, r1 = self.res_pp
+        x1, res_prev = self.x[:1], None
+        for li, Lw in enumerate(self.w.layers):
+            if li == 0:
+                self._norm_linear(x1, None, Lw["in_norm"], None, Lw["qkv"], self.qkv[:1], False)
+                res_in = x1
+            else:
+                self._norm_linear(self.mlp[:1], res_prev, Lw["in_norm"], r0, Lw["qkv"], self.qkv[:1], False)
+                res_in = r0
+            self._check(L.ekernel_decode_attention_bf16(
+                ctypes.byref(rope), ctypes.c_void_p(qkv_p), ctypes.c_void_p(qkv_p + k_off),
+                ctypes.c_void_p(qkv_p + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos), _vp(self.sin),
+                _vp(self.state), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(self.block_ids),
+                _vp(self.attn)), "ekernel_decode_attention_bf16")
+            self._linear(self.attn[:1], Lw["o"], self.o[:1], 1)
+            self._norm_linear(self.o[:1], res_in, Lw["post_norm"], r1, Lw["gate_up"], self.act[:1], True)
+            self._linear(self.act[:1], Lw["down"], self.mlp[:1], 1)
+            res_prev = r1
+        self._norm(self.mlp[:1], res_prev, self.w.norm, self.h, None, 1)
+        self._linear(self.h[:1], self.w.lm_head, self.logits.view(1, -1), 1)
+        self._check(L.ekernel_greedy_step_bf16(_vp(self.logits), c.vocab, _vp(self.state), _vp(self.tokens),
+                                               self.max_new, _vp(self.next_id)), "ekernel_greedy_step_bf16")
 
     def _forward(self, m: int, with_logits: bool, groups=None):
         """The model over the m tokens in self.x.  groups None: one sequence at
@@ -307,7 +353,10 @@ class Qwen3Decoder:
         """One token: embedding of the last generated id, the model, lm_head,
         argmax; advances the state word."""
         torch.index_select(self.w.embed, 0, self.next_id, out=self.x[:1])
-        self._forward(1, with_logits=True)
+        if self.fused_norm:
+            self._forward_decode()
+        else:
+            self._forward(1, with_logits=True)
 
     def capture(self) -> None:
         """Capture decode_step into a HIP graph (the state word makes each

@@ -76,6 +76,8 @@ def test_descriptor_layout_matches_reference():
     assert abi.EkernelRmsnormDesc.eps.offset == 16 and ctypes.sizeof(abi.EkernelRmsnormDesc) == 24
     assert abi.EkernelQkRopeDesc.eps.offset == 96 and ctypes.sizeof(abi.EkernelQkRopeDesc) == 104
     assert ctypes.sizeof(abi.EkernelAttentionExactDesc) == 80
+    assert abi.EkernelNormLinearDesc.eps.offset == 24 and abi.EkernelNormLinearDesc.swiglu.offset == 28
+    assert ctypes.sizeof(abi.EkernelNormLinearDesc) == 32
 
 
 def test_missing_symbol_fails_loudly(tmp_path, monkeypatch):

@@ -118,6 +118,75 @@ def test_rmsnorm_unaligned_rows(lib, dev):
     assert np.array_equal(_bits(out), want) and np.array_equal(_bits(res_out), want_res)
 
 
+# ----------------------------------------------------- norm + W4A16 g128 linear
+
+@pytest.mark.parametrize("N,K,swiglu,with_res", [(6144, 2048, False, True), (12288, 2048, True, True),
+                                                 (1536, 256, False, False), (1024, 256, True, True),
+                                                 (10240, 4096, False, True), (24576, 4096, True, True),
+                                                 (2048, 2048, False, False), (48, 512, True, False)])
+def test_rmsnorm_linear_fused(lib, dev, N, K, swiglu, with_res):
+    """ekernel_rmsnorm_linear_w4a16g128_bf16 against the oracle's GemmaRMSNorm,
+    W4A16 g128 linear and (swiglu) F.silu(gate) * up, bit for bit: Qwen3-1.7B
+    and 8B q/k/v and gate/up shapes, the two-layer model's, and small ones."""
+    import ctypes
+    from oracle import oracle as O
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(N + K + swiglu)
+    x, r, nw = _rand16(rng, (1, K), 3.0), _rand16(rng, (1, K)), _rand16(rng, (K,), 0.02)
+    q = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = (rng.random((N, K // 128)) * 0.019 + 0.001).astype(np.float32)
+    a, h = OD.rmsnorm_gemma_bf16(x, r if with_res else None, nw, 1e-6)
+    y = O.linear_w4a16g_bf16(a, q, sc, 128)
+    if swiglu:
+        half = N // 2
+        want = OD.silu_mul_bf16(np.ascontiguousarray(y[:, :half]), np.ascontiguousarray(y[:, half:]), 1, half, half)
+    else:
+        want = y
+    xd, rd, nwd = _dev16(x, dev), _dev16(r, dev), _dev16(nw, dev)
+    qd, sd = torch.from_numpy(q).to(dev), torch.from_numpy(sc).to(dev)
+    out = torch.empty((1, N // 2 if swiglu else N), dtype=torch.bfloat16, device=dev)
+    res_out = torch.empty((1, K), dtype=torch.bfloat16, device=dev)
+    _say(f"[gpu] rmsnorm + linear N={N} K={K} swiglu={swiglu} residual={with_res}")
+    _bind()
+    d = abi.EkernelNormLinearDesc(1, N, K, 1e-6, int(swiglu))
+    rc = lib.ekernel_rmsnorm_linear_w4a16g128_bf16(ctypes.byref(d), _vp(xd), _vp(rd if with_res else None), _vp(nwd),
+                                                   _vp(res_out if with_res else None), _vp(qd), _vp(sd), _vp(out))
+    assert rc == 0, abi.last_error()
+    got = _bits(out)
+    bad = np.argwhere(got != want.reshape(got.shape))
+    assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()}"
+    if with_res:
+        assert np.array_equal(_bits(res_out), h)
+
+
+def test_rmsnorm_linear_fused_refuses(lib, dev):
+    """Two rows, K not a multiple of 256, misaligned rows and outputs that
+    overlap the inputs are refused before any launch."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    buf = torch.zeros(1 << 20, dtype=torch.bfloat16, device=dev)
+    q = torch.zeros((64, 1024), dtype=torch.uint8, device=dev)
+    sc = torch.ones((64, 16), dtype=torch.float32, device=dev)
+    _bind()
+    p = buf.data_ptr()
+
+    def call(rows, N, K, x, res, res_out, out, swiglu=0):
+        d = abi.EkernelNormLinearDesc(rows, N, K, 1e-6, swiglu)
+        return lib.ekernel_rmsnorm_linear_w4a16g128_bf16(ctypes.byref(d), ctypes.c_void_p(x),
+                                                         ctypes.c_void_p(res) if res else None,
+                                                         ctypes.c_void_p(p + 65536),
+                                                         ctypes.c_void_p(res_out) if res_out else None, _vp(q),
+                                                         _vp(sc), ctypes.c_void_p(out))
+    assert call(1, 64, 2048, p, p + 8192, p + 16384, p + 32768) == 0
+    assert call(2, 64, 2048, p, p + 8192, p + 16384, p + 32768) == abi.ECPU_ERR_UNSUPPORTED
+    assert call(1, 64, 2000, p, p + 8192, p + 16384, p + 32768) == abi.ECPU_ERR_UNSUPPORTED
+    assert call(1, 64, 2048, p + 2, p + 8192, p + 16384, p + 32768) == abi.ECPU_ERR_UNSUPPORTED
+    assert call(1, 64, 2048, p, p + 8192, p + 8192, p + 32768) == abi.ECPU_ERR_PARAM       # residual_out = residual
+    assert call(1, 64, 2048, p, p + 8192, p + 16384, p + 1024) == abi.ECPU_ERR_PARAM       # out inside x
+    assert call(1, 24, 2048, p, p + 8192, p + 16384, p + 32768, swiglu=1) == abi.ECPU_ERR_UNSUPPORTED
+    torch.cuda.synchronize()
+
+
 # ----------------------------------------------------- q/k norm + rope + attention
 
 def _attn_case(rng, S, H, Hkv, D, pos0, bs=16, spare=3):
@@ -370,9 +439,9 @@ def test_decoder_tiny_matches_reference(dev):
     assert dec2.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
     # a second sequence on the same decoder (graph already captured) starts clean
     assert dec2.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
-    _say("[gpu] decoder, two-layer model: the two-call attention path")
+    _say("[gpu] decoder, two-layer model: norm, attention and SwiGLU as separate launches")
     dec3 = Q.Qwen3Decoder(w, max_positions=dec.max_pos, max_new_tokens=dec.max_new)
-    dec3.fused_decode = False
+    dec3.fused_decode = dec3.fused_norm = False
     assert dec3.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
 
 
