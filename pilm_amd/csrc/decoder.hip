@@ -443,18 +443,19 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
 }
 
 // ---- one decode row: q/k norm + rope + cache write + attention ---------------
-// The steps of qk_rope_kernel and attn_exact_kernel for S = 1 in one launch,
-// one 512-thread workgroup per kv head: waves 0 .. rep-1 normalize and rotate
-// the rep q heads that read this kv head, wave rep the k head (and write the
-// k and v rows into the cache).  The scores are computed once per kv head, one
-// position per thread, the new position from the k row just made.  The value
-// rows are staged whole in LDS (the new one from registers), and thread
-// (chain k, column c), c fastest, sums P.V for every head of the kv head, so
-// a wave reads one value row contiguously and each weight by broadcast.
+// The steps of qk_rope_kernel and attn_exact_kernel for S = 1 in one launch.
+// A 512-thread workgroup serves HPW of the rep q heads that read one kv head
+// (grid: kv heads x rep / HPW): waves 0 .. HPW-1 normalize and rotate those q
+// heads, wave HPW the k head (the first workgroup of the kv head also writes
+// the k and v rows into the cache).  Key rows come by DMA into LDS, their
+// 16-byte chunks XOR-swizzled, the new position's from registers; scores run
+// one position per thread.  The value rows follow into the same LDS, and
+// thread (chain k, column c), c fastest, sums P.V for the workgroup's heads,
+// so a wave reads one value row contiguously and each weight by broadcast.
 // Every sum keeps the order of the two-kernel path above.
 constexpr int kDecodeThreads = 512;
 
-template <int D, int REP>
+template <int D, int REP, int HPW>
 __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
     const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, const float *__restrict__ cos_t,
@@ -465,14 +466,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     constexpr int kPer = D / 64;          // elements per lane of one head
     constexpr int nthreads = kDecodeThreads;
     constexpr int rep = REP;              // q heads per kv head (H / Hkv)
+    constexpr int hpw = HPW;              // of them, heads of this workgroup: h0 .. h0 + hpw - 1
+    static_assert(REP % HPW == 0, "heads per workgroup divide the heads per kv head");
     extern __shared__ float lds[];
     const int kh = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int h0 = kh * rep + blockIdx.y * hpw;
+    const bool writer = blockIdx.y == 0;  // the workgroup that stores the new cache rows
     const int scs = (max_len + 3) & ~3;
-    float *xn = lds;                                           // [rep + 1][D] normalized heads
-    float *qs = xn + (rep + 1) * D;                            // [rep][D] roped q
-    float *sc = qs + rep * D;                                  // [rep][scs]
-    float *part = sc + (size_t)rep * scs;                      // [rep][4][D] chain sums
-    int *bids = (int *)(part + rep * 4 * D);                   // [n_block_ids]
+    float *xn = lds;                                           // [hpw + 1][D] normalized heads
+    float *qs = xn + (hpw + 1) * D;                            // [hpw][D] roped q
+    float *sc = qs + hpw * D;                                  // [hpw][scs]
+    float *part = sc + (size_t)hpw * scs;                      // [hpw][4][D] chain sums
+    int *bids = (int *)(part + hpw * 4 * D);                   // [n_block_ids]
     uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [vcap][D]
 
     const int pos = step ? step[0] : pos0_host;
@@ -483,13 +488,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     const bool pos_ok = pos >= 0 && pos < max_len;
     for (int i = t; i < n_block_ids; i += nthreads) bids[i] = min(max(block_ids[i], 0), num_blocks - 1);
 
-    // the head this wave normalizes: q head kh * rep + wave, or the k head
-    const bool head_wave = wave <= rep;
-    const bool is_k = wave == rep;
+    // the head this wave normalizes: q head h0 + wave, or the k head
+    const bool head_wave = wave <= hpw;
+    const bool is_k = wave == hpw;
     float xr[kPer];
     uint16_t wr[kPer], vr[kPer], kb[kPer];
     if (head_wave) {
-        const uint16_t *src = is_k ? kin + (size_t)kh * D : qg + (size_t)(kh * rep + wave) * 2 * D;
+        const uint16_t *src = is_k ? kin + (size_t)kh * D : qg + (size_t)(h0 + wave) * 2 * D;
         const uint16_t *nw = is_k ? kw : qw;
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
@@ -519,7 +524,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
 #pragma unroll
     for (int it = 0; it < kGatePre; ++it) {
         const int o = t + nthreads * it;
-        gpre[it] = o < rep * D ? bf(qg[(size_t)(kh * rep + o / D) * 2 * D + D + o % D]) : 0.0f;
+        gpre[it] = o < hpw * D ? bf(qg[(size_t)(h0 + o / D) * 2 * D + D + o % D]) : 0.0f;
     }
     if (head_wave) {
 #pragma unroll
@@ -565,7 +570,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const float *x = xn + wave * D;
         float *dst = qs + wave * D;       // roped q
-        const size_t crow = (is_k && pos_ok) ? row_of(pos) : 0;
+        const size_t crow = (is_k && pos_ok && writer) ? row_of(pos) : 0;
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
             const int i = lane + 64 * u;
@@ -578,7 +583,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
             const uint16_t ob = f32_to_bf16(o);
             if (!is_k) dst[i] = bf(ob);
             kb[u] = ob;
-            if (is_k && pos_ok) {
+            if (is_k && pos_ok && writer) {
                 k_cache[crow + i] = ob;
                 v_cache[crow + i] = vr[u];
             }
@@ -618,7 +623,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
                 ka[4 * u + 3] = c[3];
             }
 #pragma unroll
-            for (int r = 0; r < rep; ++r)
+            for (int r = 0; r < hpw; ++r)
                 sc[(size_t)r * scs + j] = bfr(bfr(score_dot<D>(qs + r * D, ka, naive)) * scale);
         }
     }
@@ -626,7 +631,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     stage(v_cache, 0, false);             // value rows arrive during the softmax
 
     // softmax per head: wave r
-    for (int r = wave; r < rep; r += nthreads / 64) {
+    for (int r = wave; r < hpw; r += nthreads / 64) {
         float *x = sc + (size_t)r * scs;
         float mx = -__builtin_inff();
         for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
@@ -669,9 +674,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
         const int i = base + t;
         const bool active = i < nthr;
         const int k = (i / D) & 3, c = i % D;
-        float acc[rep];
+        float acc[hpw];
 #pragma unroll
-        for (int r = 0; r < rep; ++r) acc[r] = 0.0f;
+        for (int r = 0; r < hpw; ++r) acc[r] = 0.0f;
         for (int j0 = 0; j0 < vis; j0 += vcap) {
             if (j0 > 0) {
                 __syncthreads();          // the previous rows have been read
@@ -692,7 +697,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
                 auto fma_row = [&](int j) {
                     const float vv = bf(vc[(size_t)j * D]);
 #pragma unroll
-                    for (int r = 0; r < rep; ++r) acc[r] = __builtin_fmaf(sc[(size_t)r * scs + j], vv, acc[r]);
+                    for (int r = 0; r < hpw; ++r) acc[r] = __builtin_fmaf(sc[(size_t)r * scs + j], vv, acc[r]);
                 };
                 if (naive) {
                     if (k == 0)
@@ -701,17 +706,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
                     int j = j0 + ((k - j0) & 3);
                     const int jm = min(j1, main_len);
                     for (; j + 28 < jm; j += 32) {
-                        float vv[8], wv[8][rep];
+                        float vv[8], wv[8][hpw];
 #pragma unroll
                         for (int u = 0; u < 8; ++u) {
                             vv[u] = bf(vc[(size_t)(j + 4 * u) * D]);
 #pragma unroll
-                            for (int r = 0; r < rep; ++r) wv[u][r] = sc[(size_t)r * scs + j + 4 * u];
+                            for (int r = 0; r < hpw; ++r) wv[u][r] = sc[(size_t)r * scs + j + 4 * u];
                         }
 #pragma unroll
                         for (int u = 0; u < 8; ++u)
 #pragma unroll
-                            for (int r = 0; r < rep; ++r) acc[r] = __builtin_fmaf(wv[u][r], vv[u], acc[r]);
+                            for (int r = 0; r < hpw; ++r) acc[r] = __builtin_fmaf(wv[u][r], vv[u], acc[r]);
                     }
                     for (; j < jm; j += 4) fma_row(j);
                     if (k == 0)
@@ -724,18 +729,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
             }
         }
         if (active)
-            for (int r = 0; r < rep; ++r) part[(size_t)r * 4 * D + i] = acc[r];
+            for (int r = 0; r < hpw; ++r) part[(size_t)r * 4 * D + i] = acc[r];
     }
     __syncthreads();
     // fold: output (head r, column c) for r * D + c = t + nthreads * it
-    for (int o = t, it = 0; o < rep * D; o += nthreads, ++it) {
+    for (int o = t, it = 0; o < hpw * D; o += nthreads, ++it) {
         const int r = o / D, c = o % D;
         const float *pp = part + (size_t)r * 4 * D + c;
         float v = naive ? pp[0] : ((pp[0] + pp[D]) + pp[2 * D]) + pp[3 * D];
         v = bfr(v);
-        const float g = it == 0 ? gpre[0] : it == 1 ? gpre[1] : bf(qg[(size_t)(kh * rep + r) * 2 * D + D + c]);
+        const float g = it == 0 ? gpre[0] : it == 1 ? gpre[1] : bf(qg[(size_t)(h0 + r) * 2 * D + D + c]);
         v = v * bfr(__fdiv_rn(1.0f, 1.0f + sleef_expf(-g)));
-        out[(size_t)(kh * rep + r) * D + c] = f32_to_bf16(v);
+        out[(size_t)(h0 + r) * D + c] = f32_to_bf16(v);
     }
 }
 
@@ -967,7 +972,12 @@ int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint
     const size_t max_len = d.n_block_ids * d.block_size;
     if (!step && (d.pos0 + 1 > d.max_positions || d.pos0 + 1 > max_len))
         return fail(ECPU_ERR_PARAM, "%s: position %zu beyond the tables", fn, d.pos0);
-    const size_t fixed = ((rep + 1) * D + rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * 4 * D +
+    // heads per workgroup: one (rep workgroups per kv head, each scoring its
+    // own q head with q held in registers; measured faster: Qwen3-1.7B decode
+    // 796 -> 848 tok/s), or all rep q heads of the kv head sharing the key
+    // rows' widening (PILM_DECODE_ATTN_SHARED=1)
+    const size_t hpw = env_int("PILM_DECODE_ATTN_SHARED", 0) == 1 ? rep : 1;
+    const size_t fixed = ((hpw + 1) * D + hpw * D + hpw * ((max_len + 3) & ~(size_t)3) + hpw * 4 * D +
                           ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
     const size_t budget = lds_limit();
     const size_t room = fixed < budget ? (budget - fixed) / (D * 2) : 0;
@@ -986,11 +996,17 @@ int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint
     if (rc != ECPU_OK) return rc;
     const float scale = (float)(1.0 / __builtin_sqrt((double)D));
     hipStream_t st = current_stream();
-#define PILM_DECODE_ATTN(DD, RR)                                                                                     \
-    decode_attn_kernel<DD, RR><<<(unsigned)d.n_kv_heads, kDecodeThreads, lds, st>>>(                                \
+    const dim3 grid((unsigned)d.n_kv_heads, (unsigned)(rep / hpw));
+#define PILM_DECODE_ATTN_H(DD, RR, HH)                                                                               \
+    decode_attn_kernel<DD, RR, HH><<<grid, kDecodeThreads, lds, st>>>(                                               \
         qg, k, v, q_norm_w, k_norm_w, cos_table, sin_table, (int)d.max_positions, step, (int)d.pos0, k_cache,       \
         v_cache, block_ids, (int)d.n_block_ids, (int)d.block_size, (int)d.num_blocks, (int)d.n_heads,              \
         (int)d.n_kv_heads, (int)d.rot_dim, d.eps, (int)max_len, (int)vcap, scale, out)
+#define PILM_DECODE_ATTN(DD, RR)                                                                                     \
+    do {                                                                                                             \
+        if (hpw == 1) PILM_DECODE_ATTN_H(DD, RR, 1);                                                                 \
+        else PILM_DECODE_ATTN_H(DD, RR, RR);                                                                         \
+    } while (0)
     if (D == 64) {
         if (rep == 1) PILM_DECODE_ATTN(64, 1);
         else if (rep == 2) PILM_DECODE_ATTN(64, 2);
@@ -1001,6 +1017,7 @@ int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint
         else PILM_DECODE_ATTN(128, 4);
     }
 #undef PILM_DECODE_ATTN
+#undef PILM_DECODE_ATTN_H
     return check_launch(fn);
 }
 

@@ -254,15 +254,18 @@ def test_qk_rope_then_attention(lib, dev, S, H, Hkv, D, pos0):
                                           (16, 8, 128, 3), (16, 8, 128, 7), (16, 8, 128, 64), (32, 8, 128, 2043),
                                           (4, 2, 128, 0), (8, 8, 64, 17), (16, 4, 128, 100), (16, 8, 128, 4000),
                                           (32, 8, 64, 515)])
-def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0):
+@pytest.mark.parametrize("shared", [False, True])
+def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0, shared, monkeypatch):
     """ekernel_decode_attention_bf16 (one launch) against the oracle's two
     steps: the same output bits and the same cache rows, with the position
     from the host and from the device state word.  Cases: lengths 1-4
     (torch's small-matrix kernel below 4), 8 and 65 (tails of the four- and
     eight-way sums), 1, 2 and 4 q heads per kv head, value rows staged in one
-    pass and in several (2044 and 4001 positions)."""
+    pass and in several (2044 and 4001 positions); one q head per workgroup
+    and (shared) all q heads of a kv head per workgroup."""
     import ctypes
     from pilm_amd import bindings as abi
+    monkeypatch.setenv("PILM_DECODE_ATTN_SHARED", "1" if shared else "0")
     rng = np.random.default_rng(pos0 * 31 + H + D)
     bs, S = 16, 1
     L, block_ids, kc, vc, qkv, qw, kw = _attn_case(rng, S, H, Hkv, D, pos0, bs)
