@@ -78,6 +78,15 @@ int run_rows(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
 int run_group_quad(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
                    hipStream_t st, const char *fn);
 
+// W8A16 GEMV of one activation row with the greedy argmax epilogue
+// (kernels.c:658-737), no logits written: part holds 2 * rows_argmax_tiles(N)
+// words, the ticket must be zero (it is left at zero); ECPU_ERR_UNSUPPORTED
+// when the shape or alignment does not suit the kernel (nothing launched).
+// Workgroups of the argmax GEMV: 64-row tiles, or at most 512 smaller ones.
+constexpr size_t rows_argmax_tiles(size_t N) { return (N + 63) / 64 > 512 ? (N + 63) / 64 : 512; }
+int run_rows_argmax(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint32_t *part,
+                    int *ticket, uint32_t *result, size_t *out_index, float *out_value, hipStream_t st);
+
 // One activation row of W4A16 g128 through a GemmaRMSNorm prologue
 // (h = x + res, res_out = h, a = norm(h)) computed by every workgroup, then
 // the group-quad GEMV of a; with swiglu, W = [gate; up] (N/2 rows each) and

@@ -156,18 +156,40 @@ int linear_argmax_core(size_t N, size_t K, const uint16_t *A, const uint8_t *W, 
                        uint32_t *part, uint32_t *result, int *ticket, bool clear_ticket, size_t *out_index,
                        float *out_value, bool index_on_device, bool value_on_device, const char *fn) {
     hipStream_t st = current_stream();
-    int rc = run_linear(F_W8A16, 1, N, K, A, W, S, logits, fn);
-    if (rc != ECPU_OK) return rc;
-    hipEvent_t ev0 = prof_begin(st);
     if (clear_ticket) clear_int_kernel<<<1, 64, 0, st>>>(ticket);
-    const uint32_t nblk = (uint32_t)std::min<size_t>(kArgMaxBlocks, (N + kArgStep - 1) / kArgStep);
-    const uint32_t per_block = (uint32_t)round_up((N + nblk - 1) / nblk, 8);
-    argmax_bf16_kernel<<<nblk, kArgThreads, 0, st>>>(logits, (uint32_t)N, per_block, part, ticket, result,
-                                                     index_on_device ? out_index : nullptr,
-                                                     value_on_device ? out_value : nullptr);
-    rc = check_launch(fn);
-    if (rc != ECPU_OK) return rc;
-    prof_end(ev0, st, "w8a16_argmax", 2.0 * (double)N, 0.0);
+    // The GEMV into logits, then the argmax kernel over them; with
+    // PILM_HIP_ARGMAX_EPILOGUE=1 the argmax as the GEMV's epilogue instead (no
+    // logits written), where the stripe kernel takes the shape.  Measured at
+    // the Qwen3 lm_head (151936 rows, MI355X): GEMV alone 54.3 / 117.8 us
+    // (K 2048 / 4096), GEMV + argmax kernel 55.2 / 118.4 us, epilogue 61.0 /
+    // 124.2 us -- every workgroup of the epilogue waits for its parked pair to
+    // reach the device-coherent level before taking its ticket.
+    hipEvent_t ev0 = prof_begin(st);
+    int rc = env_int("PILM_HIP_ARGMAX_EPILOGUE", 0) != 0
+                 ? run_rows_argmax(N, K, A, W, S, part, ticket, result, index_on_device ? out_index : nullptr,
+                                   value_on_device ? out_value : nullptr, st)
+                 : ECPU_ERR_UNSUPPORTED;
+    if (rc == ECPU_OK) {
+        rc = check_launch(fn);
+        if (rc != ECPU_OK) return rc;
+        prof_end(ev0, st, "w8a16_gemv_argmax", (double)N * (double)K + 4.0 * (double)N + 2.0 * (double)K,
+                 2.0 * (double)N * (double)K);
+    } else if (rc == ECPU_ERR_UNSUPPORTED) {
+        prof_end(ev0, st, nullptr, 0.0, 0.0);
+        rc = run_linear(F_W8A16, 1, N, K, A, W, S, logits, fn);
+        if (rc != ECPU_OK) return rc;
+        ev0 = prof_begin(st);
+        const uint32_t nblk = (uint32_t)std::min<size_t>(kArgMaxBlocks, (N + kArgStep - 1) / kArgStep);
+        const uint32_t per_block = (uint32_t)round_up((N + nblk - 1) / nblk, 8);
+        argmax_bf16_kernel<<<nblk, kArgThreads, 0, st>>>(logits, (uint32_t)N, per_block, part, ticket, result,
+                                                         index_on_device ? out_index : nullptr,
+                                                         value_on_device ? out_value : nullptr);
+        rc = check_launch(fn);
+        if (rc != ECPU_OK) return rc;
+        prof_end(ev0, st, "w8a16_argmax", 2.0 * (double)N, 0.0);
+    } else {
+        return fail(ECPU_ERR_DEVICE, "%s: raising the LDS limit of the GEMV kernel failed", fn);
+    }
     if (index_on_device && value_on_device) return ECPU_OK;
     // Host outputs (the reference's binding passes ctypes byref): wait for the
     // result like the reference's synchronous call.
@@ -188,7 +210,7 @@ int linear_argmax_core(size_t N, size_t K, const uint16_t *A, const uint8_t *W, 
 // from hipGetSymbolAddress with that device current) for the whole process;
 // calls that overlap in time on one GPU share it and race.
 constexpr size_t kStaticLogitBytes = round_up(kStaticArgmaxMaxN * 2, 256);
-constexpr size_t kStaticPartBytes = (size_t)kArgMaxBlocks * 8;
+constexpr size_t kStaticPartBytes = rows_argmax_tiles(kStaticArgmaxMaxN) * 8;
 constexpr size_t kStaticBytes = kStaticLogitBytes + kStaticPartBytes + 256 + 256;
 __device__ __align__(256) unsigned char scratch[kStaticBytes];
 
@@ -221,7 +243,7 @@ int run_linear_argmax_w8a16(size_t N, size_t K, const uint16_t *A, const uint8_t
                             const char *fn) {
     hipStream_t st = current_stream();
     const size_t logit_bytes = round_up(N * 2, 256);
-    const size_t part_bytes = (size_t)kArgMaxBlocks * 8;
+    const size_t part_bytes = round_up(std::max<size_t>(kArgMaxBlocks, rows_argmax_tiles(N)) * 8, 256);
     void *Y = nullptr;
     int rc = aux_scratch(logit_bytes + part_bytes + 256, &Y, fn);
     if (rc != ECPU_OK) return rc;

@@ -178,11 +178,42 @@ __device__ __forceinline__ void rows_loop(float (&acc)[MT][CH], unsigned char *l
     }
 }
 
-template <int FMT, int MT, int D, int ROWS>
+// The greedy argmax epilogue (kernels.c:658-737): the bf16 logits become
+// (value, index) pairs reduced in the reference scan's order -- a larger
+// value first, then the lower index, from (-inf, 0) -- within the workgroup,
+// parked per workgroup (part[2b], part[2b + 1]), and the last workgroup to
+// take a ticket reduces the parked pairs into result[0..1] and, when not
+// null, *out_index / *out_value; it leaves the ticket at zero.
+struct RowsArgmax {
+    uint32_t *part = nullptr;
+    int *ticket = nullptr;
+    uint32_t *result = nullptr;
+    size_t *out_index = nullptr;
+    float *out_value = nullptr;
+};
+
+__device__ __forceinline__ void rows_arg_take(float v, uint32_t n, float &bv, uint32_t &bn) {
+    if (v > bv || (v == bv && n < bn)) {
+        bv = v;
+        bn = n;
+    }
+}
+
+__device__ __forceinline__ void rows_arg_wave(float &bv, uint32_t &bn) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t on = (uint32_t)__shfl_xor((int)bn, off);
+        rows_arg_take(ov, on, bv, bn);
+    }
+}
+
+template <int FMT, int MT, int D, int ROWS, bool ARG = false>
 __global__ __launch_bounds__(64 * kRowWaves) void gemv_rows_kernel(const void *__restrict__ A_,
                                                                   const uint8_t *__restrict__ W,
                                                                   const float *__restrict__ S, void *__restrict__ C,
-                                                                  int M, int N, int K, int m0) {
+                                                                  int M, int N, int K, int m0, RowsArgmax ao) {
+    static_assert(!ARG || (FMT == F_W8A16 && MT == 1), "argmax epilogue: W8A16, one activation row");
     using R = RowPlan<FMT, MT>;
     extern __shared__ __align__(16) unsigned char lds[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -239,6 +270,75 @@ __global__ __launch_bounds__(64 * kRowWaves) void gemv_rows_kernel(const void *_
         for (int m = 0; m < MT; ++m) ex[(chain * MT + m) * 64 + lane] = acc[m][c];
     }
     __syncthreads();
+    if constexpr (ARG) {
+        // wave 0: this tile's best pair, parked; the workgroup that takes the
+        // last ticket reduces every parked pair with all its threads
+        // (in the dynamic LDS past the 8 x 64 chain sums: a static array would
+        // count against the 160 KB the launch raises the dynamic limit to)
+        int &s_last = *(int *)(ex + 8 * 64);
+        float *s_v = ex + 8 * 64 + 4;
+        uint32_t *s_n = (uint32_t *)(ex + 8 * 64 + 4 + kRowWaves);
+        if (wave == 0) {
+            float bv = -__builtin_inff();
+            uint32_t bn = 0;
+            if (lane < ROWS && n < N) {
+                float l[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) l[c] = ex[c * 64 + lane];
+                const float y = hsum8(l) * S[n];
+                rows_arg_take(__uint_as_float((uint32_t)f32_to_bf16(y) << 16), (uint32_t)n, bv, bn);
+            }
+            rows_arg_wave(bv, bn);
+            if (lane == 0) {
+                // agent-scope stores reach the device-coherent level; once
+                // they have completed the lane takes a ticket (no cache-wide
+                // release: that writes back a whole L2 per workgroup)
+                __hip_atomic_store(ao.part + 2 * blockIdx.x, __float_as_uint(bv), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(ao.part + 2 * blockIdx.x + 1, bn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wait_vmcnt<0>();
+                const int tk = __hip_atomic_fetch_add(ao.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_last = tk == (int)gridDim.x - 1;
+            }
+        }
+        __syncthreads();
+        if (!s_last) return;
+        float bv = -__builtin_inff();
+        uint32_t bn = 0;
+        const uint32_t t = threadIdx.x;
+        // every thread's pairs loaded before any is compared (the loads are
+        // independent; one round trip instead of one per pair)
+        constexpr int kPer = 16;
+        for (uint32_t b0 = t; b0 < gridDim.x; b0 += kPer * 64 * kRowWaves) {
+            uint32_t v[kPer], i[kPer];
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const uint32_t b = b0 + (uint32_t)u * 64 * kRowWaves;
+                if (b < gridDim.x) {
+                    v[u] = __hip_atomic_load(ao.part + 2 * b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    i[u] = __hip_atomic_load(ao.part + 2 * b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kPer; ++u)
+                if (b0 + (uint32_t)u * 64 * kRowWaves < gridDim.x) rows_arg_take(__uint_as_float(v[u]), i[u], bv, bn);
+        }
+        rows_arg_wave(bv, bn);
+        if (lane == 0) {
+            s_v[wave] = bv;
+            s_n[wave] = bn;
+        }
+        __syncthreads();
+        if (t == 0) {
+            for (int w = 1; w < kRowWaves; ++w) rows_arg_take(s_v[w], s_n[w], bv, bn);
+            ao.result[0] = __float_as_uint(bv);
+            ao.result[1] = bn;
+            if (ao.out_index) *ao.out_index = (size_t)bn;
+            if (ao.out_value) *ao.out_value = bv;
+            __hip_atomic_store(ao.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     if (wave != 0 || lane >= ROWS || n >= N) return;
     const float scale = S[n];
 #pragma unroll
@@ -272,7 +372,23 @@ int launch_rows_one(hipStream_t st, const void *A, const uint8_t *W, const float
     if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
     const size_t lds = std::max<size_t>((size_t)D * ROWS * kStripe, (size_t)16 * MT * 64 * sizeof(float));
     const dim3 grid((unsigned)((N + ROWS - 1) / ROWS));
-    gemv_rows_kernel<FMT, MT, D, ROWS><<<grid, 64 * kRowWaves, lds, st>>>(A, W, S, C, M, N, K, m0);
+    gemv_rows_kernel<FMT, MT, D, ROWS><<<grid, 64 * kRowWaves, lds, st>>>(A, W, S, C, M, N, K, m0, RowsArgmax{});
+    return ECPU_OK;
+}
+
+template <int D, int ROWS>
+int launch_rows_argmax(hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, int N, int K,
+                       const RowsArgmax &ao) {
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_rows_kernel<F_W8A16, 1, D, ROWS, true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowMaxLds);
+    });
+    if (attr_rc != hipSuccess) return ECPU_ERR_DEVICE;
+    const size_t lds = std::max<size_t>((size_t)D * ROWS * kStripe, (size_t)16 * 64 * sizeof(float));
+    const dim3 grid((unsigned)((N + ROWS - 1) / ROWS));
+    gemv_rows_kernel<F_W8A16, 1, D, ROWS, true><<<grid, 64 * kRowWaves, lds, st>>>(A, W, S, nullptr, 1, N, K, 0, ao);
     return ECPU_OK;
 }
 
@@ -2211,6 +2327,32 @@ int launch_gq_fmt(int p, int d, int mt, int ntiles, hipStream_t st, const uint16
 }
 
 }  // namespace
+
+// W8A16 GEMV of one activation row with the greedy argmax as its epilogue
+// (the 64-row chain kernel at every N; 32- or 16-row tiles when there are few
+// 64-row ones): no logits are written.  part holds 2 * rows_argmax_tiles(N)
+// words and is 16-byte aligned, ticket must be zero.  ECPU_ERR_UNSUPPORTED (nothing launched) for K not a
+// multiple of the 128-byte stripe or unaligned A / W.
+int run_rows_argmax(size_t N, size_t K, const uint16_t *A, const uint8_t *W, const float *S, uint32_t *part,
+                    int *ticket, uint32_t *result, size_t *out_index, float *out_value, hipStream_t st) {
+    if (N == 0 || K == 0 || K % kStripe || (((uintptr_t)A | (uintptr_t)W | (uintptr_t)part) & 15) ||
+        N >= ((size_t)1 << 31))
+        return ECPU_ERR_UNSUPPORTED;
+    RowsArgmax ao;
+    ao.part = part;
+    ao.ticket = ticket;
+    ao.result = result;
+    ao.out_index = out_index;
+    ao.out_value = out_value;
+    const int ntiles = (int)((N + 63) / 64);
+    const int rows = ntiles >= 256 ? 64 : (ntiles >= 128 ? 32 : 16);
+    const int depth = ntiles <= 256 ? 16 : (ntiles <= 512 ? 8 : 4);
+    if (rows == 16) return launch_rows_argmax<16, 16>(st, A, W, S, (int)N, (int)K, ao);
+    if (rows == 32) return launch_rows_argmax<16, 32>(st, A, W, S, (int)N, (int)K, ao);
+    if (depth == 16) return launch_rows_argmax<16, 64>(st, A, W, S, (int)N, (int)K, ao);
+    if (depth == 8) return launch_rows_argmax<8, 64>(st, A, W, S, (int)N, (int)K, ao);
+    return launch_rows_argmax<4, 64>(st, A, W, S, (int)N, (int)K, ao);
+}
 
 int run_gq_norm(bool swiglu, size_t N, size_t K, const uint16_t *x, const uint16_t *res, const uint16_t *norm_w,
                 uint16_t *res_out, float eps, const uint8_t *W, const float *S, uint16_t *C, hipStream_t st) {

@@ -167,18 +167,24 @@ def test_argmax_golden(case, device_out, dev):
 
 @pytest.mark.parametrize("device_out", [False, True], ids=["host_out", "device_out"])
 @pytest.mark.parametrize("kind", ARGMAX_KINDS)
-def test_argmax_special_logits(kind, device_out, dev):
-    x, w, s = argmax_special_inputs(kind, 4100 + ARGMAX_KINDS.index(kind))
-    _say(f"[gpu] argmax special {kind} device_out={device_out}")
+@pytest.mark.parametrize("epilogue", ["0", "1"], ids=["separate_argmax", "epilogue"])
+def test_argmax_special_logits(kind, device_out, epilogue, dev, monkeypatch):
+    """The GEMV + argmax kernel pair (default), and the GEMV with the argmax
+    epilogue (K = 128: whole 128-byte stripes)."""
+    monkeypatch.setenv("PILM_HIP_ARGMAX_EPILOGUE", epilogue)
+    x, w, s = argmax_special_inputs(kind, 4100 + ARGMAX_KINDS.index(kind), k=128)
+    _say(f"[gpu] argmax special {kind} epilogue={epilogue} device_out={device_out}")
     assert _same(argmax_gpu(x, w, s, dev, device_out), O.linear_w8a16_bf16_argmax(x, w, s))
 
 
-def test_argmax_many_workgroups_and_ties(dev):
-    """Sizes that spread the logits over 1..512 workgroups, with the maximum
+@pytest.mark.parametrize("epilogue", ["0", "1"], ids=["separate_argmax", "epilogue"])
+def test_argmax_many_workgroups_and_ties(epilogue, dev, monkeypatch):
+    """Sizes that spread the logits over 1..2374 workgroups, with the maximum
     placed in the last, the first and a middle workgroup and repeated."""
+    monkeypatch.setenv("PILM_HIP_ARGMAX_EPILOGUE", epilogue)
+    k = 128
     rng = np.random.default_rng(9)
     for n in (1, 7, 2048, 2049, 4097, 65536 + 3, 151936):
-        k = 64
         x = S.activations_bf16(int(n) + 11, 1, k)
         w = S.weights_i8(int(n) + 12, n, k)
         s = S.scales_uniform(int(n) + 13, (n,), fp16_round=False)
@@ -196,9 +202,12 @@ def test_argmax_many_workgroups_and_ties(dev):
             assert _same(argmax_gpu(x, w2, s2, dev, True), exp)
 
 
+@pytest.mark.parametrize("epilogue", ["0", "1"], ids=["separate_argmax", "epilogue"])
 @pytest.mark.parametrize("k", [2048, 4096], ids=["qwen3_1p7b", "qwen3_8b"])
-def test_argmax_lm_head_shape(k, dev):
-    """The Qwen3 lm_head (151936 rows) of the two decode configurations."""
+def test_argmax_lm_head_shape(k, epilogue, dev, monkeypatch):
+    """The Qwen3 lm_head (151936 rows) of the two decode configurations, with
+    the argmax as the GEMV's epilogue and as a kernel of its own."""
+    monkeypatch.setenv("PILM_HIP_ARGMAX_EPILOGUE", epilogue)
     n = 151936
     x = S.activations_bf16(8100 + k, 1, k)
     w = S.weights_i8(8101 + k, n, k)

@@ -57,9 +57,11 @@ def _call(lib, name, x, w, s, n, k, device_out):
     return int(i.value), np.float32(v.value).view(np.uint32)
 
 
+@pytest.mark.parametrize("epilogue", ["0", "1"], ids=["separate_argmax", "epilogue"])
 @pytest.mark.parametrize("device_out", [False, True])
-def test_noalloc_argmax_matches_the_allocating_entry(dev, device_out):
+def test_noalloc_argmax_matches_the_allocating_entry(dev, device_out, epilogue, monkeypatch):
     from pilm_amd import bindings as abi
+    monkeypatch.setenv("PILM_HIP_ARGMAX_EPILOGUE", epilogue)
     lib = abi._load_lib()
     # the first call sizes the array's use with a vocabulary-sized row, the
     # second (fewer rows, ties) reuses whatever the first left in it
