@@ -180,8 +180,10 @@ def test_rejected_arguments(dev):
         A.paged_attention(q, k_new, v_new)                      # host tensors
     with pytest.raises(RuntimeError):
         A.paged_attention(gq, gk, gv, gkc, gvc, ids, 1)         # cache_len < S
+    with pytest.raises(IndexError):
+        A.paged_attention(gq, gk, gv, gkc, gvc, ids[:1], 40)    # too few block ids (a host list, as the reference indexes)
     with pytest.raises(RuntimeError):
-        A.paged_attention(gq, gk, gv, gkc, gvc, ids[:1], 40)    # too few block ids
+        A.paged_attention(gq, gk, gv, gkc, gvc, torch.tensor(ids[:1], dtype=torch.int32, device=dev), 40)   # device table
     with pytest.raises(RuntimeError):
         A.paged_attention(gq, gk, gv, None, None, None, 40)     # no cache needs cache_len == S
 
