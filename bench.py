@@ -331,7 +331,7 @@ def copy_peak(torch, dev, nbytes: int = 1 << 30, reps: int = 10) -> float:
 
 def sweep(torch, dev, sections) -> dict:
     """Per-shape times of the measurement configurations:
-      g128   W4A16 g128 at the Qwen3-1.7B shapes, M = 1, 4, 16
+      g128   W4A16 g128 at the Qwen3-1.7B shapes, M = 1, 4, 16, and the 8B shapes, M = 1
       w4row  per-row W4A16 (bundle v2) at the 1.7B shapes, M = 1, 4, 16
       w8a32  W8A32: 4096x4096 (the single-GEMV configuration) and the 8B shapes, M = 1
       w8a16  W8A16 at the 8B shapes, M = 1 and 5 (MTP verify of one sequence)
@@ -348,6 +348,8 @@ def sweep(torch, dev, sections) -> dict:
     if "g128" in sections:
         res["g128_1p7b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4g128", n, k, (1, 4, 16))}
                             for name, n, k in LAYER_SHAPES + [LM_HEAD]}
+        res["g128_8b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4g128", n, k, (1,))}
+                          for name, n, k in SHAPES_8B}
     if "w4row" in sections:
         res["w4row_1p7b"] = {name: {"N": n, "K": k, **time_linear(torch, dev, "w4row", n, k, (1, 4, 16))}
                              for name, n, k in SHAPES_1P7B_ROW}
