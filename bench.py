@@ -54,6 +54,13 @@ Profiling helpers (rocprofv3 runs the program, these read its output):
   --attn-traffic F W    FETCH_SIZE / WRITE_SIZE CSVs of two such passes ->
                         bytes per dispatch of each attention kernel beside
                         the K or V bytes it must read
+  --shape-pmc-pass      the Qwen3-8B GEMV shapes (W4A16 g128 and W8A32, M=1),
+                        the 80-row exact verify and three matrix-core GEMMs,
+                        each --steps times after a marker kernel, then the
+                        copy kernel, for one counter pass
+  --shape-counters S F  the SQ/GRBM and FETCH_SIZE CSVs of two such passes
+                        -> per-shape table (time, HBM bytes vs algorithmic,
+                        wait share, VALU and MFMA busy, VALU per MFMA)
 """
 from __future__ import annotations
 
@@ -633,6 +640,116 @@ def pmc_pass(torch, dev, steps: int) -> None:
           f"{CALIB_BYTES} B", flush=True)
 
 
+# Shapes of the per-shape counter pass: (label, format, N, K, M, matrix-core threshold or None)
+SHAPE_PMC_CASES = [(f"g128 M=1 {name}", "w4g128", n, k, 1, None) for name, n, k in SHAPES_8B] + [
+    ("w8a32 M=1 single 4096x4096", "w8a32", 4096, 4096, 1, None),
+    ("w8a32 M=1 q_proj", "w8a32", 8192, 4096, 1, None),
+    ("w8a32 M=1 gate_up_proj", "w8a32", 24576, 4096, 1, None),
+    ("w8a32 M=1 down_proj", "w8a32", 4096, 12288, 1, None),
+    ("w8a16 M=80 gate_up_proj, exact", "w8a16", 24576, 4096, 80, 0),
+    ("g128 M=64 gate_up_proj, matrix cores", "w4g128", 24576, 4096, 64, None),
+    ("g128 M=2048 gate_up_proj, matrix cores", "w4g128", 24576, 4096, 2048, None),
+    ("w8a32 M=1024 gate_up_proj, matrix cores", "w8a32", 24576, 4096, 1024, None),
+]
+SHAPE_PMC_COUNTERS = ("SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_INSTS_VALU SQ_INSTS_MFMA "
+                      "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE")
+
+
+def shape_pmc_pass(torch, dev, reps: int) -> None:
+    """Each shape of SHAPE_PMC_CASES called `reps` times eagerly after a
+    marker (a 1-element fill), then the 1 GiB copy kernel: one rocprofv3
+    counter pass attributes every dispatch between two markers to a shape."""
+    from pilm_amd import bindings as abi
+    lib = abi._load_lib()
+    marker = torch.empty(1, device=dev)       # (no kernel: the first fill is the first marker)
+    gen = torch.Generator(device=dev)
+    for label, fmt, n, k, m, thr in SHAPE_PMC_CASES:
+        gen.manual_seed(n + k + m)
+        w, sc = _fmt_weights(torch, dev, fmt, n, k, gen)
+        x = torch.randn((m, k), device=dev, generator=gen)
+        x = x if fmt == "w8a32" else x.to(torch.bfloat16)
+        out = torch.empty((m, n), dtype=torch.float32 if fmt == "w8a32" else torch.bfloat16, device=dev)
+        d = abi.EkernelLinearW8A32Desc(m, n, k)
+        fn = getattr(lib, _ENTRY[fmt])
+        prev = abi.matrix_core_min_rows()
+        if thr is not None:
+            abi.set_matrix_core_min_rows(thr)
+        try:
+            abi.set_stream(torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            marker.fill_(1.0)
+            for _ in range(reps):
+                rc = fn(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                        ctypes.c_void_p(sc.data_ptr()), ctypes.c_void_p(out.data_ptr()), 6)
+                if rc != 0:
+                    raise RuntimeError(abi.last_error())
+            torch.cuda.synchronize()
+        finally:
+            abi.set_matrix_core_min_rows(prev)
+        print(f"[bench] shape pmc: {label}", flush=True)
+        del w, sc, x, out
+    marker.fill_(1.0)
+    torch.cuda.empty_cache()
+    xc = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    yc = torch.empty_like(xc)
+    for _ in range(3):
+        torch.neg(xc, out=yc)
+    torch.cuda.synchronize()
+
+
+def shape_counters(sq_csv: str, fetch_csv: str, reps: int) -> str:
+    """Markdown table of the shape pass: per call, counter-run time, HBM
+    bytes (FETCH_SIZE scaled by the copy kernel) against the algorithmic
+    bytes, the share of wave cycles spent waiting, VALU busy, MFMA busy, and
+    VALU instructions per MFMA."""
+    import csv
+
+    def load(path):
+        disp = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"], "t": (int(r["End_Timestamp"]) -
+                                                                                            int(r["Start_Timestamp"]))})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        return [disp[i] for i in sorted(disp)]
+
+    def segments(ds):
+        segs, cur = [], None
+        for d in ds:
+            if "FillFunctor" in d["name"]:
+                if cur is not None:
+                    segs.append(cur)
+                cur = []
+            elif cur is not None and ("pilm::" in d["name"] or "_ZN4pilm" in d["name"]):
+                cur.append(d)
+        tail = [d for d in ds if "neg_kernel" in d["name"]]
+        return [sg for sg in segs if sg], tail
+
+    sq_segs, _ = segments(load(sq_csv))
+    f_segs, f_copy = segments(load(fetch_csv))
+    if len(sq_segs) != len(SHAPE_PMC_CASES) or len(f_segs) != len(SHAPE_PMC_CASES) or not f_copy:
+        raise SystemExit(f"expected {len(SHAPE_PMC_CASES)} shape segments and the copy kernel")
+    ff = CALIB_BYTES / (sum(d["FETCH_SIZE"] for d in f_copy) / len(f_copy) * 1024)
+    lines = ["| shape | N x K x M | us per call | HBM GB/s (% of 8 TB/s) | fetch / algorithmic | waiting (% of wave cycles) "
+             "| VALU busy % | MFMA busy % | VALU instr per MFMA |", "|---|---|---|---|---|---|---|---|---|"]
+    for (label, fmt, n, k, m, _), sq, fs in zip(SHAPE_PMC_CASES, sq_segs, f_segs):
+        us = sum(d["t"] for d in sq) / reps / 1e3
+        fetch = sum(d["FETCH_SIZE"] for d in fs) / reps * 1024 * ff
+        alg = _fmt_bytes(fmt, m, n, k)
+        tot = {c: sum(d.get(c, 0.0) for d in sq) for c in SHAPE_PMC_COUNTERS.split()}
+        # GRBM_GUI_ACTIVE comes summed over the 8 XCDs: per XCD it is the
+        # busy cycles the derived VALUBusy / MfmaUtil metrics divide by
+        grbm = max(tot["GRBM_GUI_ACTIVE"] / 8, 1.0)
+        wait = 100.0 * tot["SQ_WAIT_ANY"] / max(tot["SQ_WAVE_CYCLES"], 1.0)
+        valu = 100.0 * tot["SQ_ACTIVE_INST_VALU"] / 256 / grbm
+        mfma = 100.0 * tot["SQ_VALU_MFMA_BUSY_CYCLES"] / (grbm * 1024)
+        per = (f"{tot['SQ_INSTS_VALU'] / tot['SQ_INSTS_MFMA']:.1f}" if tot["SQ_INSTS_MFMA"] > 0 else "-")
+        gbps = alg / (us * 1e-6) / 1e9
+        lines.append(f"| {label} | {n} x {k} x {m} | {us:.2f} | {gbps:.0f} ({gbps / 80:.1f} %) | {fetch / alg:.3f} | "
+                     f"{wait:.0f} | {valu:.1f} | {mfma:.1f} | {per} |")
+    return "\n".join(lines)
+
+
 ATTN_PMC_CASE = ("qwen3_8b", 32, 8, 1, 32768)   # model, H, Hkv, S, L (16-token blocks, D = 128)
 
 
@@ -789,6 +906,10 @@ def main(argv=None) -> int:
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--stats-summary", metavar="STATS_CSV")
     ap.add_argument("--attn-pmc-pass", action="store_true")
+    ap.add_argument("--shape-pmc-pass", action="store_true",
+                    help="the Qwen3-8B GEMV / GEMM / verify shapes, one counter pass")
+    ap.add_argument("--shape-counters", nargs=2, metavar=("SQ_CSV", "FETCH_CSV"),
+                    help="counter CSVs of two --shape-pmc-pass runs -> markdown table")
     ap.add_argument("--attn-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--layout", choices=("fused", "separate"), default="fused",
                     help="q/k/v and gate/up as one matrix each (the decoder's layout) or one call per projection")
@@ -818,6 +939,9 @@ def main(argv=None) -> int:
     if args.attn_traffic:
         print(json.dumps(attn_traffic_summary(*args.attn_traffic)))
         return 0
+    if args.shape_counters:
+        print(shape_counters(*args.shape_counters, reps=args.steps))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: there is no multi-GPU path (asked for --gpus {args.gpus}); "
               "the decode GEMV would shard by output rows, each GPU holding W[N/G, K] and its scales",
@@ -834,6 +958,9 @@ def main(argv=None) -> int:
         return 0
     if args.attn_pmc_pass:
         attn_pmc_pass(torch, dev, args.steps)
+        return 0
+    if args.shape_pmc_pass:
+        shape_pmc_pass(torch, dev, args.steps)
         return 0
     m = 1
     print(f"[bench] building step: {len(step_shapes())} W4A16-g128 linears, M={m}", flush=True)
