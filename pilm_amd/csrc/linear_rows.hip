@@ -2290,7 +2290,16 @@ template <int FMT, int MT>
 int launch_gq8(int p, int ntiles, hipStream_t st, const uint16_t *A, const uint8_t *W, const float *S, uint16_t *C,
                int N, int K, int m0) {
     switch (p) {
-        case 8: return launch_gq8_one<FMT, MT, 4, 8>(ntiles, st, A, W, S, C, N, K, m0);
+        case 8: {
+            // ring slots: five where a wave has three stripes, so all three are
+            // in flight at once (2048x6144: 6.13 -> 5.90 us); four otherwise
+            // (PILM_HIP_GQ8_D = 4, 5 or 8)
+            const int sps = (K / 256 + 7) / 8;
+            const int de = env_int("PILM_HIP_GQ8_D", sps == 3 ? 5 : 4);
+            if (de == 5) return launch_gq8_one<FMT, MT, 5, 8>(ntiles, st, A, W, S, C, N, K, m0);
+            if (de == 8) return launch_gq8_one<FMT, MT, 8, 8>(ntiles, st, A, W, S, C, N, K, m0);
+            return launch_gq8_one<FMT, MT, 4, 8>(ntiles, st, A, W, S, C, N, K, m0);
+        }
         case 4: return launch_gq8_one<FMT, MT, 8, 4>(ntiles, st, A, W, S, C, N, K, m0);
         case 2: return launch_gq8_one<FMT, MT, 8, 2>(ntiles, st, A, W, S, C, N, K, m0);
         default: return launch_gq8_one<FMT, MT, 16, 1>(ntiles, st, A, W, S, C, N, K, m0);

@@ -68,6 +68,8 @@ SPLITS = [{"PILM_HIP_GQ": "0", "PILM_HIP_NSPLIT": "1"}, {"PILM_HIP_GQ": "0", "PI
           {"PILM_HIP_GQ_P": "1"}, {"PILM_HIP_GQ_P": "2"}, {"PILM_HIP_GQ_P": "4"},
           {"PILM_HIP_GQ_P": "4", "PILM_HIP_GQ_D": "16"}, {"PILM_HIP_GQ_P": "8"},
           {"PILM_HIP_GQ_P": "8", "PILM_HIP_GQ_D": "8"}, {"PILM_HIP_GQ8": "0"}, {"PILM_HIP_GQ8": "1"},
+          {"PILM_HIP_GQ8": "1", "PILM_HIP_GQ8_D": "4"}, {"PILM_HIP_GQ8": "1", "PILM_HIP_GQ8_D": "5"},
+          {"PILM_HIP_GQ8": "1", "PILM_HIP_GQ8_D": "8"},
           {"PILM_HIP_BCAST_PL": "1"}, {"PILM_HIP_BCAST_PL": "3"}, {"PILM_HIP_BCAST_MT": "8"},
           {"PILM_HIP_BCAST_MT": "8", "PILM_HIP_BCAST_PL": "2"}, {"PILM_HIP_BCAST": "0"},
           {"PILM_HIP_BCAST": "0", "PILM_HIP_GQ": "0"}, {"PILM_HIP_BCAST_WIN": "1", "PILM_HIP_BCAST_MT": "4"},
