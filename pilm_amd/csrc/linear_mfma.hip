@@ -32,8 +32,10 @@
 // Tiling: a workgroup of four waves computes BM x BN outputs (waves WM x WN,
 // each (BM/WM) x (BN/WN) in 32 x 32 MFMA tiles) over K in steps of 64, with a
 // double-buffered LDS stage filled by global -> LDS DMA (activation blocks
-// XOR-swizzled by row, weights row-major) while the previous step is
-// multiplied; weights are unpacked from LDS into registers per 16-k step.
+// XOR-swizzled by row, weights row-major, the stage's group scales) while the
+// previous step is multiplied; weights are unpacked from LDS into registers
+// per 16-k step, and the LDS fragments of the next 16-k step are read while
+// the current one is decoded and multiplied.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -194,7 +196,20 @@ __global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ 
 // them in split order (deterministic) and finishes the outputs.
 // X: the activations prepared by act_prep_kernel (fp16, planes x M x K).
 template <int FMT, int BM, int BN, int WM>
-__global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 *__restrict__ X,
+constexpr int mfma_stage_bytes() {
+    using F = MF<FMT>;
+    return BM * kBK * 2 * F::planes + BN * F::wrow + (F::group > 0 ? kMfmaThreads * 4 : 0);
+}
+
+// Two resident workgroups per CU where their LDS stages fit (the register
+// budget follows), else one.
+template <int FMT, int BM, int BN, int WM>
+constexpr int mfma_min_blocks() {
+    return 4 * mfma_stage_bytes<FMT, BM, BN, WM>() <= 160 * 1024 ? 2 : 1;
+}
+
+template <int FMT, int BM, int BN, int WM>
+__global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>())) void gemm_mfma_kernel(const _Float16 *__restrict__ X,
                                                                 const uint8_t *__restrict__ W,
                                                                 const float *__restrict__ S, void *__restrict__ C,
                                                                 float *__restrict__ P, const int *__restrict__ E,
@@ -206,10 +221,17 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
     constexpr int A_PLANE = BM * kBK * 2;
     constexpr int A_BYTES = A_PLANE * F::planes;
     constexpr int W_BYTES = BN * F::wrow;
-    constexpr int STAGE = A_BYTES + W_BYTES;
+    constexpr int SPS = F::group == 32 ? 2 : 1;   // groups per stage (group formats)
+    // group scales of the stage, one 4-byte DMA per thread: float tid is
+    // row tid % BN of the stage's group tid / BN (beyond SPS groups: a copy
+    // of the first, unused)
+    constexpr int SC_BYTES = F::group > 0 ? kMfmaThreads * 4 : 0;
+    constexpr int STAGE = A_BYTES + W_BYTES + SC_BYTES;
     constexpr int A_LOADS = A_PLANE / 16 / kMfmaThreads;     // 16-byte DMA per thread per plane and stage
     constexpr int W_LOADS = W_BYTES / 16 / kMfmaThreads;
     static_assert(A_LOADS >= 1 && W_LOADS >= 1, "tile too small");
+    static_assert(F::group == 0 || (kMfmaThreads % BN == 0 && SPS * BN <= kMfmaThreads), "scale slots");
+    static_assert(STAGE == mfma_stage_bytes<FMT, BM, BN, WM>(), "stage layout");
     __shared__ __align__(16) unsigned char lds[2 * STAGE];
 
     const int tid = threadIdx.x;
@@ -268,77 +290,100 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
 
     const int mrow_base = wm * (BM / WM);
     const int ncol_base = wn * (BN / WN);
-    // Group scales of the lane's weight rows for one stage: one per group the
-    // stage touches (g128: 1, g32: 2), loaded a stage ahead.
-    constexpr int SPS = F::group == 32 ? 2 : 1;
     const int G = F::group > 0 ? (K + F::group - 1) / F::group : 1;
-    float sreg[TN][SPS];
     int wexp[TN];   // weight-row exponents (group formats): scales are taken times 2^wexp
 #pragma unroll
     for (int j = 0; j < TN; ++j)
         wexp[j] = F::group > 0 ? E[M + min(n0 + ncol_base + j * 32 + (lane & 31), N - 1)] : 0;
-    auto load_scales = [&](int t) {
+    auto load_sc = [&](int t, int b) {
         if constexpr (F::group > 0) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int n = min(n0 + ncol_base + j * 32 + (lane & 31), N - 1);
-#pragma unroll
-                for (int g = 0; g < SPS; ++g)
-                    sreg[j][g] = ldexpf(S[(size_t)n * G + ((t0 + t) * kBK) / F::group + g], wexp[j]);
-            }
+            const int gl = tid / BN, row = tid % BN;
+            const int g = min(((t0 + t) * kBK) / F::group + (gl < SPS ? gl : 0), G - 1);
+            const float *src = S + (size_t)min(n0 + row, N - 1) * G + g;
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (lds_void *)(lds + b * STAGE + A_BYTES + W_BYTES + wave * 256), 4, 0, 0);
         }
     };
+    auto issue = [&](int t, int b) {
+        load_a(t, b);
+        load_w(t, b);
+        load_sc(t, b);
+    };
 
-    load_scales(0);
-    load_a(0, 0);
-    load_w(0, 0);
+    issue(0, 0);
     wait_vmcnt<0>();
     __syncthreads();
 
     const uint32_t magic = opaque_magic();
     for (int t = 0; t < nsteps; ++t) {
         const int b = t & 1;
-        h2 spair[TN][SPS];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int g = 0; g < SPS; ++g) {
-                const _Float16 h = (_Float16)sreg[j][g];
-                spair[j][g] = h2{h, h};
-            }
-        if (t + 1 < nsteps) {
-            load_scales(t + 1);
-            load_a(t + 1, b ^ 1);
-            load_w(t + 1, b ^ 1);
-        }
+        if (t + 1 < nsteps) issue(t + 1, b ^ 1);
         const unsigned char *as = lds + b * STAGE;
         const unsigned char *ws = as + A_BYTES;
+        h2 spair[TN][SPS];
+        if constexpr (F::group > 0) {
+            const float *scs = (const float *)(ws + W_BYTES);
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            half8 bfr[TN];
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < SPS; ++g) {
+                    const _Float16 h = (_Float16)ldexpf(scs[g * BN + ncol_base + j * 32 + (lane & 31)], wexp[j]);
+                    spair[j][g] = h2{h, h};
+                }
+        }
+        // LDS fragments of step kk + 1 are read while step kk decodes and
+        // multiplies (raw weight words and activation blocks, two slots)
+        uint32_t wraw[2][TN][F::w8 ? 2 : 1];
+        half8 afr[2][TM][F::planes];
+        auto read_frags = [&](int kk, int slot) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int nl = ncol_base + j * 32 + (lane & 31);
-                u32x4 q;
                 if constexpr (F::w8) {
                     // bytes k..k+7 of row nl: k = 16 kk + 8 (lane >> 5), chunk kk
                     const uint32_t *pw =
                         (const uint32_t *)(ws + nl * F::wrow + ((kk ^ F::wswz(nl)) << 4) + 8 * (lane >> 5));
+                    wraw[slot][j][0] = pw[0];
+                    wraw[slot][j][F::w8 ? 1 : 0] = pw[1];
+                } else {
+                    // nibbles k..k+7 of row nl: byte 8 kk + 4 (lane >> 5), chunk kk / 2
+                    wraw[slot][j][0] = *(const uint32_t *)(ws + nl * F::wrow + (((kk >> 1) ^ F::wswz(nl)) << 4) +
+                                                           8 * (kk & 1) + 4 * (lane >> 5));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int row = mrow_base + i * 32 + (lane & 31);
+                const int kb = 2 * kk + (lane >> 5);
+#pragma unroll
+                for (int pl = 0; pl < F::planes; ++pl)
+                    afr[slot][i][pl] =
+                        *(const half8 *)(as + pl * A_PLANE + row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4));
+            }
+        };
+        read_frags(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int slot = kk & 1;
+            if (kk + 1 < kBK / 16) read_frags(kk + 1, slot ^ 1);
+            __builtin_amdgcn_sched_barrier(0);   // keep those reads ahead of this step's work
+            half8 bfr[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                u32x4 q;
+                if constexpr (F::w8) {
                     const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
                     for (int d = 0; d < 2; ++d) {
-                        const uint32_t u = pw[d] ^ 0x80808080u;
+                        const uint32_t u = wraw[slot][j][F::w8 ? d : 0] ^ 0x80808080u;
                         const h2 lo = __builtin_bit_cast(h2, (u & 0x00FF00FFu) | magic) + bias;
                         const h2 hi = __builtin_bit_cast(h2, ((u >> 8) & 0x00FF00FFu) | magic) + bias;
                         q[2 * d] = __builtin_bit_cast(uint32_t, lo);
                         q[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
                     }
                 } else {
-                    // nibbles k..k+7 of row nl: byte 8 kk + 4 (lane >> 5), chunk kk / 2
-                    const uint32_t x = *(const uint32_t *)(ws + nl * F::wrow + (((kk >> 1) ^ F::wswz(nl)) << 4) +
-                                                           8 * (kk & 1) + 4 * (lane >> 5));
                     h2 qq[4];
-                    dequant_w4(x, magic, qq);
+                    dequant_w4(wraw[slot][j][0], magic, qq);
                     if constexpr (F::group > 0) {
                         const h2 sp = spair[j][SPS == 2 ? (kk >> 1) : 0];
 #pragma unroll
@@ -350,21 +395,15 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_mfma_kernel(const _Float16 
                 bfr[j] = __builtin_bit_cast(half8, q);
             }
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int row = mrow_base + i * 32 + (lane & 31);
-                const int kb = 2 * kk + (lane >> 5);
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int pl = 0; pl < F::planes; ++pl) {
-                    const half8 af =
-                        *(const half8 *)(as + pl * A_PLANE + row * (kBK * 2) + ((kb ^ ((row >> 1) & 7)) << 4));
+                for (int pl = 0; pl < F::planes; ++pl)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bfr[j], acc[i][j], 0, 0, 0);
-                }
-            }
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[slot][i][pl], bfr[j], acc[i][j], 0, 0, 0);
         }
-        if (t + 1 < nsteps) wait_vmcnt<0>();
-        __syncthreads();
+        wait_vmcnt<0>();               // stage t + 1 has landed
+        __syncthreads();               // ... and stage t's buffer is free for stage t + 2
     }
 
     // ---- epilogue: lane holds column (lane & 31) of each tile, rows
@@ -436,14 +475,16 @@ void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, i
     const unsigned wrows = MF<FMT>::group > 0 ? (unsigned)((N + 255) / 256) : 0u;
     act_prep_kernel<FMT><<<(unsigned)M + wrows, 256, 0, st>>>(A, (u32x4 *)X, E, M, K, S, N, G);
     // waves 1 x 4 (each wave all of the tile's rows, a quarter of its
-    // columns, so every weight is decoded once) for int4 weights below 128
-    // rows: 8B gate_up W4 g128 M=64 47.9 vs 53.2 us, M=80 59.8 vs 71.1 us;
-    // 2 x 2 otherwise (int8's cheaper decode gains nothing from it)
-    int wm = (!MF<FMT>::w8 && bm == 64) ? 1 : 2;
+    // columns, so every weight is decoded once) for int4 weights: 8B gate_up
+    // W4 g128 M = 64 47.9 vs 53.2 us, M = 80 59.8 vs 71.1 us, M = 1024 261 vs
+    // 282 us, M = 2048 (128-row tiles) 504 vs 548 us; 2 x 2 for int8 (its
+    // cheaper decode gains nothing from it: W8A32 gate_up M = 1024 443 vs 445 us)
+    int wm = MF<FMT>::w8 ? 2 : 1;
     const int env_wm = env_int("PILM_HIP_MFMA_WM", 0);
     if (env_wm == 1 || env_wm == 2) wm = env_wm;
     if (bm == 256)
-        launch_mfma<FMT, 256, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
+        wm == 1 ? launch_mfma<FMT, 256, 128, 1>(st, X, W, S, C, P, E, splits, sps, M, N, K)
+                : launch_mfma<FMT, 256, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
     else if (bm == 128)
         wm == 1 ? launch_mfma<FMT, 128, 128, 1>(st, X, W, S, C, P, E, splits, sps, M, N, K)
                 : launch_mfma<FMT, 128, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
@@ -471,10 +512,16 @@ bool mfma_supports(size_t K, const void *A, const uint8_t *W) {
 int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t *W, const float *S, void *C,
              hipStream_t st, const char *fn) {
     if (!mfma_supports(K, A, W)) return fail(ECPU_ERR_UNSUPPORTED, "%s: shape not taken by the matrix-core path", fn);
-    // 128-row tiles from M = 128 (256-row tiles at M = 2048 measured no
-    // faster for W4 and slower for W8A32: 8B gate_up 851 vs 926 us, down 450
-    // vs 551 us; W4 g128 down 287 vs 317 us), 64 below
+    // 128-row tiles from M = 128, 64 below; int4 weights take 256-row tiles
+    // where the grid still gives every CU two workgroups (each wave then
+    // multiplies every decoded weight by 256 rows: 8B W4 g128 gate_up M = 2048
+    // 475 vs 504 us, q_proj 174 vs 185 us; with fewer tiles, down M = 2048 and
+    // q_proj M = 1024, the 128-row tiles win: 277 vs 291 us, 103 vs 130 us).
+    // W8A32's two activation planes leave one 256-row workgroup per CU
+    // (gate_up M = 2048 959 vs 894 us).
     int bm = M >= 128 ? 128 : 64;
+    const bool w4 = fmt == F_W4ROW || fmt == F_W4G128 || fmt == F_W4G32;
+    if (w4 && M >= 256 && ((N + 127) / 128) * ((M + 255) / 256) >= 512) bm = 256;
     const int env_bm = env_int("PILM_HIP_MFMA_BM", 0);
     if (env_bm == 64 || env_bm == 128 || env_bm == 256) bm = env_bm;
     const size_t blocks = ((N + 127) / 128) * ((M + bm - 1) / bm);
