@@ -142,32 +142,36 @@ __device__ __forceinline__ void load_act8(const void *__restrict__ A, size_t blk
 }
 
 // Activations [M, K] (bf16 or fp32) -> X[plane][M][K] fp16, each 8-element
-// block in the weight unpack order.  Workgroup m < M takes activation row m:
-// its largest magnitude sets the row exponent E[m], then every value is
-// scaled by 2^E[m] (exact) and converted.  Workgroups beyond M (group formats
-// only) set the weight-row exponents E[M + n] from each row's largest scale.
+// block in the weight unpack order.  Workgroup m takes activation row m: its
+// largest magnitude sets the row exponent E[m], then every value is scaled by
+// 2^E[m] (exact) and converted.  The first kPrepHold 8-element blocks of
+// each thread stay in registers between the two passes (all of a row up to
+// K = 16384), so the row is read once and its loads are issued together.
+constexpr int kPrepHold = 8;
+
 template <int FMT>
 __global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ A, u32x4 *__restrict__ X,
-                                                      int *__restrict__ E, int M, int K,
-                                                      const float *__restrict__ S, int N, int G) {
+                                                      int *__restrict__ E, int M, int K) {
     using F = MF<FMT>;
     __shared__ float red[4];
     const int tid = threadIdx.x;
-    if ((int)blockIdx.x >= M) {
-        if constexpr (F::group > 0) {
-            const int n = ((int)blockIdx.x - M) * 256 + tid;
-            if (n < N) {
-                float mx = 0.0f;
-                for (int g = 0; g < G; ++g) mx = fmaxf(mx, fabsf(S[(size_t)n * G + g]));
-                E[M + n] = range_exp(mx, 12);
-            }
-        }
-        return;
-    }
     const int m = blockIdx.x;
     const size_t nb = (size_t)K / 8, row0 = (size_t)m * nb, blocks = (size_t)M * nb;
+    float hold[kPrepHold][8];
+#pragma unroll
+    for (int h = 0; h < kPrepHold; ++h) {
+        const size_t b = tid + (size_t)h * 256;
+        if (b < nb) load_act8<FMT>(A, row0 + b, hold[h]);
+    }
     float mx = 0.0f;
-    for (size_t b = tid; b < nb; b += 256) {
+#pragma unroll
+    for (int h = 0; h < kPrepHold; ++h) {
+        const size_t b = tid + (size_t)h * 256;
+        if (b < nb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(hold[h][e]));
+    }
+    for (size_t b = tid + (size_t)kPrepHold * 256; b < nb; b += 256) {
         float v[8];
         load_act8<FMT>(A, row0 + b, v);
 #pragma unroll
@@ -175,9 +179,7 @@ __global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ 
     }
     const int ex = range_exp(block_max_256(mx, red), 15);
     if (tid == 0) E[m] = ex;
-    for (size_t b = tid; b < nb; b += 256) {
-        float v[8];
-        load_act8<FMT>(A, row0 + b, v);
+    auto put = [&](size_t b, float (&v)[8]) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = ldexpf(v[e], ex);
         if constexpr (F::a32) {
@@ -188,12 +190,28 @@ __global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ 
         } else {
             X[row0 + b] = act_block<FMT>(v);
         }
+    };
+#pragma unroll
+    for (int h = 0; h < kPrepHold; ++h) {
+        const size_t b = tid + (size_t)h * 256;
+        if (b < nb) put(b, hold[h]);
+    }
+    for (size_t b = tid + (size_t)kPrepHold * 256; b < nb; b += 256) {
+        float v[8];
+        load_act8<FMT>(A, row0 + b, v);
+        put(b, v);
     }
 }
 
 // blockIdx.z selects a contiguous range of K steps (split K); with more than
-// one split the raw fp32 sums go to P[z][M][N] and split_reduce_kernel adds
-// them in split order (deterministic) and finishes the outputs.
+// one split the fp32 sums (the weight-row power of two taken out) go to
+// P[z][M][N] and split_reduce_kernel adds them in split order
+// (deterministic) and finishes the outputs.
+// Group formats scale the group scales of each weight row by a power of two
+// 2^wexp that puts the largest scale the workgroup uses in [2^11, 2^12)
+// (scale x weight then stays within fp16 and off its subnormals); a
+// workgroup finds it from the scales of its own K range, which changes
+// nothing but that exact power of two, taken out again in the epilogue.
 // X: the activations prepared by act_prep_kernel (fp16, planes x M x K).
 template <int FMT, int BM, int BN, int WM>
 constexpr int mfma_stage_bytes() {
@@ -291,10 +309,6 @@ __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>()))
     const int mrow_base = wm * (BM / WM);
     const int ncol_base = wn * (BN / WN);
     const int G = F::group > 0 ? (K + F::group - 1) / F::group : 1;
-    int wexp[TN];   // weight-row exponents (group formats): scales are taken times 2^wexp
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-        wexp[j] = F::group > 0 ? E[M + min(n0 + ncol_base + j * 32 + (lane & 31), N - 1)] : 0;
     auto load_sc = [&](int t, int b) {
         if constexpr (F::group > 0) {
             const int gl = tid / BN, row = tid % BN;
@@ -311,6 +325,22 @@ __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>()))
     };
 
     issue(0, 0);
+    // weight-row exponents (group formats): scales are taken times 2^wexp;
+    // the scale loads overlap the first stage's DMA
+    int wexp[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        wexp[j] = 0;
+        if constexpr (F::group > 0) {
+            const int n = min(n0 + ncol_base + j * 32 + (lane & 31), N - 1);
+            const int g0 = (t0 * kBK) / F::group, g1 = min(G, ((t0 + nsteps) * kBK + F::group - 1) / F::group);
+            const float *sr = S + (size_t)n * G;
+            float mx = 0.0f;
+#pragma unroll 16
+            for (int g = g0; g < g1; ++g) mx = fmaxf(mx, fabsf(sr[g]));
+            wexp[j] = range_exp(mx, 12);
+        }
+    }
     wait_vmcnt<0>();
     __syncthreads();
 
@@ -421,7 +451,7 @@ __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>()))
                 const int m = m0 + mrow_base + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 if (m >= M) continue;
                 if (pz) {
-                    pz[(size_t)m * N + n] = acc[i][j][e];
+                    pz[(size_t)m * N + n] = ldexpf(acc[i][j][e], -wexp[j]);
                     continue;
                 }
                 const float y = ldexpf(acc[i][j][e], -(E[m] + wexp[j])) * sc;
@@ -446,7 +476,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
     float y = 0.0f;
     for (int z = 0; z < splits; ++z) y += P[(size_t)z * total + idx];
     const int m = (int)(idx / N), n = (int)(idx % N);
-    y = ldexpf(y, -(E[m] + (F::group > 0 ? E[M + n] : 0)));
+    y = ldexpf(y, -E[m]);
     if constexpr (F::group == 0) y *= S[n];
     if constexpr (F::a32)
         ((float *)C)[idx] = y;
@@ -471,9 +501,7 @@ void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const floa
 template <int FMT>
 void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, int *E, const uint8_t *W,
                      const float *S, void *C, float *P, int splits, int sps, int M, int N, int K) {
-    const int G = MF<FMT>::group > 0 ? (K + MF<FMT>::group - 1) / MF<FMT>::group : 0;
-    const unsigned wrows = MF<FMT>::group > 0 ? (unsigned)((N + 255) / 256) : 0u;
-    act_prep_kernel<FMT><<<(unsigned)M + wrows, 256, 0, st>>>(A, (u32x4 *)X, E, M, K, S, N, G);
+    act_prep_kernel<FMT><<<(unsigned)M, 256, 0, st>>>(A, (u32x4 *)X, E, M, K);
     // waves 1 x 4 (each wave all of the tile's rows, a quarter of its
     // columns, so every weight is decoded once) for int4 weights: 8B gate_up
     // W4 g128 M = 64 47.9 vs 53.2 us, M = 80 59.8 vs 71.1 us, M = 1024 261 vs
@@ -540,11 +568,11 @@ int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
         const int rc = split_scratch(st, (size_t)splits * M * N, 1, &P, &T, fn);
         if (rc != ECPU_OK) return rc;
     }
-    // activation planes, then the row exponents (M activation rows, N weight rows)
+    // activation planes, then the activation-row exponents
     void *X = nullptr;
     const size_t xbytes = ((size_t)M * K * 2 * (fmt == F_W8A32 ? 2 : 1) + 255) & ~(size_t)255;
     {
-        const int rc = act_scratch(xbytes + (M + N) * sizeof(int), &X, fn);
+        const int rc = act_scratch(xbytes + M * sizeof(int), &X, fn);
         if (rc != ECPU_OK) return rc;
     }
     const _Float16 *Xh = (const _Float16 *)X;
