@@ -554,10 +554,16 @@ int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
     if (env_bm == 64 || env_bm == 128 || env_bm == 256) bm = env_bm;
     const size_t blocks = ((N + 127) / 128) * ((M + bm - 1) / bm);
     const int nsteps = (int)(K / kBK);
-    // Split K while the output tiles alone leave the GPU under-filled: aim at
-    // ~1024 workgroups, each keeping at least two K steps.
+    // Split K while the output tiles alone leave CUs idle: aim at ~256
+    // workgroups, each keeping at least four K steps.  More splits cost more
+    // than they fill: every split writes and the reduction reads an M x N fp32
+    // partial (at M = 64, 32 splits of o_proj move 4x its weight bytes).
+    // Measured best split counts land at 256 workgroups (8B W4 g128 M = 64:
+    // o_proj 30.5 -> 21.3 us, gate_up 55.1 -> 44.7, down 39.4 -> 32.6, k_proj
+    // 22.1 -> 17.5; M = 256: o_proj 43.8 -> 32.3, gate_up 107 -> 92).
     int splits = 1;
-    if (blocks < 512) splits = (int)std::min<size_t>((size_t)std::max(1, nsteps / 2), (1024 + blocks - 1) / blocks);
+    if (blocks < 256)
+        splits = (int)std::min<size_t>((size_t)std::max(1, nsteps / 4), (256 + blocks - 1) / blocks);
     const int env_splits = env_int("PILM_HIP_MFMA_SPLITS", 0);
     if (env_splits > 0) splits = std::min(env_splits, nsteps);
     const int sps = (nsteps + splits - 1) / splits;
