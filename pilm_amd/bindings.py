@@ -314,30 +314,6 @@ def last_error() -> str | None:
     return err.decode() if err else None
 
 
-def available_kernel_symbols():
-    lib = _load_lib()
-    return {name: hasattr(lib, name) for name in _OPTIONAL_KERNEL_SYMBOLS}
-
-
-def runtime_info():
-    return {
-        "library_path": library_path(),
-        "version": version(),
-        "isa": detect_isa(),
-        "symbols": available_kernel_symbols(),
-        "env_library_path": os.environ.get("PILM_ECPU_LIB"),
-    }
-
-
-def active_device_info():
-    lib = _load_lib()
-    vt = lib.edevice_active()
-    if not vt:
-        return None
-    name = vt.contents.name.decode() if vt.contents.name else "unknown"
-    return {"name": name, "id": vt.contents.id, "caps": vt.contents.caps}
-
-
 def shutdown():
     _load_lib().ecpu_shutdown()
 
