@@ -37,8 +37,9 @@ Printed JSON line:
   cpu_baseline the reference CPU kernel (kernels.c built from source, OpenMP)
                on a bounded sample of the same workload on this host
   sweep        per-shape times with --sweep [sections]: g128 (default),
-               w4row, w8a32, w8a16, gemm, fused, attention, load (bundle ->
-               HBM), verify (16-sequence MTP verify, M = 80), or all
+               w4row, w8a32, w8a16, gemm, gemm_fp16 (torch's fp16 GEMM at
+               the same shapes, for reference), fused, attention, load
+               (bundle -> HBM), verify (16-sequence MTP verify, M = 80), or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -371,6 +372,8 @@ def sweep(torch, dev, sections) -> dict:
         res["gemm_8b"] = {f"{fmt}_{name}": {"N": n, "K": k, **time_linear(torch, dev, fmt, n, k, gm, reps=5,
                                                                          min_bytes=256 << 20)}
                           for fmt in ("w8a32", "w4g128") for name, n, k in SHAPES_8B if name != "lm_head"}
+    if "gemm_fp16" in sections:
+        res["gemm_fp16_8b"] = sweep_gemm_fp16(torch, dev, (64, 256, 1024, 2048))
     if "fused" in sections:
         res["fused"] = sweep_fused(torch, dev)
     if "attention" in sections:
@@ -379,6 +382,34 @@ def sweep(torch, dev, sections) -> dict:
         res["load"] = sweep_load(torch, dev)
     if "verify" in sections:
         res["verify_8b"] = sweep_verify(torch, dev)
+    return res
+
+
+def sweep_gemm_fp16(torch, dev, ms, reps: int = 20) -> dict:
+    """The plain fp16 GEMM of torch (hipBLASLt) at the 8B shapes, fp16
+    weights already in HBM: what the matrix cores reach without a weight
+    decode, as a reference for the quantized GEMMs (TFLOP/s = 2MNK / time)."""
+    res = {}
+    for name, n, k in SHAPES_8B:
+        if name == "lm_head":
+            continue
+        w = torch.randn((n, k), device=dev, dtype=torch.float16)
+        row = {"N": n, "K": k}
+        for m in ms:
+            a = torch.randn((m, k), device=dev, dtype=torch.float16)
+            for _ in range(3):
+                torch.matmul(a, w.t())
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(a, w.t())
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            row[f"M{m}"] = {"us": round(us, 2), "TFLOPs": round(2.0 * m * n * k / us / 1e6, 1)}
+        res[name] = row
+        del w
     return res
 
 
@@ -648,6 +679,7 @@ SHAPE_PMC_CASES = [(f"g128 M=1 {name}", "w4g128", n, k, 1, None) for name, n, k 
     ("w8a32 M=1 down_proj", "w8a32", 4096, 12288, 1, None),
     ("w8a16 M=80 gate_up_proj, exact", "w8a16", 24576, 4096, 80, 0),
     ("g128 M=64 gate_up_proj, matrix cores", "w4g128", 24576, 4096, 64, None),
+    ("g128 M=1024 gate_up_proj, matrix cores", "w4g128", 24576, 4096, 1024, None),
     ("g128 M=2048 gate_up_proj, matrix cores", "w4g128", 24576, 4096, 2048, None),
     ("w8a32 M=1024 gate_up_proj, matrix cores", "w8a32", 24576, 4096, 1024, None),
 ]
@@ -700,8 +732,9 @@ def shape_pmc_pass(torch, dev, reps: int) -> None:
 def shape_counters(sq_csv: str, fetch_csv: str, reps: int) -> str:
     """Markdown table of the shape pass: per call, counter-run time, HBM
     bytes (FETCH_SIZE scaled by the copy kernel) against the algorithmic
-    bytes, the share of wave cycles spent waiting, VALU busy, MFMA busy, and
-    VALU instructions per MFMA."""
+    bytes, the share of wave cycles spent waiting, VALU busy, MFMA busy,
+    VALU instructions per MFMA, and the shader clock over the call (busy
+    cycles per XCD / time)."""
     import csv
 
     def load(path):
@@ -731,7 +764,7 @@ def shape_counters(sq_csv: str, fetch_csv: str, reps: int) -> str:
         raise SystemExit(f"expected {len(SHAPE_PMC_CASES)} shape segments and the copy kernel")
     ff = CALIB_BYTES / (sum(d["FETCH_SIZE"] for d in f_copy) / len(f_copy) * 1024)
     lines = ["| shape | N x K x M | us per call | HBM GB/s (% of 8 TB/s) | fetch / algorithmic | waiting (% of wave cycles) "
-             "| VALU busy % | MFMA busy % | VALU instr per MFMA |", "|---|---|---|---|---|---|---|---|---|"]
+             "| VALU busy % | MFMA busy % | VALU instr per MFMA | clock GHz |", "|---|---|---|---|---|---|---|---|---|---|"]
     for (label, fmt, n, k, m, _), sq, fs in zip(SHAPE_PMC_CASES, sq_segs, f_segs):
         us = sum(d["t"] for d in sq) / reps / 1e3
         fetch = sum(d["FETCH_SIZE"] for d in fs) / reps * 1024 * ff
@@ -745,8 +778,11 @@ def shape_counters(sq_csv: str, fetch_csv: str, reps: int) -> str:
         mfma = 100.0 * tot["SQ_VALU_MFMA_BUSY_CYCLES"] / (grbm * 1024)
         per = (f"{tot['SQ_INSTS_VALU'] / tot['SQ_INSTS_MFMA']:.1f}" if tot["SQ_INSTS_MFMA"] > 0 else "-")
         gbps = alg / (us * 1e-6) / 1e9
+        # (for calls of a few us the counter window around the dispatch
+        # dominates the busy cycles: no clock for those)
+        ghz = f"{grbm / reps / (us * 1e3):.2f}" if us >= 100.0 else "-"
         lines.append(f"| {label} | {n} x {k} x {m} | {us:.2f} | {gbps:.0f} ({gbps / 80:.1f} %) | {fetch / alg:.3f} | "
-                     f"{wait:.0f} | {valu:.1f} | {mfma:.1f} | {per} |")
+                     f"{wait:.0f} | {valu:.1f} | {mfma:.1f} | {per} | {ghz} |")
     return "\n".join(lines)
 
 
@@ -1017,7 +1053,7 @@ def main(argv=None) -> int:
         out["decode"] = dec
         calls = xs = run = None
     if args.sweep:
-        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "fused", "attention", "load", "verify") \
+        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "gemm_fp16", "fused", "attention", "load", "verify") \
             if args.sweep == "all" \
             else tuple(args.sweep.split(","))
         print(f"[bench] sweeps: {', '.join(sections)}", flush=True)
