@@ -496,8 +496,9 @@ void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const floa
     }
 }
 
-// Output tile per workgroup: 128 x 128 (waves 2 x 2 of 64 x 64) from M =
-// 128, 64 x 128 below; 256 x 128 on request (PILM_HIP_MFMA_BM).
+// Output tile per workgroup: bm x 128 (bm chosen by run_mfma; 64, 128 or
+// 256), waves 1 x 4 for int4 weights and 2 x 2 for int8 (PILM_HIP_MFMA_WM
+// overrides).
 template <int FMT>
 void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, int *E, const uint8_t *W,
                      const float *S, void *C, float *P, int splits, int sps, int M, int N, int K) {
