@@ -95,20 +95,73 @@ __device__ inline float chain_sumsq(const float *x, int n, int t) {
     return a;
 }
 
-// 1 / sqrt(mean(x^2) + eps) of a row in LDS, computed by one whole wave
-// (every lane gets it): the 32 chains, their lanes folded
-// ((c0 + c1) + c2) + c3 across the four chain groups, then the scalar tail and
-// the eight lanes added to 0 in order -- torch's sum -- divided by n.
-__device__ inline float wave_row_rsqrt(const float *x, int n, float eps) {
-    const int lane = threadIdx.x & 63;
-    const float c = lane < 32 ? chain_sumsq(x, n, lane) : 0.0f;
-    const int l = lane & 7;
+// The chains' lanes folded ((c0 + c1) + c2) + c3 across the four chain
+// groups, then the scalar tail and the eight lanes added to 0 in order --
+// torch's sum -- divided by n: 1 / sqrt(mean + eps).  c: chain `lane` on
+// lanes 0..31 of a whole wave (every lane gets the result).
+__device__ inline float fold_row_rsqrt(float c, const float *x, int n, float eps) {
+    const int l = (threadIdx.x & 63) & 7;
     const float p = ((c + __shfl(c, l + 8)) + __shfl(c, l + 16)) + __shfl(c, l + 24);
     float fin = 0.0f;
     for (int i = (n / 8) * 8; i < n; ++i) fin = fin + sq(x[i]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) fin = fin + __shfl(p, j);
     return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(fin, (float)n) + eps));
+}
+
+// 1 / sqrt(mean(x^2) + eps) of a row in LDS, computed by one whole wave
+// (every lane gets it): the 32 chains, then fold_row_rsqrt.
+__device__ inline float wave_row_rsqrt(const float *x, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    const float c = lane < 32 ? chain_sumsq(x, n, lane) : 0.0f;
+    return fold_row_rsqrt(c, x, n, eps);
+}
+
+// The same result with the work spread over a workgroup, for rows with
+// n % 32 == 0 and n <= 16384 (then every chain is a run of 16-vector blocks,
+// each summed from 0, and the cascade's level step is 16 blocks' worth of
+// vectors: level_power 4 in chain_sumsq).  Part one, every thread of the
+// workgroup: block sum b of chain t into bs[32 b + t] (b < nblk), and the
+// chain's remainder (its last size_ilp % 16 vectors, summed from 0) into
+// bs[32 nblk + t].  bs holds 32 (n / 512 + 1) floats.
+__device__ inline void row_sumsq_blocks(const float *x, int n, float *bs, int tid, int nthr) {
+    const int size_ilp = n / 32, nblk = size_ilp / 16, rem = size_ilp - 16 * nblk;
+    const int nb = 32 * (nblk + (rem ? 1 : 0));
+    for (int i = tid; i < nb; i += nthr) {
+        const int t = i & 31, b = i >> 5, k = t >> 3, l = t & 7;
+        const int len = b < nblk ? 16 : rem;
+        float a = 0.0f;
+        for (int j = 0; j < len; ++j) a = a + sq(x[8 * (4 * (16 * b + j) + k) + l]);
+        bs[i] = a;
+    }
+}
+
+// Part two, one whole wave after the block sums are in: each chain replays
+// chain_sumsq's cascade over its block sums (acc[1] += block; at every 256
+// vectors acc[2] += acc[1], at every 4096 acc[3] += acc[2]), adds its
+// remainder as acc[0], then fold_row_rsqrt.
+__device__ inline float wave_row_rsqrt_blocks(const float *x, const float *bs, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int size_ilp = n / 32, nblk = size_ilp / 16, rem = size_ilp - 16 * nblk;
+    float c = 0.0f;
+    if (lane < 32) {
+        float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        for (int b = 0; b < nblk; ++b) {
+            const int r = 16 * (b + 1);
+            a1 = a1 + bs[32 * b + lane];
+            if ((r & (15 << 4)) == 0) {
+                a2 = a2 + a1;
+                a1 = 0.0f;
+                if ((r & (15 << 8)) == 0) {
+                    a3 = a3 + a2;
+                    a2 = 0.0f;
+                }
+            }
+        }
+        const float a0 = rem ? bs[32 * nblk + lane] : 0.0f;
+        c = ((a0 + a1) + a2) + a3;
+    }
+    return fold_row_rsqrt(c, x, n, eps);
 }
 
 // GemmaRMSNorm (layers.py:130-147) output of one element: bf16((w + 1) *

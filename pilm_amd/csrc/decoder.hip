@@ -113,7 +113,17 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t *__rest
         }
     }
     __syncthreads();
-    if (t < 64) {
+    if (n % 32 == 0) {
+        // the block sums of torch's sum of squares by every thread, the
+        // cascade and the fold by wave 0 (same bits as wave_row_rsqrt)
+        float *bs = lds + n + 4;
+        row_sumsq_blocks(xs, n, bs, t, 256);
+        __syncthreads();
+        if (t < 64) {
+            const float r = wave_row_rsqrt_blocks(xs, bs, n, eps);
+            if (t == 0) *rsh = r;
+        }
+    } else if (t < 64) {
         const float r = wave_row_rsqrt(xs, n, eps);
         if (t == 0) *rsh = r;
     }
@@ -836,7 +846,7 @@ int ekernel_rmsnorm_gemma_bf16(const ekernel_rmsnorm_desc_t *desc, const uint16_
     if (rc == ECPU_OK) rc = check_device_buffer(out, bytes, "out", fn);
     if (rc == ECPU_OK && residual_out) rc = check_device_buffer(residual_out, bytes, "residual_out", fn);
     if (rc != ECPU_OK) return rc;
-    const size_t lds = (n + 4) * sizeof(float);
+    const size_t lds = (n + 4 + 32 * (n / 512 + 1)) * sizeof(float);   // row, r, block sums
     const uintptr_t ptrs = (uintptr_t)x | (uintptr_t)residual | (uintptr_t)weight | (uintptr_t)out |
                            (uintptr_t)residual_out;
     hipStream_t st = current_stream();

@@ -1843,8 +1843,13 @@ __global__ __launch_bounds__(64 * P) void gemv_gq_kernel(const uint16_t *__restr
             }
         }
         __syncthreads();
+        // torch's sum of squares: its 16-vector block sums by every thread,
+        // then one wave replays the cascade and the fold
+        float *bs = xs + K + 4;                    // [32 (K / 512 + 1)]
+        row_sumsq_blocks(xs, K, bs, threadIdx.x, 64 * P);
+        __syncthreads();
         if (wave == 0) {
-            const float rs = wave_row_rsqrt(xs, K, na.eps);
+            const float rs = wave_row_rsqrt_blocks(xs, bs, K, na.eps);
             if (lane == 0) xs[K] = rs;
         }
         __syncthreads();
@@ -2004,7 +2009,7 @@ template <int FMT, int MT, int D, int P, bool NORM = false>
 size_t gq_lds_bytes(int K) {
     const size_t G = (size_t)K / (FMT == F_W4G128 ? 128 : 32);
     return (size_t)P * D * kQuadSlotBytes + (size_t)MT * K * 2 + 16 * G * 4 + (size_t)MT * 16 * G * 4 +
-           (NORM ? ((size_t)K + 4) * 4 : 0);
+           (NORM ? ((size_t)K + 4 + 32 * ((size_t)K / 512 + 1)) * 4 : 0);
 }
 
 template <int FMT, int MT, int D, int P>
