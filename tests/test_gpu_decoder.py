@@ -123,7 +123,8 @@ def test_rmsnorm_unaligned_rows(lib, dev):
 @pytest.mark.parametrize("N,K,swiglu,with_res", [(6144, 2048, False, True), (12288, 2048, True, True),
                                                  (1536, 256, False, False), (1024, 256, True, True),
                                                  (10240, 4096, False, True), (24576, 4096, True, True),
-                                                 (2048, 2048, False, False), (48, 512, True, False)])
+                                                 (2048, 2048, False, False), (48, 512, True, False),
+                                                 (512, 12288, False, True)])
 def test_rmsnorm_linear_fused(lib, dev, N, K, swiglu, with_res):
     """ekernel_rmsnorm_linear_w4a16g128_bf16 against the oracle's GemmaRMSNorm,
     W4A16 g128 linear and (swiglu) F.silu(gate) * up, bit for bit: Qwen3-1.7B
