@@ -465,6 +465,20 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
 // Every sum keeps the order of the two-kernel path above.
 constexpr int kDecodeThreads = 512;
 
+// Largest value of a wave (every lane gets it) through DPP row shifts and
+// broadcasts instead of LDS-routed shuffles: max is exact in any order.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    const int ninf = __float_as_int(-__builtin_inff());
+    auto step = [&](int w) { v = fmaxf(v, __int_as_float(w)); };
+    step(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x111, 0xF, 0xF, false));   // row_shr:1
+    step(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x112, 0xF, 0xF, false));   // row_shr:2
+    step(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x114, 0xF, 0xF, false));   // row_shr:4
+    step(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x118, 0xF, 0xF, false));   // row_shr:8
+    step(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x142, 0xA, 0xF, false));   // row_bcast:15
+    step(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 template <int D, int REP, int HPW>
 __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
@@ -602,51 +616,88 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
 
     // scores from the staged key rows, one position per thread; the new
     // position's row is written into the staging from registers (the copy the
-    // DMA brought may predate the cache write)
-    for (int j0 = 0; j0 < vis; j0 += vcap) {
-        if (j0 > 0) {
-            __syncthreads();              // the previous rows have been read
-            stage(k_cache, j0, true);
-        }
+    // DMA brought may predate the cache write).  When every position is one
+    // thread's and one staging pass holds them, each thread first copies its
+    // key row to registers and the value rows' DMA into the same region
+    // starts at once, under the scores (an LDS-only barrier after them; the
+    // softmax's LDS writes then wait for the DMA).
+    const bool early_v = vis <= nthreads && vis <= vcap;
+    if (early_v) {
         wait_vmcnt<0>();
         __syncthreads();                  // the key rows (and the roped q and k) are in
-        const int j1 = min(vis, j0 + vcap);
-        if (is_k && pos >= j0 && pos < j1) {
-            const int jr = pos - j0;
+        if (is_k && pos >= 0 && pos < vis) {
 #pragma unroll
             for (int u = 0; u < kPer; ++u) {
                 const int i = lane + 64 * u;
-                vs[(size_t)jr * D + 8 * ((i / 8) ^ (jr & (per_row - 1))) + i % 8] = kb[u];
+                vs[(size_t)pos * D + 8 * ((i / 8) ^ (pos & (per_row - 1))) + i % 8] = kb[u];
             }
         }
         __syncthreads();
-        for (int j = j0 + t; j < j1; j += nthreads) {
-            uint32_t ka[D / 2];
-            const int jr = j - j0;
-            const uint16_t *row = vs + (size_t)jr * D;
+        uint32_t ka[D / 2];
+        if (t < vis) {
+            const uint16_t *row = vs + (size_t)t * D;
 #pragma unroll
             for (int u = 0; u < per_row; ++u) {
-                const u32x4 c = *(const u32x4 *)(row + 8 * (u ^ (jr & (per_row - 1))));
+                const u32x4 c = *(const u32x4 *)(row + 8 * (u ^ (t & (per_row - 1))));
                 ka[4 * u] = c[0];
                 ka[4 * u + 1] = c[1];
                 ka[4 * u + 2] = c[2];
                 ka[4 * u + 3] = c[3];
             }
+        }
+        __syncthreads();                  // every key row is out of the staging
+        stage(v_cache, 0, false);         // value rows arrive during the scores and the softmax
+        if (t < vis) {
 #pragma unroll
             for (int r = 0; r < hpw; ++r)
-                sc[(size_t)r * scs + j] = bfr(bfr(score_dot<D>(qs + r * D, ka, naive)) * scale);
+                sc[(size_t)r * scs + t] = bfr(bfr(score_dot<D>(qs + r * D, ka, naive)) * scale);
         }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // every score is in
+    } else {
+        for (int j0 = 0; j0 < vis; j0 += vcap) {
+            if (j0 > 0) {
+                __syncthreads();              // the previous rows have been read
+                stage(k_cache, j0, true);
+            }
+            wait_vmcnt<0>();
+            __syncthreads();                  // the key rows (and the roped q and k) are in
+            const int j1 = min(vis, j0 + vcap);
+            if (is_k && pos >= j0 && pos < j1) {
+                const int jr = pos - j0;
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    const int i = lane + 64 * u;
+                    vs[(size_t)jr * D + 8 * ((i / 8) ^ (jr & (per_row - 1))) + i % 8] = kb[u];
+                }
+            }
+            __syncthreads();
+            for (int j = j0 + t; j < j1; j += nthreads) {
+                uint32_t ka[D / 2];
+                const int jr = j - j0;
+                const uint16_t *row = vs + (size_t)jr * D;
+#pragma unroll
+                for (int u = 0; u < per_row; ++u) {
+                    const u32x4 c = *(const u32x4 *)(row + 8 * (u ^ (jr & (per_row - 1))));
+                    ka[4 * u] = c[0];
+                    ka[4 * u + 1] = c[1];
+                    ka[4 * u + 2] = c[2];
+                    ka[4 * u + 3] = c[3];
+                }
+#pragma unroll
+                for (int r = 0; r < hpw; ++r)
+                    sc[(size_t)r * scs + j] = bfr(bfr(score_dot<D>(qs + r * D, ka, naive)) * scale);
+            }
+        }
+        __syncthreads();                      // every score is in; the staged key rows are free
+        stage(v_cache, 0, false);             // value rows arrive during the softmax
     }
-    __syncthreads();                      // every score is in; the staged key rows are free
-    stage(v_cache, 0, false);             // value rows arrive during the softmax
 
     // softmax per head: wave r
     for (int r = wave; r < hpw; r += nthreads / 64) {
         float *x = sc + (size_t)r * scs;
         float mx = -__builtin_inff();
         for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        mx = wave_max_dpp(mx);
         for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -666,15 +717,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
                 }
                 for (; j < vis; j += 8) a = a + x[j];
             }
-            const float b = a + __shfl_xor(a, 4);
-            const float c = b + __shfl_xor(b, 2);
-            sum = __shfl(c + __shfl_xor(c, 1), 0);
+            // ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)), lanes read with readlane
+            float l[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) l[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), q));
+            sum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
         } else {
             for (int j = 0; j < vis; ++j) sum = sum + x[j];
         }
         const float inv = __fdiv_rn(1.0f, sum);
         for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
     }
+
 
     // P.V: thread (chain k, column c), every head of this kv head at once;
     // eight positions of a chain (their value and rep weights) loaded ahead
