@@ -860,7 +860,13 @@ __global__ __launch_bounds__(256) void argmax_key_kernel(const uint16_t *__restr
                                      (uint32_t)__shfl_xor((int)(uint32_t)best, off);
         best = max_u64(best, o);
     }
-    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_max(key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // one atomic per workgroup (the key's maximum does not depend on the order)
+    __shared__ unsigned long long wbest[4];
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_max(key, max_u64(max_u64(wbest[0], wbest[1]), max_u64(wbest[2], wbest[3])),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ __launch_bounds__(64) void greedy_advance_kernel(unsigned long long *__restrict__ key,
@@ -1121,7 +1127,9 @@ int ekernel_greedy_step_bf16(const uint16_t *logits, size_t n, int32_t *state, i
     rc = split_scratch(st, 0, 4096, &P, &T, fn);
     if (rc != ECPU_OK) return rc;
     unsigned long long *key = (unsigned long long *)(T + 4092);
-    const unsigned blocks = (unsigned)std::min<size_t>(256, std::max<size_t>(1, (n / 8 + 255) / 256));
+    // up to 64 workgroups, each thread a few 16-byte chunks (151936 logits:
+    // two per thread)
+    const unsigned blocks = (unsigned)std::min<size_t>(64, std::max<size_t>(1, (n / 8 + 255) / 256));
     argmax_key_kernel<<<blocks, 256, 0, st>>>(logits, (int)n, key);
     greedy_advance_kernel<<<1, 64, 0, st>>>(key, state, tokens, next_id, (int)max_tokens);
     return check_launch(fn);
