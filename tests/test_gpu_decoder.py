@@ -254,7 +254,7 @@ def test_qk_rope_then_attention(lib, dev, S, H, Hkv, D, pos0):
 @pytest.mark.parametrize("H,Hkv,D,pos0", [(16, 8, 128, 383), (16, 8, 128, 0), (16, 8, 128, 1), (16, 8, 128, 2),
                                           (16, 8, 128, 3), (16, 8, 128, 7), (16, 8, 128, 64), (32, 8, 128, 2043),
                                           (4, 2, 128, 0), (8, 8, 64, 17), (16, 4, 128, 100), (16, 8, 128, 4000),
-                                          (32, 8, 64, 515)])
+                                          (32, 8, 64, 515), (16, 8, 128, 511)])
 @pytest.mark.parametrize("shared", [False, True])
 def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0, shared, monkeypatch):
     """ekernel_decode_attention_bf16 (one launch) against the oracle's two
