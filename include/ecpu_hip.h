@@ -390,6 +390,37 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
                                  const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *block_ids,
                                  const uint16_t *gate, const int32_t *step, uint16_t *out);
 
+/* Several sequences' rows in one launch (continuous batching: an MTP verify
+ * step of every running sequence, prefill chunks of several prompts).  No
+ * counterpart in the reference, which runs attention per sequence
+ * (src/engine.py:416-545 under src/runtime/scheduler/scheduler.py:70-178);
+ * each row's result is bit-identical to the per-sequence call's.  Batch rows
+ * 0 .. desc->S - 1 (at most 128) are dealt to n_seqs sequences: sequence i
+ * owns rows row0 .. row0 + rows - 1 at positions pos0 .. pos0 + rows - 1 and
+ * the block table block_ids[table * n_block_ids ...] (block_ids holds
+ * n_tables tables of desc->n_block_ids entries).  Every row must belong to
+ * exactly one sequence. */
+typedef struct {
+    int32_t row0;    /* first batch row of the sequence */
+    int32_t rows;    /* its rows in this call */
+    int32_t pos0;    /* position of its first row (its cached positions before the call) */
+    int32_t table;   /* index of its block table in block_ids */
+} ekernel_batch_seq_t;
+
+/* ekernel_qk_norm_rope_bf16 for a batch (desc->S = batch rows; pos0 ignored). */
+int ekernel_qk_norm_rope_batch_bf16(const ekernel_qk_rope_desc_t *desc, const ekernel_batch_seq_t *seqs,
+                                    size_t n_seqs, size_t n_tables, const uint16_t *qg, const uint16_t *k,
+                                    const uint16_t *v, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                                    const float *cos_table, const float *sin_table, uint16_t *q_out,
+                                    uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids);
+
+/* ekernel_attention_exact_bf16 for a batch (desc->S = batch rows; cache_len
+ * ignored: each sequence's is pos0 + rows). */
+int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *desc, const ekernel_batch_seq_t *seqs,
+                                       size_t n_seqs, size_t n_tables, const uint16_t *q, const uint16_t *k_cache,
+                                       const uint16_t *v_cache, const int32_t *block_ids, const uint16_t *gate,
+                                       uint16_t *out);
+
 typedef struct {
     size_t rows;      /* activation rows: 1 (one decode token) */
     size_t N;         /* rows of W (with swiglu: gate rows then as many up rows) */

@@ -50,6 +50,8 @@ _OPTIONAL_KERNEL_SYMBOLS = [
     "ekernel_rmsnorm_linear_w4a16g128_bf16",
     "ekernel_silu_mul_bf16",
     "ekernel_greedy_step_bf16",
+    "ekernel_qk_norm_rope_batch_bf16",
+    "ekernel_attention_exact_batch_bf16",
 ]
 
 DEFAULT_LIB = Path(__file__).resolve().parent / "lib" / "libecpu.so"
@@ -184,6 +186,11 @@ class EkernelAttentionExactDesc(ctypes.Structure):
                                                "num_blocks", "n_block_ids", "gate_row_stride", "gate_head_stride")]
 
 
+class EkernelBatchSeq(ctypes.Structure):
+    """ekernel_batch_seq_t: one sequence's rows of a batched call."""
+    _fields_ = [(n, ctypes.c_int32) for n in ("row0", "rows", "pos0", "table")]
+
+
 _LINEAR_ARGTYPES = [ctypes.POINTER(EkernelLinearW8A32Desc), ctypes.c_void_p, ctypes.c_void_p,
                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
 
@@ -267,6 +274,14 @@ def _configure(lib):
         lib.ekernel_rmsnorm_linear_w4a16g128_bf16.argtypes = [ctypes.POINTER(EkernelNormLinearDesc)] + \
             [ctypes.c_void_p] * 7
         lib.ekernel_rmsnorm_linear_w4a16g128_bf16.restype = ctypes.c_int
+        lib.ekernel_qk_norm_rope_batch_bf16.argtypes = [ctypes.POINTER(EkernelQkRopeDesc),
+                                                        ctypes.POINTER(EkernelBatchSeq), ctypes.c_size_t,
+                                                        ctypes.c_size_t] + [ctypes.c_void_p] * 11
+        lib.ekernel_qk_norm_rope_batch_bf16.restype = ctypes.c_int
+        lib.ekernel_attention_exact_batch_bf16.argtypes = [ctypes.POINTER(EkernelAttentionExactDesc),
+                                                           ctypes.POINTER(EkernelBatchSeq), ctypes.c_size_t,
+                                                           ctypes.c_size_t] + [ctypes.c_void_p] * 6
+        lib.ekernel_attention_exact_batch_bf16.restype = ctypes.c_int
         lib.ekernel_silu_mul_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
                                               ctypes.c_size_t, ctypes.c_void_p]
         lib.ekernel_silu_mul_bf16.restype = ctypes.c_int

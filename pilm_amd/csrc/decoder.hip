@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "cpu_order.h"
 #include "gemv_device.h"
@@ -143,6 +144,21 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t *__rest
     }
 }
 
+// ---- rows of several sequences in one launch -------------------------------
+// Continuous batching: batch row r belongs to a sequence of nrows[r] rows
+// whose cache holds len[r] positions after the call; the row sits at
+// position pos[r] and the sequence's block table starts at block_ids +
+// tbl[r].  Passed by value as a kernel argument (no device copy, capturable).
+constexpr int kMaxBatchRows = 128;
+struct BatchRows {
+    int32_t pos[kMaxBatchRows];
+    int32_t len[kMaxBatchRows];
+    int32_t nrows[kMaxBatchRows];
+    int32_t tbl[kMaxBatchRows];
+};
+// The single-sequence form: positions from the descriptor or the state word.
+struct OneSeq {};
+
 // ---- q/k GemmaRMSNorm + rope + cache write ---------------------------------
 // One wave per (s, head): head < H normalizes q (the first D of the head's 2D
 // q_proj outputs) into q_out[s, head, :]; head >= H normalizes k of kv head
@@ -150,13 +166,15 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t *__rest
 // (layers.py:150-195, NeoX halves) on the first rot dims: with c, s the fp32
 // tables at the position, (a, b) = (x[f], x[f + rot/2]) becomes
 // (a c - b s, a s + b c), each product and sum rounded, then bf16.
+template <typename RowsT>
 __global__ __launch_bounds__(64) void qk_rope_kernel(
     const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
     size_t q_stride, size_t kv_stride, const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
     const float *__restrict__ cos_t, const float *__restrict__ sin_t, int max_pos, const int32_t *__restrict__ step,
     int pos0_host, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
     const int32_t *__restrict__ block_ids, int n_block_ids, int block_size, int num_blocks, int H, int Hkv, int D,
-    int rot, float eps) {
+    int rot, float eps, RowsT rows) {
+    constexpr bool batched = !std::is_same<RowsT, OneSeq>::value;
     __shared__ float xs[256];
     constexpr int kPer = 4;                  // elements per lane (D <= 256)
     const int s = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
@@ -168,7 +186,14 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(
     // every load issued before the arithmetic: the head's values, the norm
     // weight, v; then (once the position is known) the rope table entries and
     // the cache block
-    const int pos = (step ? step[0] : pos0_host) + s;
+    int pos;
+    const int32_t *bt = block_ids;
+    if constexpr (batched) {
+        pos = rows.pos[s];
+        bt = block_ids + rows.tbl[s];
+    } else {
+        pos = (step ? step[0] : pos0_host) + s;
+    }
     float xr[kPer];
     uint16_t wr[kPer], vr[kPer];
 #pragma unroll
@@ -193,7 +218,7 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(
         }
     }
     int blk = 0;
-    if (!is_q) blk = min(max(block_ids[min(max(pos / block_size, 0), n_block_ids - 1)], 0), num_blocks - 1);
+    if (!is_q) blk = min(max(bt[min(max(pos / block_size, 0), n_block_ids - 1)], 0), num_blocks - 1);
 #pragma unroll
     for (int u = 0; u < kPer; ++u)
         if (t + 64 * u < D) xs[t + 64 * u] = xr[u];
@@ -278,20 +303,32 @@ __device__ __forceinline__ void load_krow(const uint16_t *kr, uint32_t (&kv)[D /
     }
 }
 
-template <int D>
+template <int D, typename RowsT>
 __global__ __launch_bounds__(256) void attn_exact_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache,
     const int32_t *__restrict__ block_ids, int n_block_ids, int num_blocks, int block_size,
     const uint16_t *__restrict__ gate, size_t gate_row_stride, size_t gate_head_stride,
-    const int32_t *__restrict__ step, int cache_len_host, int S, int H, int Hkv, int max_len, int vcap, float scale,
-    uint16_t *__restrict__ out) {
+    const int32_t *__restrict__ step, int cache_len_host, int S_call, int H, int Hkv, int max_len, int vcap,
+    float scale, uint16_t *__restrict__ out, RowsT rows) {
+    constexpr bool batched = !std::is_same<RowsT, OneSeq>::value;
     extern __shared__ float lds[];
     const int kh = blockIdx.x, s = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
     const int rep = H / Hkv;
-    int cache_len = step ? step[1] : cache_len_host;
-    cache_len = min(max(cache_len, S), max_len);
-    const int vis = cache_len - S + s + 1;   // visible positions 0 .. vis-1
+    // this row's sequence: its rows (S), its cached length and the row's
+    // visible positions 0 .. vis-1
+    int S, cache_len, vis;
+    if constexpr (batched) {
+        S = max(rows.nrows[s], 1);
+        cache_len = min(max(rows.len[s], S), max_len);
+        vis = min(max(rows.pos[s], cache_len - S), cache_len - 1) + 1;
+        block_ids += rows.tbl[s];
+    } else {
+        S = S_call;
+        cache_len = step ? step[1] : cache_len_host;
+        cache_len = min(max(cache_len, S), max_len);
+        vis = cache_len - S + s + 1;
+    }
     const bool naive = (long long)S * cache_len * D < 400;
     const int scs = (max_len + 3) & ~3;                        // score row stride (16-byte rows)
     float *qs = lds;                                           // [rep][D]
@@ -884,6 +921,39 @@ __global__ __launch_bounds__(64) void greedy_advance_kernel(unsigned long long *
     state[1] = state[1] + 1;
 }
 
+// The batch rows of a table of sequences: every row of [0, total) belongs
+// to exactly one sequence, whose positions fit max_len and whose table
+// index is below n_tables.
+int build_batch_rows(const ekernel_batch_seq_t *seqs, size_t n_seqs, size_t total, size_t n_tables,
+                     size_t n_block_ids, size_t max_len, BatchRows &br, const char *fn) {
+    if (!seqs || n_seqs == 0) return fail(ECPU_ERR_PARAM, "%s: no sequences", fn);
+    if (total > (size_t)kMaxBatchRows)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu rows in one call (at most %d)", fn, total, kMaxBatchRows);
+    for (int r = 0; r < kMaxBatchRows; ++r) br.nrows[r] = 0;
+    for (size_t i = 0; i < n_seqs; ++i) {
+        const ekernel_batch_seq_t &q = seqs[i];
+        if (q.row0 < 0 || q.rows < 1 || (size_t)q.row0 + (size_t)q.rows > total)
+            return fail(ECPU_ERR_PARAM, "%s: sequence %zu: rows %d..%d outside the %zu batch rows", fn, i, q.row0,
+                        q.row0 + q.rows - 1, total);
+        if (q.pos0 < 0 || (size_t)q.pos0 + (size_t)q.rows > max_len)
+            return fail(ECPU_ERR_PARAM, "%s: sequence %zu: positions %d..%d beyond the %zu its tables hold", fn, i,
+                        q.pos0, q.pos0 + q.rows - 1, max_len);
+        if (q.table < 0 || (size_t)q.table >= n_tables)
+            return fail(ECPU_ERR_PARAM, "%s: sequence %zu: table %d of %zu", fn, i, q.table, n_tables);
+        for (int u = 0; u < q.rows; ++u) {
+            const int r = q.row0 + u;
+            if (br.nrows[r] != 0) return fail(ECPU_ERR_PARAM, "%s: batch row %d in two sequences", fn, r);
+            br.pos[r] = q.pos0 + u;
+            br.len[r] = q.pos0 + q.rows;
+            br.nrows[r] = q.rows;
+            br.tbl[r] = (int32_t)((size_t)q.table * n_block_ids);
+        }
+    }
+    for (size_t r = 0; r < total; ++r)
+        if (br.nrows[r] == 0) return fail(ECPU_ERR_PARAM, "%s: batch row %zu belongs to no sequence", fn, r);
+    return ECPU_OK;
+}
+
 }  // namespace
 
 }  // namespace pilm
@@ -951,10 +1021,10 @@ int ekernel_qk_norm_rope_bf16(const ekernel_qk_rope_desc_t *desc, const uint16_t
     if (rc == ECPU_OK) rc = check_device_buffer(sin_table, d.max_positions * (d.rot_dim / 2) * 4, "sin_table", fn);
     if (rc != ECPU_OK) return rc;
     const dim3 grid((unsigned)d.S, (unsigned)(d.n_heads + d.n_kv_heads));
-    qk_rope_kernel<<<grid, 64, 0, current_stream()>>>(
+    qk_rope_kernel<OneSeq><<<grid, 64, 0, current_stream()>>>(
         qg, k, v, d.q_stride, d.kv_stride, q_norm_w, k_norm_w, cos_table, sin_table, (int)d.max_positions, step, (int)d.pos0,
         q_out, k_cache, v_cache, block_ids, (int)d.n_block_ids, (int)d.block_size, (int)d.num_blocks,
-        (int)d.n_heads, (int)d.n_kv_heads, (int)D, (int)d.rot_dim, d.eps);
+        (int)d.n_heads, (int)d.n_kv_heads, (int)D, (int)d.rot_dim, d.eps, OneSeq{});
     return check_launch(fn);
 }
 
@@ -993,15 +1063,99 @@ int ekernel_attention_exact_bf16(const ekernel_attention_exact_desc_t *desc, con
     const float scale = (float)(1.0 / __builtin_sqrt((double)D));
     hipStream_t st = current_stream();
 #define PILM_ATTN_EXACT(DD)                                                                                         \
-    attn_exact_kernel<DD><<<grid, 256, lds, st>>>(q, k_cache, v_cache, block_ids, (int)d.n_block_ids,             \
-                                                  (int)d.num_blocks, (int)d.block_size, gate, d.gate_row_stride,    \
-                                                  d.gate_head_stride, step, (int)d.cache_len, (int)d.S,             \
-                                                  (int)d.n_heads, (int)d.n_kv_heads, (int)max_len, (int)vcap, scale, \
-                                                  out)
+    attn_exact_kernel<DD, OneSeq><<<grid, 256, lds, st>>>(q, k_cache, v_cache, block_ids, (int)d.n_block_ids,     \
+                                                          (int)d.num_blocks, (int)d.block_size, gate,               \
+                                                          d.gate_row_stride, d.gate_head_stride, step,              \
+                                                          (int)d.cache_len, (int)d.S, (int)d.n_heads,               \
+                                                          (int)d.n_kv_heads, (int)max_len, (int)vcap, scale, out,   \
+                                                          OneSeq{})
     if (D == 64) PILM_ATTN_EXACT(64);
     else if (D == 128) PILM_ATTN_EXACT(128);
     else PILM_ATTN_EXACT(256);
 #undef PILM_ATTN_EXACT
+    return check_launch(fn);
+}
+
+int ekernel_qk_norm_rope_batch_bf16(const ekernel_qk_rope_desc_t *desc, const ekernel_batch_seq_t *seqs,
+                                    size_t n_seqs, size_t n_tables, const uint16_t *qg, const uint16_t *k,
+                                    const uint16_t *v, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                                    const float *cos_table, const float *sin_table, uint16_t *q_out,
+                                    uint16_t *k_cache, uint16_t *v_cache, const int32_t *block_ids) {
+    static const char *fn = "ekernel_qk_norm_rope_batch_bf16";
+    if (!desc || !qg || !k || !v || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !q_out || !k_cache ||
+        !v_cache || !block_ids)
+        return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    const ekernel_qk_rope_desc_t &d = *desc;
+    if (d.S == 0) return ECPU_OK;
+    if (d.head_dim < 32 || d.head_dim > 256 || d.head_dim % 8 || d.rot_dim > d.head_dim || d.rot_dim % 2 ||
+        d.n_kv_heads == 0 || d.n_heads % d.n_kv_heads || d.block_size == 0 || d.n_block_ids == 0 ||
+        d.max_positions == 0)
+        return fail(ECPU_ERR_PARAM, "%s: inconsistent descriptor", fn);
+    BatchRows br;
+    const size_t max_len = std::min(d.max_positions, d.n_block_ids * d.block_size);
+    int rc = build_batch_rows(seqs, n_seqs, d.S, n_tables, d.n_block_ids, max_len, br, fn);
+    if (rc != ECPU_OK) return rc;
+    const size_t D = d.head_dim;
+    rc = check_device_buffer(q_out, d.S * d.n_heads * D * 2, "q_out", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(k_cache, d.num_blocks * d.block_size * d.n_kv_heads * D * 2, "k_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(v_cache, d.num_blocks * d.block_size * d.n_kv_heads * D * 2, "v_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(block_ids, n_tables * d.n_block_ids * 4, "block_ids", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(cos_table, d.max_positions * (d.rot_dim / 2) * 4, "cos_table", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(sin_table, d.max_positions * (d.rot_dim / 2) * 4, "sin_table", fn);
+    if (rc != ECPU_OK) return rc;
+    const dim3 grid((unsigned)d.S, (unsigned)(d.n_heads + d.n_kv_heads));
+    qk_rope_kernel<BatchRows><<<grid, 64, 0, current_stream()>>>(
+        qg, k, v, d.q_stride, d.kv_stride, q_norm_w, k_norm_w, cos_table, sin_table, (int)d.max_positions, nullptr,
+        0, q_out, k_cache, v_cache, block_ids, (int)d.n_block_ids, (int)d.block_size, (int)d.num_blocks,
+        (int)d.n_heads, (int)d.n_kv_heads, (int)D, (int)d.rot_dim, d.eps, br);
+    return check_launch(fn);
+}
+
+int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *desc, const ekernel_batch_seq_t *seqs,
+                                       size_t n_seqs, size_t n_tables, const uint16_t *q, const uint16_t *k_cache,
+                                       const uint16_t *v_cache, const int32_t *block_ids, const uint16_t *gate,
+                                       uint16_t *out) {
+    static const char *fn = "ekernel_attention_exact_batch_bf16";
+    if (!desc || !q || !k_cache || !v_cache || !block_ids || !out)
+        return fail(ECPU_ERR_PARAM, "%s: null argument", fn);
+    const ekernel_attention_exact_desc_t &d = *desc;
+    if (d.S == 0) return ECPU_OK;
+    if (d.n_kv_heads == 0 || d.n_heads % d.n_kv_heads || d.block_size == 0 || d.n_block_ids == 0)
+        return fail(ECPU_ERR_PARAM, "%s: inconsistent descriptor", fn);
+    if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: head_dim %zu (64, 128 or 256)", fn, d.head_dim);
+    const size_t max_len = d.n_block_ids * d.block_size;
+    BatchRows br;
+    int rc = build_batch_rows(seqs, n_seqs, d.S, n_tables, d.n_block_ids, max_len, br, fn);
+    if (rc != ECPU_OK) return rc;
+    const size_t rep = d.n_heads / d.n_kv_heads, D = d.head_dim;
+    const size_t fixed = (rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * kDS * 4 +
+                          ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
+    const size_t room = fixed < 64 * 1024 ? (64 * 1024 - fixed) / (kDS * 2) : 0;
+    const size_t vcap = std::min<size_t>(room / 64 * 64, (max_len + 63) / 64 * 64);
+    if (vcap < 64)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu positions x %zu heads per kv head exceed LDS", fn, max_len, rep);
+    const size_t lds = fixed + vcap * kDS * 2;
+    const size_t cache_bytes = d.num_blocks * d.block_size * d.n_kv_heads * D * 2;
+    rc = check_device_buffer(q, d.S * d.n_heads * D * 2, "q", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(k_cache, cache_bytes, "k_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(v_cache, cache_bytes, "v_cache", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(block_ids, n_tables * d.n_block_ids * 4, "block_ids", fn);
+    if (rc == ECPU_OK) rc = check_device_buffer(out, d.S * d.n_heads * D * 2, "out", fn);
+    if (rc != ECPU_OK) return rc;
+    const dim3 grid((unsigned)d.n_kv_heads, (unsigned)d.S, (unsigned)(D / kDS));
+    const float scale = (float)(1.0 / __builtin_sqrt((double)D));
+    hipStream_t st = current_stream();
+#define PILM_ATTN_BATCH(DD)                                                                                         \
+    attn_exact_kernel<DD, BatchRows><<<grid, 256, lds, st>>>(q, k_cache, v_cache, block_ids, (int)d.n_block_ids,  \
+                                                             (int)d.num_blocks, (int)d.block_size, gate,            \
+                                                             d.gate_row_stride, d.gate_head_stride, nullptr, 0, 0,  \
+                                                             (int)d.n_heads, (int)d.n_kv_heads, (int)max_len,       \
+                                                             (int)vcap, scale, out, br)
+    if (D == 64) PILM_ATTN_BATCH(64);
+    else if (D == 128) PILM_ATTN_BATCH(128);
+    else PILM_ATTN_BATCH(256);
+#undef PILM_ATTN_BATCH
     return check_launch(fn);
 }
 

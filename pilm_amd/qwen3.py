@@ -262,17 +262,32 @@ class Qwen3Decoder:
         """The model over the m tokens in self.x.  groups None: one sequence at
         the positions the state word names (graph-capturable); with_logits:
         final norm + lm_head of the last token and the greedy step.  groups:
-        [(row0, rows, pos0, block table)] -- several sequences' rows in one
-        batch, positions from the host; the linears take all m rows at once
-        and with_logits gives the logits of every row (self.logits_rows)."""
+        [(row0, rows, pos0, block table[, sequence])] -- several sequences'
+        rows in one batch, positions from the host; the linears take all m
+        rows at once and with_logits gives the logits of every row
+        (self.logits_rows).  With the sequence index (the row of its table in
+        self.tables_all) rope and attention take every sequence's rows in one
+        launch each; otherwise one pair of launches per sequence."""
         c, L = self.cfg, self.lib
         D, Hq, Hkv, I = c.head_dim, c.heads, c.kv_heads, c.intermediate
         qkv_p = self.qkv.data_ptr()
         k_off, v_off = 2 * Hq * D * 2, (2 * Hq * D + Hkv * D) * 2
+        batch = None
         if groups is None:
             groups_run = [(0, m, None, self.block_ids)]
         else:
-            groups_run = groups
+            groups_run = [g[:4] for g in groups]
+            tables_all = getattr(self, "tables_all", None)
+            if tables_all is not None and len(groups[0]) == 5 and m <= 128:
+                n_tables = len(self.tables)
+                per = tables_all.numel() // n_tables
+                seqs = (abi.EkernelBatchSeq * len(groups))(
+                    *[abi.EkernelBatchSeq(r0, n, pos0, sq) for (r0, n, pos0, _, sq) in groups])
+                rope_b = abi.EkernelQkRopeDesc(m, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, 0, self.max_pos,
+                                               c.block_size, self.pool, per, c.eps)
+                att_b = abi.EkernelAttentionExactDesc(m, Hq, Hkv, D, 0, c.block_size, self.pool, per, self.nqkv,
+                                                      2 * D)
+                batch = (seqs, len(groups), rope_b, att_b, tables_all, n_tables)
         res_in = None
         for li, Lw in enumerate(self.w.layers):
             if li == 0:
@@ -282,36 +297,51 @@ class Qwen3Decoder:
                 self._norm(self.mlp, self.res, Lw["in_norm"], self.h, self.res, m)
                 res_in = self.res
             self._linear(self.h, Lw["qkv"], self.qkv, m)
-            for (r0, n, pos0, table) in groups_run:
-                def mk_rope():
-                    return abi.EkernelQkRopeDesc(n, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, pos0 or 0,
-                                                 self.max_pos, c.block_size, self.pool, table.numel(), c.eps)
+            if batch is not None:
+                # every sequence's rows in one rope launch and one attention launch
+                seqs, nseq, rope_b, att_b, tables_all, n_tables = batch
+                q_p = self.q.data_ptr()
+                self._check(L.ekernel_qk_norm_rope_batch_bf16(
+                    ctypes.byref(rope_b), seqs, nseq, n_tables, ctypes.c_void_p(qkv_p), ctypes.c_void_p(qkv_p + k_off),
+                    ctypes.c_void_p(qkv_p + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos),
+                    _vp(self.sin), ctypes.c_void_p(q_p), _vp(self.k_cache[li]), _vp(self.v_cache[li]),
+                    _vp(tables_all)), "ekernel_qk_norm_rope_batch_bf16")
+                self._check(L.ekernel_attention_exact_batch_bf16(
+                    ctypes.byref(att_b), seqs, nseq, n_tables, ctypes.c_void_p(q_p), _vp(self.k_cache[li]),
+                    _vp(self.v_cache[li]), _vp(tables_all), ctypes.c_void_p(qkv_p + D * 2),
+                    _vp(self.attn)), "ekernel_attention_exact_batch_bf16")
+            else:
+                for (r0, n, pos0, table) in groups_run:
+                    def mk_rope():
+                        return abi.EkernelQkRopeDesc(n, Hq, Hkv, D, c.rot_dim, self.nqkv, self.nqkv, pos0 or 0,
+                                                     self.max_pos, c.block_size, self.pool, table.numel(), c.eps)
 
-                def mk_att():
-                    return abi.EkernelAttentionExactDesc(n, Hq, Hkv, D, (pos0 or 0) + n, c.block_size, self.pool,
-                                                         table.numel(), self.nqkv, 2 * D)
-                # one sequence's descriptors are reused; batch positions change every step
-                rope = self._desc(("rope", n), mk_rope) if pos0 is None else mk_rope()
-                att = self._desc(("attn", n), mk_att) if pos0 is None else mk_att()
-                step = self.state if pos0 is None else None
-                rp = qkv_p + r0 * self.nqkv * 2
-                if n == 1 and self.fused_decode:
-                    # one decode row: norm, rope, cache write and attention in one launch
-                    self._check(L.ekernel_decode_attention_bf16(
+                    def mk_att():
+                        return abi.EkernelAttentionExactDesc(n, Hq, Hkv, D, (pos0 or 0) + n, c.block_size, self.pool,
+                                                             table.numel(), self.nqkv, 2 * D)
+                    # one sequence's descriptors are reused; batch positions change every step
+                    rope = self._desc(("rope", n), mk_rope) if pos0 is None else mk_rope()
+                    att = self._desc(("attn", n), mk_att) if pos0 is None else mk_att()
+                    step = self.state if pos0 is None else None
+                    rp = qkv_p + r0 * self.nqkv * 2
+                    if n == 1 and self.fused_decode:
+                        # one decode row: norm, rope, cache write and attention in one launch
+                        self._check(L.ekernel_decode_attention_bf16(
+                            ctypes.byref(rope), ctypes.c_void_p(rp), ctypes.c_void_p(rp + k_off),
+                            ctypes.c_void_p(rp + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos),
+                            _vp(self.sin), _vp(step), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(table),
+                            ctypes.c_void_p(self.attn.data_ptr() + r0 * Hq * D * 2)), "ekernel_decode_attention_bf16")
+                        continue
+                    self._check(L.ekernel_qk_norm_rope_bf16(
                         ctypes.byref(rope), ctypes.c_void_p(rp), ctypes.c_void_p(rp + k_off),
                         ctypes.c_void_p(rp + v_off), _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos),
-                        _vp(self.sin), _vp(step), _vp(self.k_cache[li]), _vp(self.v_cache[li]), _vp(table),
-                        ctypes.c_void_p(self.attn.data_ptr() + r0 * Hq * D * 2)), "ekernel_decode_attention_bf16")
-                    continue
-                self._check(L.ekernel_qk_norm_rope_bf16(
-                    ctypes.byref(rope), ctypes.c_void_p(rp), ctypes.c_void_p(rp + k_off), ctypes.c_void_p(rp + v_off),
-                    _vp(Lw["q_norm"]), _vp(Lw["k_norm"]), _vp(self.cos), _vp(self.sin), _vp(step),
-                    ctypes.c_void_p(self.q.data_ptr() + r0 * Hq * D * 2), _vp(self.k_cache[li]),
-                    _vp(self.v_cache[li]), _vp(table)), "ekernel_qk_norm_rope_bf16")
-                self._check(L.ekernel_attention_exact_bf16(
-                    ctypes.byref(att), ctypes.c_void_p(self.q.data_ptr() + r0 * Hq * D * 2), _vp(self.k_cache[li]),
-                    _vp(self.v_cache[li]), _vp(table), ctypes.c_void_p(rp + D * 2), _vp(step),
-                    ctypes.c_void_p(self.attn.data_ptr() + r0 * Hq * D * 2)), "ekernel_attention_exact_bf16")
+                        _vp(self.sin), _vp(step),
+                        ctypes.c_void_p(self.q.data_ptr() + r0 * Hq * D * 2), _vp(self.k_cache[li]),
+                        _vp(self.v_cache[li]), _vp(table)), "ekernel_qk_norm_rope_bf16")
+                    self._check(L.ekernel_attention_exact_bf16(
+                        ctypes.byref(att), ctypes.c_void_p(self.q.data_ptr() + r0 * Hq * D * 2), _vp(self.k_cache[li]),
+                        _vp(self.v_cache[li]), _vp(table), ctypes.c_void_p(rp + D * 2), _vp(step),
+                        ctypes.c_void_p(self.attn.data_ptr() + r0 * Hq * D * 2)), "ekernel_attention_exact_bf16")
             self._linear(self.attn, Lw["o"], self.o, m)
             self._norm(self.o, res_in, Lw["post_norm"], self.h, self.res, m)
             self._linear(self.h, Lw["gate_up"], self.gu, m)
@@ -442,8 +472,8 @@ class Qwen3Batch(Qwen3Decoder):
         per_seq = (max_positions + bs - 1) // bs
         super().__init__(weights, max_positions, max_new_tokens=1, max_rows=max_rows,
                          pool_blocks=per_seq * n_seqs)
-        self.tables = [torch.arange(i * per_seq, (i + 1) * per_seq, dtype=torch.int32, device=self.dev)
-                       for i in range(n_seqs)]
+        self.tables_all = torch.arange(n_seqs * per_seq, dtype=torch.int32, device=self.dev)
+        self.tables = [self.tables_all[i * per_seq:(i + 1) * per_seq] for i in range(n_seqs)]
         self.cache_len = [0] * n_seqs
 
     def _run(self, groups_tokens, with_logits: bool):
@@ -457,7 +487,7 @@ class Qwen3Batch(Qwen3Decoder):
             pos0 = self.cache_len[seq]
             if pos0 + len(toks) > self.max_pos:
                 raise ValueError(f"sequence {seq} would exceed {self.max_pos} positions")
-            groups.append((r0, len(toks), pos0, self.tables[seq]))
+            groups.append((r0, len(toks), pos0, self.tables[seq], seq))
             r0 += len(toks)
         prev = abi.matrix_core_min_rows()
         abi.set_matrix_core_min_rows(0)          # 0: exact kernels at every M

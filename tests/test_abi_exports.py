@@ -59,7 +59,7 @@ def test_library_loads_and_configures(lib_path):
         "ekernel_linear_w4a16g32_bf16", "ekernel_linear_w4a16g128_bf16", "ekernel_swiglu_bf16",
         "ekernel_linear_w8a16_bf16_argmax", "ekernel_swiglu_w4a16_bf16", "ekernel_rmsnorm_gemma_bf16",
         "ekernel_qk_norm_rope_bf16", "ekernel_attention_exact_bf16", "ekernel_silu_mul_bf16",
-        "ekernel_greedy_step_bf16"))
+        "ekernel_greedy_step_bf16", "ekernel_qk_norm_rope_batch_bf16", "ekernel_attention_exact_batch_bf16"))
     vt = lib.edevice_get  # exported registry accessor
     assert vt is not None
 
@@ -78,6 +78,8 @@ def test_descriptor_layout_matches_reference():
     assert ctypes.sizeof(abi.EkernelAttentionExactDesc) == 80
     assert abi.EkernelNormLinearDesc.eps.offset == 24 and abi.EkernelNormLinearDesc.swiglu.offset == 28
     assert ctypes.sizeof(abi.EkernelNormLinearDesc) == 32
+    # ekernel_batch_seq_t: four int32
+    assert ctypes.sizeof(abi.EkernelBatchSeq) == 16 and abi.EkernelBatchSeq.table.offset == 12
 
 
 def test_missing_symbol_fails_loudly(tmp_path, monkeypatch):

@@ -251,6 +251,106 @@ def test_qk_rope_then_attention(lib, dev, S, H, Hkv, D, pos0):
         assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()} (step={use_step})"
 
 
+@pytest.mark.parametrize("H,Hkv,D,plan", [
+    (16, 8, 128, [(5, 130), (5, 0), (1, 47), (5, 16), (3, 2), (5, 255), (1, 0), (4, 60)]),
+    (32, 8, 128, [(5, 300), (5, 31), (5, 0), (5, 511)]),
+    (8, 8, 64, [(2, 3), (7, 40), (1, 1)]),
+    (16, 8, 128, [(5, p) for p in range(0, 256, 16)]),                   # 16 sequences x 5 rows: M = 80
+])
+def test_rope_attention_batch_matches_per_sequence(lib, dev, H, Hkv, D, plan):
+    """ekernel_qk_norm_rope_batch_bf16 + ekernel_attention_exact_batch_bf16:
+    several sequences (rows, pos0) with their own block tables in one shared
+    pool, listed out of table order, in one call each; every q row, cache row
+    and output row equal to the oracle's per-sequence steps."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(len(plan) * 131 + H + D)
+    bs, nseq = 16, len(plan)
+    per = max((p + n + bs - 1) // bs for n, p in plan) + 1         # blocks per table
+    nphys = nseq * per + 5
+    perm = rng.permutation(nphys).astype(np.int32)
+    tables = perm[:nseq * per].reshape(nseq, per)                  # disjoint physical blocks per sequence
+    kc = _rand16(rng, (nphys, bs, Hkv, D))
+    vc = _rand16(rng, (nphys, bs, Hkv, D))
+    rows = sum(n for n, _ in plan)
+    width = (2 * H + 2 * Hkv) * D
+    qkv = _rand16(rng, (rows, width))
+    qw, kw = _rand16(rng, (D,), 0.02), _rand16(rng, (D,), 0.02)
+    max_pos = per * bs
+    cos, sin = OD.rope_tables(1e6, D, max_pos)
+    order = rng.permutation(nseq)          # batch rows follow this order; sequence i keeps table i
+    row0, r = {}, 0
+    for i in order:
+        row0[i] = r
+        r += plan[i][0]
+    kc_o, vc_o = kc.copy(), vc.copy()
+    q_want = np.zeros((rows, H, D), dtype=np.uint16)
+    out_want = np.zeros((rows, H * D), dtype=np.uint16)
+    for i in range(nseq):
+        n, p0 = plan[i]
+        blk = qkv[row0[i]:row0[i] + n]
+        qg, k, v = blk[:, :2 * H * D], blk[:, 2 * H * D:2 * H * D + Hkv * D], blk[:, 2 * H * D + Hkv * D:]
+        qi = OD.qk_norm_rope_bf16(qg, k, v, qw, kw, cos, sin, p0, kc_o, vc_o, tables[i], n_heads=H, n_kv_heads=Hkv,
+                                  head_dim=D, rot_dim=D, eps=1e-6, block_size=bs)
+        q_want[row0[i]:row0[i] + n] = qi.reshape(n, H, D)
+        gate = blk.reshape(-1)[D:]
+        out_want[row0[i]:row0[i] + n] = OD.attention_exact_bf16(qi, kc_o, vc_o, tables[i], p0 + n, gate, width,
+                                                                2 * D, block_size=bs).reshape(n, H * D)
+    qkv_d, kc_d, vc_d = _dev16(qkv, dev), _dev16(kc, dev), _dev16(vc, dev)
+    tab_d = torch.from_numpy(tables.reshape(-1).copy()).to(dev)
+    cos_d, sin_d = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    qw_d, kw_d = _dev16(qw, dev), _dev16(kw, dev)
+    q_d = torch.empty((rows, H, D), dtype=torch.bfloat16, device=dev)
+    out_d = torch.empty((rows, H * D), dtype=torch.bfloat16, device=dev)
+    seqs = (abi.EkernelBatchSeq * nseq)(*[abi.EkernelBatchSeq(row0[i], plan[i][0], plan[i][1], i) for i in order])
+    _say(f"[gpu] batched rope + attention H={H} Hkv={Hkv} D={D} {nseq} sequences, {rows} rows")
+    _bind()
+    p = qkv_d.data_ptr()
+    rd = abi.EkernelQkRopeDesc(rows, H, Hkv, D, D, width, width, 0, max_pos, bs, nphys, per, 1e-6)
+    rc = lib.ekernel_qk_norm_rope_batch_bf16(ctypes.byref(rd), seqs, nseq, nseq, ctypes.c_void_p(p),
+                                             ctypes.c_void_p(p + 2 * H * D * 2),
+                                             ctypes.c_void_p(p + (2 * H * D + Hkv * D) * 2), _vp(qw_d), _vp(kw_d),
+                                             _vp(cos_d), _vp(sin_d), _vp(q_d), _vp(kc_d), _vp(vc_d), _vp(tab_d))
+    assert rc == 0, abi.last_error()
+    assert np.array_equal(_bits(q_d), q_want)
+    assert np.array_equal(_bits(kc_d), kc_o) and np.array_equal(_bits(vc_d), vc_o)
+    ad = abi.EkernelAttentionExactDesc(rows, H, Hkv, D, 0, bs, nphys, per, width, 2 * D)
+    rc = lib.ekernel_attention_exact_batch_bf16(ctypes.byref(ad), seqs, nseq, nseq, _vp(q_d), _vp(kc_d), _vp(vc_d),
+                                                _vp(tab_d), ctypes.c_void_p(p + D * 2), _vp(out_d))
+    assert rc == 0, abi.last_error()
+    got = _bits(out_d)
+    bad = np.argwhere(got != out_want)
+    assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()}"
+
+
+def test_rope_attention_batch_rejects_bad_tables(lib, dev):
+    """Rows in two sequences or in none, a table index beyond n_tables,
+    positions beyond the tables and more than 128 rows are refused before
+    anything is launched."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    H, Hkv, D, bs, per, nphys = 4, 2, 64, 16, 4, 16
+    buf = torch.zeros(1 << 20, dtype=torch.bfloat16, device=dev)
+    tab = torch.arange(8, dtype=torch.int32, device=dev)
+    p = buf.data_ptr()
+
+    def att(rows, plan, n_tables=2):
+        seqs = (abi.EkernelBatchSeq * len(plan))(*[abi.EkernelBatchSeq(*x) for x in plan])
+        ad = abi.EkernelAttentionExactDesc(rows, H, Hkv, D, 0, bs, nphys, per, 0, 0)
+        return lib.ekernel_attention_exact_batch_bf16(ctypes.byref(ad), seqs, len(plan), n_tables,
+                                                      ctypes.c_void_p(p), ctypes.c_void_p(p + 65536),
+                                                      ctypes.c_void_p(p + 131072), _vp(tab), None,
+                                                      ctypes.c_void_p(p + 262144))
+    _bind()
+    assert att(4, [(0, 2, 0, 0), (2, 2, 5, 1)]) == 0
+    assert att(4, [(0, 3, 0, 0), (2, 2, 5, 1)]) == abi.ECPU_ERR_PARAM          # row 2 in two sequences
+    assert att(5, [(0, 2, 0, 0), (2, 2, 5, 1)]) == abi.ECPU_ERR_PARAM          # row 4 in none
+    assert att(4, [(0, 2, 0, 0), (2, 2, 5, 2)]) == abi.ECPU_ERR_PARAM          # table 2 of 2
+    assert att(4, [(0, 2, 0, 0), (2, 2, 63, 1)]) == abi.ECPU_ERR_PARAM         # positions 63, 64 of 64
+    assert att(130, [(0, 130, 0, 0)], 1) == abi.ECPU_ERR_UNSUPPORTED           # more than 128 rows
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("H,Hkv,D,pos0", [(16, 8, 128, 383), (16, 8, 128, 0), (16, 8, 128, 1), (16, 8, 128, 2),
                                           (16, 8, 128, 3), (16, 8, 128, 7), (16, 8, 128, 64), (32, 8, 128, 2043),
                                           (4, 2, 128, 0), (8, 8, 64, 17), (16, 4, 128, 100), (16, 8, 128, 4000),
