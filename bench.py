@@ -39,7 +39,8 @@ Printed JSON line:
   sweep        per-shape times with --sweep [sections]: g128 (default),
                w4row, w8a32, w8a16, gemm, gemm_fp16 (torch's fp16 GEMM at
                the same shapes, for reference), fused, attention, load
-               (bundle -> HBM), verify (16-sequence MTP verify, M = 80), or all
+               (bundle -> HBM), verify (16-sequence MTP verify, M = 80),
+               verify_step (the whole batched verify step, Qwen3-1.7B), or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -382,6 +383,8 @@ def sweep(torch, dev, sections) -> dict:
         res["load"] = sweep_load(torch, dev)
     if "verify" in sections:
         res["verify_8b"] = sweep_verify(torch, dev)
+    if "verify_step" in sections:
+        res["verify_step_1p7b"] = sweep_verify_step(torch, dev)
     return res
 
 
@@ -411,6 +414,46 @@ def sweep_gemm_fp16(torch, dev, ms, reps: int = 20) -> dict:
         res[name] = row
         del w
     return res
+
+
+def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int = 8, prompt_len: int = 128,
+                      seed: int = 1) -> dict:
+    """One batched MTP verify step end to end on Qwen3-1.7B W4A16-g128
+    (Qwen3Batch.verify: n_seq sequences x (1 + drafts) rows through every
+    linear as one M, rope and attention for all sequences in one launch
+    each, lm_head on every row, acceptance on the host): GPU time between
+    HIP events and wall time per step after a prefill of every prompt.
+    The drafts are fixed tokens (mostly rejected): the step's work is the
+    same whatever is accepted, every row goes through the model."""
+    from pilm_amd import qwen3 as Q
+    from pilm_amd import synth_model as SM
+    cfg = Q.QWEN3_1P7B
+    w = Q.Qwen3Weights.synthetic(cfg, seed, 0.02, device=dev)
+    b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=prompt_len + (steps + 2) * (1 + drafts) + 1,
+                     max_rows=n_seq * (1 + drafts))
+    prompts = [SM.token_ids(seed + i, prompt_len, cfg.vocab).tolist() for i in range(n_seq)]
+    last = b.prefill_seqs(list(range(n_seq)), prompts)
+    drafts_of = [[0] * drafts for _ in range(n_seq)]
+    s = torch.cuda.current_stream(dev)
+    gpu_ms, wall_ms, accepted = [], [], 0
+    for it in range(steps + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(s)
+        out = b.verify(last, drafts_of)
+        e1.record(s)
+        torch.cuda.synchronize()
+        if it > 0:                                         # the first step warms the descriptors and scratch
+            wall_ms.append((time.perf_counter() - t0) * 1e3)
+            gpu_ms.append(e0.elapsed_time(e1))
+            accepted += sum(len(a) for a, _ in out)
+        last = [nxt for _, nxt in out]
+    m = n_seq * (1 + drafts)
+    g = sorted(gpu_ms)[len(gpu_ms) // 2]
+    return {"sequences": n_seq, "rows_per_step": m, "steps": steps, "gpu_ms_per_step": round(g, 3),
+            "wall_ms_per_step": round(sorted(wall_ms)[len(wall_ms) // 2], 3),
+            "rows_per_s": round(m / g * 1e3, 1), "accepted_drafts_per_step": round(accepted / steps, 1)}
 
 
 def sweep_verify(torch, dev, n_seq: int = 16, drafts: int = 4) -> dict:
@@ -1053,7 +1096,8 @@ def main(argv=None) -> int:
         out["decode"] = dec
         calls = xs = run = None
     if args.sweep:
-        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "gemm_fp16", "fused", "attention", "load", "verify") \
+        sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "gemm_fp16", "fused", "attention", "load", "verify",
+                    "verify_step") \
             if args.sweep == "all" \
             else tuple(args.sweep.split(","))
         print(f"[bench] sweeps: {', '.join(sections)}", flush=True)

@@ -447,7 +447,11 @@ def accept_drafts(logits_rows: torch.Tensor, drafts: list) -> tuple:
     when all are accepted the argmax of the last row, is the next token.
     Returns (accepted drafts, next token).  Argmax as torch.argmax on the
     fp32 copy: the first index of the largest value."""
-    ids = torch.argmax(logits_rows.to(torch.float32), dim=-1).tolist()
+    return accept_draft_ids(torch.argmax(logits_rows.to(torch.float32), dim=-1).tolist(), drafts)
+
+
+def accept_draft_ids(ids: list, drafts: list) -> tuple:
+    """accept_drafts on the rows' argmax ids already taken."""
     acc = []
     for i, d in enumerate(drafts):
         if ids[i] != int(d):
@@ -548,10 +552,12 @@ class Qwen3Batch(Qwen3Decoder):
         go through the model as one batch; returns [(accepted, next token)]
         per sequence and advances each cache past the accepted tokens."""
         groups = [(i, [int(last_tokens[i])] + [int(d) for d in drafts[i]]) for i in range(len(drafts))]
-        self._run(groups, with_logits=True)
+        rows = self._run(groups, with_logits=True)
+        # every row's argmax in one pass and one copy to the host
+        ids = torch.argmax(self.logits_rows[:rows].to(torch.float32), dim=-1).tolist()
         out, r0 = [], 0
         for (i, toks) in groups:
-            acc, nxt = accept_drafts(self.logits_rows[r0:r0 + len(toks)], drafts[i])
+            acc, nxt = accept_draft_ids(ids[r0:r0 + len(toks)], drafts[i])
             out.append((acc, nxt))
             self.cache_len[i] += 1 + len(acc)
             r0 += len(toks)
