@@ -291,6 +291,46 @@ __device__ __forceinline__ float score_dot(const float *qr, const uint32_t (&kv)
     return p[0];
 }
 
+// One wave turns the bf16 scores x[0 .. vis) of a row (cache_len positions
+// long with the masked ones) into bf16 softmax weights in place: max, exp,
+// the sum in torch's order (eight chains j = c mod 8 folded as ((0+4) +
+// (2+6)) + ((1+5) + (3+7)); one plain chain below eight positions), then
+// x * (1 / sum) rounded to bf16.
+__device__ __forceinline__ void softmax_weights(float *x, int vis, int cache_len, int lane) {
+    float mx = -__builtin_inff();
+    for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float sum = 0.0f;
+    if (cache_len >= 8) {
+        // lane c < 8: chain c = positions j = c mod 8, in order from x[c]
+        float a = 0.0f;
+        if (lane < 8) {
+            a = lane < vis ? x[lane] : 0.0f;
+            int j = lane + 8;
+            for (; j + 56 < vis; j += 64) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = x[j + 8 * u];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a = a + v[u];
+            }
+            for (; j < vis; j += 8) a = a + x[j];
+        }
+        const float b = a + __shfl_xor(a, 4);    // lanes c < 4: (c) + (c + 4)
+        const float c = b + __shfl_xor(b, 2);    // ((0+4) + (2+6)), ((1+5) + (3+7))
+        sum = __shfl(c + __shfl_xor(c, 1), 0);
+    } else {
+        for (int j = 0; j < vis; ++j) sum = sum + x[j];
+    }
+    const float inv = __fdiv_rn(1.0f, sum);
+    for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
+}
+
 template <int D>
 __device__ __forceinline__ void load_krow(const uint16_t *kr, uint32_t (&kv)[D / 2]) {
 #pragma unroll
@@ -394,41 +434,7 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
     __syncthreads();
 
     // softmax per head: wave r (looping when rep exceeds the wave count)
-    for (int r = wave; r < rep; r += blockDim.x / 64) {
-        float *x = sc + (size_t)r * scs;
-        float mx = -__builtin_inff();
-        for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float sum = 0.0f;
-        if (cache_len >= 8) {
-            // lane c < 8: chain c = positions j = c mod 8, in order from x[c]
-            float a = 0.0f;
-            if (lane < 8) {
-                a = lane < vis ? x[lane] : 0.0f;
-                int j = lane + 8;
-                for (; j + 56 < vis; j += 64) {
-                    float v[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) v[u] = x[j + 8 * u];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) a = a + v[u];
-                }
-                for (; j < vis; j += 8) a = a + x[j];
-            }
-            const float b = a + __shfl_xor(a, 4);    // lanes c < 4: (c) + (c + 4)
-            const float c = b + __shfl_xor(b, 2);    // ((0+4) + (2+6)), ((1+5) + (3+7))
-            sum = __shfl(c + __shfl_xor(c, 1), 0);
-        } else {
-            for (int j = 0; j < vis; ++j) sum = sum + x[j];
-        }
-        const float inv = __fdiv_rn(1.0f, sum);
-        for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
-    }
+    for (int r = wave; r < rep; r += blockDim.x / 64) softmax_weights(sc + (size_t)r * scs, vis, cache_len, lane);
 
     // P.V: thread (r, column c, chain k) over the staged value rows
     const int main_len = naive ? 0 : (cache_len / 4) * 4;
@@ -485,6 +491,188 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
                 o = o * bfr(__fdiv_rn(1.0f, 1.0f + sleef_expf(-g)));
             }
             out[((size_t)s * H + h) * D + d] = f32_to_bf16(o);
+        }
+    }
+}
+
+// ---- attention over several rows of one sequence ----------------------------
+// Continuous batching: a workgroup serves one kv head for a tile of
+// consecutive rows of one sequence (rows x rep <= kTileVecs (row, q head)
+// vectors), so each key row is loaded once per tile and each score is
+// computed once, over the full head width.  Every vector gets exactly what
+// attn_exact_kernel computes for its row: the same score order and roundings,
+// softmax_weights, the same four P.V chains over the positions the row sees
+// (j = k mod 4 below the last multiple of four of cache_len, the tail on
+// chain 0), the fold ((p0 + p1) + p2) + p3 and the gate.
+// Threads: scores by (position, vector parity); P.V by (vector group g,
+// column pair, chain k), the four chains of a column pair in adjacent lanes.
+constexpr int kTileVecs = 16;
+constexpr int kTileThreads = 512;
+
+struct BatchTiles {
+    int32_t tile[kMaxBatchRows];       // first batch row | rows << 16
+};
+
+template <int D, int NV>
+__global__ __launch_bounds__(kTileThreads) void attn_tile_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache,
+    const int32_t *__restrict__ block_ids, int n_block_ids, int num_blocks, int block_size,
+    const uint16_t *__restrict__ gate, size_t gate_row_stride, size_t gate_head_stride, int H, int Hkv,
+    int max_len, int vecs, int scs, int vcap, float scale, uint16_t *__restrict__ out, BatchRows rows,
+    BatchTiles tiles) {
+    constexpr int CP = D / 2;                        // column pairs
+    constexpr int G = kTileThreads / (4 * CP);       // vector groups of the P.V pass
+    static_assert(NV >= 1 && NV * G <= kTileVecs, "vectors per P.V thread");
+    constexpr int QS = D + 4;                        // q row stride: the vectors on different banks
+    constexpr int PPR = D / 8;                       // 16-byte pieces per value row
+    extern __shared__ float lds[];
+    const int kh = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int rep = H / Hkv;
+    const int row0 = tiles.tile[blockIdx.y] & 0xFFFF, nr = tiles.tile[blockIdx.y] >> 16;
+    const int RR = nr * rep;
+    const int S = max(rows.nrows[row0], 1);
+    const int cache_len = min(max(rows.len[row0], S), max_len);
+    auto vis_of = [&](int rr) {                      // visible positions of vector rr's row
+        return min(max(rows.pos[row0 + rr / rep], cache_len - S), cache_len - 1) + 1;
+    };
+    const int vis_min = vis_of(0), vis_max = vis_of(RR - 1);
+    const bool naive = (long long)S * cache_len * D < 400;
+    const int main_len = naive ? 0 : (cache_len / 4) * 4;
+    block_ids += rows.tbl[row0];
+    // P.V thread: vectors g + n G (n < NV; the ones past RR compute on a
+    // clamped row and are dropped), columns 2 cp, 2 cp + 1, chain k.  Its
+    // gate values are fetched now, not after the sums.
+    const int k = t & 3, cp = (t >> 2) % CP, g = t / (4 * CP);
+    float gv[NV][2];
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int rr = g + n * G;
+        gv[n][0] = gv[n][1] = 0.0f;
+        if (gate && k == 0 && rr < RR) {
+            const uint16_t *gp = gate + (size_t)(row0 + rr / rep) * gate_row_stride +
+                                 (size_t)(kh * rep + rr % rep) * gate_head_stride + 2 * cp;
+            gv[n][0] = bf(gp[0]);
+            gv[n][1] = bf(gp[1]);
+        }
+    }
+    float *qs = lds;                                             // [vecs][QS]
+    float *sc = qs + (size_t)vecs * QS;                          // [vecs][scs]
+    int *bids = (int *)(sc + (size_t)vecs * scs);                // [n_block_ids]
+    uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [vcap][D]
+    for (int i = t; i < n_block_ids; i += kTileThreads) bids[i] = min(max(block_ids[i], 0), num_blocks - 1);
+    for (int i = t; i < RR * D; i += kTileThreads) {
+        const int rr = i / D, d = i % D;
+        qs[rr * QS + d] = bf(q[((size_t)(row0 + rr / rep) * H + kh * rep + rr % rep) * D + d]);
+    }
+    __syncthreads();
+
+    auto row_of = [&](int j) -> size_t {
+        const int blk = bids[min(j / block_size, n_block_ids - 1)];
+        return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
+    };
+    // value rows [j0, j0 + vcap) into vs, 16 bytes per lane; whole
+    // instructions of every wave, pieces past the rows repeat the last row
+    auto stage_v = [&](int j0) {
+        const int nrows = min(vcap, vis_max - j0);
+        const int pieces = ((nrows * PPR + kTileThreads - 1) / kTileThreads) * kTileThreads;
+        for (int base = 0; base < pieces; base += kTileThreads) {
+            const int idx = base + t;
+            const int j = j0 + min(idx / PPR, nrows - 1);
+            const uint16_t *src = v_cache + row_of(j) + 8 * (idx % PPR);
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(vs + (size_t)(base + wave * 64) * 8), 16,
+                                             0, 0);
+        }
+    };
+    stage_v(0);
+
+    // scores: thread (position j, vector parity); the key row stays in registers
+    for (int j = t % 256; j < vis_max; j += 256) {
+        uint32_t ka[D / 2];
+        load_krow<D>(k_cache + row_of(j), ka);
+        for (int rr = t / 256; rr < RR; rr += kTileThreads / 256)
+            if (j < vis_of(rr)) sc[(size_t)rr * scs + j] = bfr(bfr(score_dot<D>(qs + rr * QS, ka, naive)) * scale);
+    }
+    __syncthreads();
+    for (int rr = wave; rr < RR; rr += kTileThreads / 64) softmax_weights(sc + (size_t)rr * scs, vis_of(rr), cache_len, lane);
+
+    // P.V
+    int visv[NV], wo[NV];
+    float acc[NV][2];
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int rr = g + n * G;
+        visv[n] = rr < RR ? vis_of(rr) : 0;
+        wo[n] = min(rr, RR - 1) * scs;
+        acc[n][0] = acc[n][1] = 0.0f;
+    }
+    const uint32_t *vw = (const uint32_t *)vs;
+    for (int j0 = 0; j0 < vis_max; j0 += vcap) {
+        if (j0 > 0) {
+            __syncthreads();              // every wave is done with the previous rows
+            stage_v(j0);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();                  // every wave's copies (and the weights) are in
+        const int j1 = min(vis_max, j0 + vcap);
+        // every vector of the tile sees j: no condition
+        auto step_all = [&](int j) {
+            const uint32_t vp = vw[(j - j0) * CP + cp];
+            const float v0 = bf16_lo(vp), v1 = bf16_hi(vp);
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                const float w = sc[wo[n] + j];
+                acc[n][0] = __builtin_fmaf(w, v0, acc[n][0]);
+                acc[n][1] = __builtin_fmaf(w, v1, acc[n][1]);
+            }
+        };
+        // only the vectors whose row sees j take it
+        auto step_masked = [&](int j) {
+            const uint32_t vp = vw[(j - j0) * CP + cp];
+            const float v0 = bf16_lo(vp), v1 = bf16_hi(vp);
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                const float w = sc[wo[n] + j];
+                const bool on = j < visv[n];
+                acc[n][0] = on ? __builtin_fmaf(w, v0, acc[n][0]) : acc[n][0];
+                acc[n][1] = on ? __builtin_fmaf(w, v1, acc[n][1]) : acc[n][1];
+            }
+        };
+        if (naive) {
+            if (k == 0)
+                for (int j = j0; j < j1; ++j) step_masked(j);
+        } else {
+            int j = j0 + ((k - j0) & 3);
+            const int jm = min(j1, main_len);
+            const int ja = min(jm, vis_min);
+#pragma unroll 2
+            for (; j < ja; j += 4) step_all(j);
+            for (; j < jm; j += 4) step_masked(j);
+            if (k == 0)
+                for (j = max(j0, main_len); j < j1; ++j) step_masked(j);
+        }
+    }
+
+    // fold the four chains of each column (adjacent lanes), gate, store
+    const int lb = lane & ~3;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int rr = g + n * G;
+        if (rr >= RR) break;
+        float o[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const float a0 = acc[n][c];
+            const float a1 = __shfl(a0, lb + 1), a2 = __shfl(a0, lb + 2), a3 = __shfl(a0, lb + 3);
+            o[c] = bfr(naive ? a0 : ((a0 + a1) + a2) + a3);
+        }
+        if (k == 0) {
+            const int row = row0 + rr / rep, h = kh * rep + rr % rep, d = 2 * cp;
+            if (gate) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) o[c] = o[c] * bfr(__fdiv_rn(1.0f, 1.0f + sleef_expf(-gv[n][c])));
+            }
+            *(uint32_t *)(out + ((size_t)row * H + h) * D + d) =
+                (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
         }
     }
 }
@@ -1129,13 +1317,6 @@ int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *des
     int rc = build_batch_rows(seqs, n_seqs, d.S, n_tables, d.n_block_ids, max_len, br, fn);
     if (rc != ECPU_OK) return rc;
     const size_t rep = d.n_heads / d.n_kv_heads, D = d.head_dim;
-    const size_t fixed = (rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * kDS * 4 +
-                          ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
-    const size_t room = fixed < 64 * 1024 ? (64 * 1024 - fixed) / (kDS * 2) : 0;
-    const size_t vcap = std::min<size_t>(room / 64 * 64, (max_len + 63) / 64 * 64);
-    if (vcap < 64)
-        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu positions x %zu heads per kv head exceed LDS", fn, max_len, rep);
-    const size_t lds = fixed + vcap * kDS * 2;
     const size_t cache_bytes = d.num_blocks * d.block_size * d.n_kv_heads * D * 2;
     rc = check_device_buffer(q, d.S * d.n_heads * D * 2, "q", fn);
     if (rc == ECPU_OK) rc = check_device_buffer(k_cache, cache_bytes, "k_cache", fn);
@@ -1143,10 +1324,89 @@ int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *des
     if (rc == ECPU_OK) rc = check_device_buffer(block_ids, n_tables * d.n_block_ids * 4, "block_ids", fn);
     if (rc == ECPU_OK) rc = check_device_buffer(out, d.S * d.n_heads * D * 2, "out", fn);
     if (rc != ECPU_OK) return rc;
-    const dim3 grid((unsigned)d.n_kv_heads, (unsigned)d.S, (unsigned)(D / kDS));
     const float scale = (float)(1.0 / __builtin_sqrt((double)D));
     hipStream_t st = current_stream();
-#define PILM_ATTN_BATCH(DD)                                                                                         \
+    if ((D == 64 || D == 128) && rep <= (size_t)kTileVecs && env_int("PILM_HIP_ATTN_TILE", 1) != 0) {
+        // tiles of at most rt rows per sequence: the most rows per tile that
+        // still give 256 workgroups (else one row per tile), fewer if the
+        // scores do not fit the LDS budget
+        int longest = 1, most = 1;
+        for (size_t i = 0; i < n_seqs; ++i) {
+            longest = std::max(longest, seqs[i].pos0 + seqs[i].rows);
+            most = std::max(most, seqs[i].rows);
+        }
+        const int rt_max = std::min((int)(kTileVecs / rep), most);
+        int rt = env_int("PILM_HIP_ATTN_TILE_ROWS", 0);
+        if (rt <= 0) {
+            rt = 1;
+            for (int c = rt_max; c > 1; --c) {
+                size_t n = 0;
+                for (size_t i = 0; i < n_seqs; ++i) n += (size_t)(seqs[i].rows + c - 1) / c;
+                if (n * d.n_kv_heads >= 256) {
+                    rt = c;
+                    break;
+                }
+            }
+        }
+        const size_t scs = ((size_t)longest + 3) & ~(size_t)3, budget = 64 * 1024;
+        for (rt = std::min(rt, rt_max); rt >= 1; --rt) {
+            BatchTiles bt;
+            int n_tiles = 0, widest = 0;
+            for (size_t i = 0; i < n_seqs; ++i) {
+                const int nrow = seqs[i].rows, nt = (nrow + rt - 1) / rt, per = (nrow + nt - 1) / nt;
+                for (int r = 0; r < nrow; r += per) {
+                    const int m = std::min(per, nrow - r);
+                    bt.tile[n_tiles++] = (seqs[i].row0 + r) | (m << 16);
+                    widest = std::max(widest, m);
+                }
+            }
+            const size_t vecs = (size_t)widest * rep;
+            const size_t fixed = (vecs * (D + 4) + vecs * scs + ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
+            if (fixed >= budget) continue;
+            const size_t vcap = std::min((budget - fixed) / (D * 2) / 64 * 64, ((size_t)longest + 63) / 64 * 64);
+            if (vcap < 64) continue;
+            const size_t lds = fixed + vcap * D * 2;
+            const dim3 tgrid((unsigned)d.n_kv_heads, (unsigned)n_tiles);
+            // vectors per P.V thread: the widest tile's over the vector groups
+            const int nv = (int)((vecs + (kTileThreads / (2 * D)) - 1) / (kTileThreads / (2 * D)));
+#define PILM_ATTN_TILE(DD, NVV)                                                                                     \
+    attn_tile_kernel<DD, NVV><<<tgrid, kTileThreads, lds, st>>>(                                                    \
+        q, k_cache, v_cache, block_ids, (int)d.n_block_ids, (int)d.num_blocks, (int)d.block_size, gate,             \
+        d.gate_row_stride, d.gate_head_stride, (int)d.n_heads, (int)d.n_kv_heads, (int)max_len, (int)vecs,          \
+        (int)scs, (int)vcap, scale, out, br, bt)
+            if (D == 64) {
+                switch (nv) {
+                case 1: PILM_ATTN_TILE(64, 1); break;
+                case 2: PILM_ATTN_TILE(64, 2); break;
+                case 3: PILM_ATTN_TILE(64, 3); break;
+                default: PILM_ATTN_TILE(64, 4); break;
+                }
+            } else {
+                switch (nv) {
+                case 1: PILM_ATTN_TILE(128, 1); break;
+                case 2: PILM_ATTN_TILE(128, 2); break;
+                case 3: PILM_ATTN_TILE(128, 3); break;
+                case 4: PILM_ATTN_TILE(128, 4); break;
+                case 5: PILM_ATTN_TILE(128, 5); break;
+                case 6: PILM_ATTN_TILE(128, 6); break;
+                case 7: PILM_ATTN_TILE(128, 7); break;
+                default: PILM_ATTN_TILE(128, 8); break;
+                }
+            }
+#undef PILM_ATTN_TILE
+            return check_launch(fn);
+        }
+    }
+    // the per-row kernel: value rows staged per pass, all of them when they fit
+    const size_t fixed = (rep * D + rep * ((max_len + 3) & ~(size_t)3) + rep * kDS * 4 +
+                          ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
+    const size_t room = fixed < 64 * 1024 ? (64 * 1024 - fixed) / (kDS * 2) : 0;
+    const size_t vcap = std::min<size_t>(room / 64 * 64, (max_len + 63) / 64 * 64);
+    if (vcap < 64)
+        return fail(ECPU_ERR_UNSUPPORTED, "%s: %zu positions x %zu heads per kv head exceed LDS", fn, max_len, rep);
+    const size_t lds = fixed + vcap * kDS * 2;
+    const dim3 grid((unsigned)d.n_kv_heads, (unsigned)d.S, (unsigned)(D / kDS));
+#define PILM_ATTN_BATCH(DD)                                                                                       \
     attn_exact_kernel<DD, BatchRows><<<grid, 256, lds, st>>>(q, k_cache, v_cache, block_ids, (int)d.n_block_ids,  \
                                                              (int)d.num_blocks, (int)d.block_size, gate,            \
                                                              d.gate_row_stride, d.gate_head_stride, nullptr, 0, 0,  \

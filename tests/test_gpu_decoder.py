@@ -256,12 +256,17 @@ def test_qk_rope_then_attention(lib, dev, S, H, Hkv, D, pos0):
     (32, 8, 128, [(5, 300), (5, 31), (5, 0), (5, 511)]),
     (8, 8, 64, [(2, 3), (7, 40), (1, 1)]),
     (16, 8, 128, [(5, p) for p in range(0, 256, 16)]),                   # 16 sequences x 5 rows: M = 80
+    (16, 8, 128, [(16, 0), (16, 16), (13, 100), (9, 200), (16, 480), (2, 5)]),   # prefill chunks, long rows
+    (8, 8, 64, [(16, 48), (11, 3), (16, 0), (1, 700)]),
 ])
-def test_rope_attention_batch_matches_per_sequence(lib, dev, H, Hkv, D, plan):
+def test_rope_attention_batch_matches_per_sequence(lib, dev, monkeypatch, H, Hkv, D, plan):
     """ekernel_qk_norm_rope_batch_bf16 + ekernel_attention_exact_batch_bf16:
     several sequences (rows, pos0) with their own block tables in one shared
     pool, listed out of table order, in one call each; every q row, cache row
-    and output row equal to the oracle's per-sequence steps."""
+    and output row equal to the oracle's per-sequence steps.  The attention
+    runs with every tiling: the per-row kernel (PILM_HIP_ATTN_TILE=0), the
+    chosen tile rows, one row per tile, three (ragged tiles) and the most a
+    tile holds (16 (row, q head) vectors)."""
     import ctypes
     from pilm_amd import bindings as abi
     rng = np.random.default_rng(len(plan) * 131 + H + D)
@@ -315,12 +320,17 @@ def test_rope_attention_batch_matches_per_sequence(lib, dev, H, Hkv, D, plan):
     assert np.array_equal(_bits(q_d), q_want)
     assert np.array_equal(_bits(kc_d), kc_o) and np.array_equal(_bits(vc_d), vc_o)
     ad = abi.EkernelAttentionExactDesc(rows, H, Hkv, D, 0, bs, nphys, per, width, 2 * D)
-    rc = lib.ekernel_attention_exact_batch_bf16(ctypes.byref(ad), seqs, nseq, nseq, _vp(q_d), _vp(kc_d), _vp(vc_d),
-                                                _vp(tab_d), ctypes.c_void_p(p + D * 2), _vp(out_d))
-    assert rc == 0, abi.last_error()
-    got = _bits(out_d)
-    bad = np.argwhere(got != out_want)
-    assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()}"
+    for tile, tile_rows in (("0", "0"), ("1", "0"), ("1", "1"), ("1", "3"), ("1", "16")):
+        monkeypatch.setenv("PILM_HIP_ATTN_TILE", tile)
+        monkeypatch.setenv("PILM_HIP_ATTN_TILE_ROWS", tile_rows)
+        _say(f"[gpu]   attention, tile kernel {tile}, rows per tile {tile_rows}")
+        out_d.fill_(0)
+        rc = lib.ekernel_attention_exact_batch_bf16(ctypes.byref(ad), seqs, nseq, nseq, _vp(q_d), _vp(kc_d),
+                                                    _vp(vc_d), _vp(tab_d), ctypes.c_void_p(p + D * 2), _vp(out_d))
+        assert rc == 0, abi.last_error()
+        got = _bits(out_d)
+        bad = np.argwhere(got != out_want)
+        assert len(bad) == 0, f"{len(bad)} outputs differ (tile {tile}/{tile_rows}), first {bad[:4].tolist()}"
 
 
 def test_rope_attention_batch_rejects_bad_tables(lib, dev):
