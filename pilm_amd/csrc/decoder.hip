@@ -291,20 +291,55 @@ __device__ __forceinline__ float score_dot(const float *qr, const uint32_t (&kv)
     return p[0];
 }
 
-// One wave turns the bf16 scores x[0 .. vis) of a row (cache_len positions
-// long with the masked ones) into bf16 softmax weights in place: max, exp,
-// the sum in torch's order (eight chains j = c mod 8 folded as ((0+4) +
-// (2+6)) + ((1+5) + (3+7)); one plain chain below eight positions), then
-// x * (1 / sum) rounded to bf16.
-__device__ __forceinline__ void softmax_weights(float *x, int vis, int cache_len, int lane) {
-    float mx = -__builtin_inff();
-    for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
+// Block index and offset of position j in a paged cache: shifts when the
+// block size is a power of two (the staging loops compute this per 16-byte
+// piece, where an integer division would cost more than the copy's issue).
+__device__ __forceinline__ void split_pos(int j, int block_size, int &bi, int &off) {
+    if ((block_size & (block_size - 1)) == 0) {
+        bi = j >> __builtin_ctz(block_size);
+        off = j & (block_size - 1);
+    } else {
+        bi = j / block_size;
+        off = j - bi * block_size;
+    }
+}
+
+// LDS DMA of the cache rows [j0, j0 + nrows) (nrows >= 1): PPR 16-byte
+// pieces per row from base (a kv head's first column of the slice; rows
+// row_elems apart), staging row r at dst + r * PPR * 8 elements; SWZ stores
+// piece c of row r in slot c ^ (r mod PPR).  Whole instructions of every
+// wave (pieces past the rows repeat the last row), four pieces per thread per
+// round so that the round's block table reads share one wait.
+template <int PPR, int NT, bool SWZ>
+__device__ __forceinline__ void stage_rows(const uint16_t *base, uint32_t row_elems, const int *bids, int n_block_ids,
+                                           int block_size, int j0, int nrows, uint16_t *dst, int t) {
+    const int wave = t >> 6;
+    const int pieces = ((nrows * PPR + NT - 1) / NT) * NT;
+    for (int b = 0; b < pieces; b += 4 * NT) {
+        size_t off[4];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int u = 0; u < 4; ++u) {
+            const int idx = b + u * NT + t;
+            const int r = min(idx / PPR, nrows - 1);
+            const int slot = idx % PPR;
+            const int c = SWZ ? (slot ^ (r & (PPR - 1))) : slot;
+            int bi, o;
+            split_pos(j0 + r, block_size, bi, o);
+            const uint32_t row = (uint32_t)bids[min(bi, n_block_ids - 1)] * (uint32_t)block_size + (uint32_t)o;
+            off[u] = (size_t)row * row_elems + 8 * c;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (b + u * NT < pieces)
+                __builtin_amdgcn_global_load_lds((const void *)(base + off[u]),
+                                                 (lds_void *)(dst + (size_t)(b + u * NT + wave * 64) * 8), 16, 0, 0);
+    }
+}
+
+// Sum of x[0 .. vis) in torch's order for a row of cache_len positions (every
+// lane of the wave gets it): eight chains j = c mod 8, each in order, folded
+// as ((0+4) + (2+6)) + ((1+5) + (3+7)); one plain chain below eight.
+__device__ __forceinline__ float exp_sum(const float *x, int vis, int cache_len, int lane) {
     float sum = 0.0f;
     if (cache_len >= 8) {
         // lane c < 8: chain c = positions j = c mod 8, in order from x[c]
@@ -321,13 +356,67 @@ __device__ __forceinline__ void softmax_weights(float *x, int vis, int cache_len
             }
             for (; j < vis; j += 8) a = a + x[j];
         }
-        const float b = a + __shfl_xor(a, 4);    // lanes c < 4: (c) + (c + 4)
-        const float c = b + __shfl_xor(b, 2);    // ((0+4) + (2+6)), ((1+5) + (3+7))
-        sum = __shfl(c + __shfl_xor(c, 1), 0);
+        float l[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) l[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), q));
+        sum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
     } else {
         for (int j = 0; j < vis; ++j) sum = sum + x[j];
     }
-    const float inv = __fdiv_rn(1.0f, sum);
+    return sum;
+}
+
+// exp_sum over values stored by chain: x[j] at xc[(j mod 8) * cs + j / 8]
+// (cs a multiple of four, xc 16-byte aligned), so that lane c reads its
+// chain four values at a time; the same order of additions.
+__device__ __forceinline__ float exp_sum_chains(const float *xc, int cs, int vis, int cache_len, int lane) {
+    float sum = 0.0f;
+    if (cache_len >= 8) {
+        float a = 0.0f;
+        if (lane < 8) {
+            const float *x = xc + lane * cs;
+            const int n = (vis - lane + 7) / 8;          // positions lane + 8 i below vis
+            if (n > 0) a = x[0];
+            int i = 1;
+            for (; i < min(n, 4); ++i) a = a + x[i];
+            for (; i + 16 <= n; i += 16) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = *(const float4 *)(x + i + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) a = (((a + v[u].x) + v[u].y) + v[u].z) + v[u].w;
+            }
+            for (; i + 4 <= n; i += 4) {
+                const float4 v = *(const float4 *)(x + i);
+                a = (((a + v.x) + v.y) + v.z) + v.w;
+            }
+            for (; i < n; ++i) a = a + x[i];
+        }
+        float l[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) l[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), q));
+        sum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+    } else {
+        for (int j = 0; j < vis; ++j) sum = sum + xc[(j & 7) * cs + (j >> 3)];
+    }
+    return sum;
+}
+
+// One wave turns the bf16 scores x[0 .. vis) of a row (cache_len positions
+// long with the masked ones) into bf16 softmax weights in place: max, exp,
+// the sum in torch's order (eight chains j = c mod 8 folded as ((0+4) +
+// (2+6)) + ((1+5) + (3+7)); one plain chain below eight positions), then
+// x * (1 / sum) rounded to bf16.
+__device__ __forceinline__ void softmax_weights(float *x, int vis, int cache_len, int lane) {
+    float mx = -__builtin_inff();
+    for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int j = lane; j < vis; j += 64) x[j] = sleef_expf(x[j] - mx);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float inv = __fdiv_rn(1.0f, exp_sum(x, vis, cache_len, lane));
     for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
 }
 
@@ -399,22 +488,17 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
     __syncthreads();
 
     auto row_of = [&](int j) -> size_t {
-        const int blk = bids[min(j / block_size, n_block_ids - 1)];
-        return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
+        int bi, off;
+        split_pos(j, block_size, bi, off);
+        const uint32_t row = (uint32_t)bids[min(bi, n_block_ids - 1)] * (uint32_t)block_size + (uint32_t)off;
+        return (size_t)row * (uint32_t)(Hkv * D) + (size_t)kh * D;
     };
     // value rows [j0, j0 + vcap) of this slice into vs: 16 bytes per lane,
     // four lanes per row; rows past the visible ones repeat the last visible
     // row (never read).
     auto stage_v = [&](int j0) {
-        const int nrows = min(vcap, vis - j0);
-        const int pieces = ((nrows * 4 + 255) / 256) * 256;   // whole instructions of every wave
-        for (int base = 0; base < pieces; base += 256) {
-            const int idx = base + t;
-            const int j = j0 + min(idx >> 2, nrows - 1);
-            const uint16_t *src = v_cache + row_of(j) + d0 + 8 * (idx & 3);
-            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(vs + (size_t)(base + wave * 64) * 8), 16,
-                                             0, 0);
-        }
+        stage_rows<kDS / 8, 256, false>(v_cache + (size_t)kh * D + d0, (uint32_t)(Hkv * D), bids, n_block_ids,
+                                        block_size, j0, min(vcap, vis - j0), vs, t);
     };
     stage_v(0);
 
@@ -567,21 +651,16 @@ __global__ __launch_bounds__(kTileThreads) void attn_tile_kernel(
     __syncthreads();
 
     auto row_of = [&](int j) -> size_t {
-        const int blk = bids[min(j / block_size, n_block_ids - 1)];
-        return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
+        int bi, off;
+        split_pos(j, block_size, bi, off);
+        const uint32_t row = (uint32_t)bids[min(bi, n_block_ids - 1)] * (uint32_t)block_size + (uint32_t)off;
+        return (size_t)row * (uint32_t)(Hkv * D) + (size_t)kh * D;
     };
     // value rows [j0, j0 + vcap) into vs, 16 bytes per lane; whole
     // instructions of every wave, pieces past the rows repeat the last row
     auto stage_v = [&](int j0) {
-        const int nrows = min(vcap, vis_max - j0);
-        const int pieces = ((nrows * PPR + kTileThreads - 1) / kTileThreads) * kTileThreads;
-        for (int base = 0; base < pieces; base += kTileThreads) {
-            const int idx = base + t;
-            const int j = j0 + min(idx / PPR, nrows - 1);
-            const uint16_t *src = v_cache + row_of(j) + 8 * (idx % PPR);
-            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(vs + (size_t)(base + wave * 64) * 8), 16,
-                                             0, 0);
-        }
+        stage_rows<PPR, kTileThreads, false>(v_cache + (size_t)kh * D, (uint32_t)(Hkv * D), bids, n_block_ids,
+                                             block_size, j0, min(vcap, vis_max - j0), vs, t);
     };
     stage_v(0);
 
@@ -690,6 +769,10 @@ __global__ __launch_bounds__(kTileThreads) void attn_tile_kernel(
 // Every sum keeps the order of the two-kernel path above.
 constexpr int kDecodeThreads = 512;
 
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are
+// complete, its global loads and LDS copies may still be in flight.
+__device__ __forceinline__ void lds_only_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Largest value of a wave (every lane gets it) through DPP row shifts and
 // broadcasts instead of LDS-routed shuffles: max is exact in any order.
 __device__ __forceinline__ float wave_max_dpp(float v) {
@@ -726,7 +809,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     float *qs = xn + (hpw + 1) * D;                            // [hpw][D] roped q
     float *sc = qs + hpw * D;                                  // [hpw][scs]
     float *part = sc + (size_t)hpw * scs;                      // [hpw][4][D] chain sums
-    int *bids = (int *)(part + hpw * 4 * D);                   // [n_block_ids]
+    float *cm = part + hpw * 4 * D;                            // [scs + 32] one row, chain-major
+    int *bids = (int *)(cm + scs + 32);                        // [n_block_ids]
     uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [vcap][D]
 
     const int pos = step ? step[0] : pos0_host;
@@ -782,8 +866,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     __syncthreads();                      // block ids and the raw heads are in
 
     auto row_of = [&](int j) -> size_t {
-        const int blk = bids[min(j / block_size, n_block_ids - 1)];
-        return (((size_t)blk * block_size + j % block_size) * Hkv + kh) * D;
+        int bi, off;
+        split_pos(j, block_size, bi, off);
+        const uint32_t row = (uint32_t)bids[min(bi, n_block_ids - 1)] * (uint32_t)block_size + (uint32_t)off;
+        return (size_t)row * (uint32_t)(Hkv * D) + (size_t)kh * D;
     };
     // rows [j0, j0 + vcap) of a cache into the staging region: 16 bytes per
     // lane, D / 8 lanes per row, one DMA instruction per 64 pieces; rows past
@@ -793,17 +879,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     // without bank conflicts; value rows are stored plainly.
     constexpr int per_row = D / 8;
     auto stage = [&](const uint16_t *cache, int j0, bool swizzle) {
-        const int nrows = min(vcap, vis - j0);
-        const int pieces = ((nrows * per_row + nthreads - 1) / nthreads) * nthreads;
-        for (int base = 0; base < pieces; base += nthreads) {
-            const int idx = base + t;
-            const int jr = min(idx / per_row, nrows - 1);
-            const int slot = idx % per_row;
-            const int u = swizzle ? (slot ^ (jr & (per_row - 1))) : slot;
-            const uint16_t *src = cache + row_of(j0 + jr) + 8 * u;
-            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(vs + (size_t)(base + wave * 64) * 8), 16,
-                                             0, 0);
-        }
+        if (swizzle)
+            stage_rows<per_row, nthreads, true>(cache + (size_t)kh * D, (uint32_t)(Hkv * D), bids, n_block_ids,
+                                                block_size, j0, min(vcap, vis - j0), vs, t);
+        else
+            stage_rows<per_row, nthreads, false>(cache + (size_t)kh * D, (uint32_t)(Hkv * D), bids, n_block_ids,
+                                                 block_size, j0, min(vcap, vis - j0), vs, t);
     };
     stage(k_cache, 0, true);
 
@@ -846,8 +927,87 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     // key row to registers and the value rows' DMA into the same region
     // starts at once, under the scores (an LDS-only barrier after them; the
     // softmax's LDS writes then wait for the DMA).
-    const bool early_v = vis <= nthreads && vis <= vcap;
-    if (early_v) {
+    // One q head per workgroup and one position per thread: each thread
+    // loads its share of the value rows into registers as soon as the key
+    // rows are out of the staging (plain loads, so the LDS traffic of the
+    // scores and the softmax does not wait for them, as it would for LDS
+    // copies), every wave computes scores and the softmax (max over DPP and
+    // the waves' maxima, exp, the chain sums on wave 0, the weights), and
+    // the value rows go into the staging before the P.V pass.
+    constexpr int kWaves = nthreads / 64;
+    const bool split_v = HPW == 1 && vis <= nthreads && vis <= vcap;
+    const bool early_v = !split_v && vis <= nthreads && vis <= vcap;
+    if (split_v) {
+        wait_vmcnt<0>();
+        __syncthreads();                  // the key rows (and the roped q and k) are in
+        if (is_k && pos >= 0 && pos < vis) {
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int i = lane + 64 * u;
+                vs[(size_t)pos * D + 8 * ((i / 8) ^ (pos & (per_row - 1))) + i % 8] = kb[u];
+            }
+        }
+        __syncthreads();
+        uint32_t ka[D / 2];
+        if (t < vis) {
+            const uint16_t *row = vs + (size_t)t * D;
+#pragma unroll
+            for (int u = 0; u < per_row; ++u) {
+                const u32x4 c = *(const u32x4 *)(row + 8 * (u ^ (t & (per_row - 1))));
+                ka[4 * u] = c[0];
+                ka[4 * u + 1] = c[1];
+                ka[4 * u + 2] = c[2];
+                ka[4 * u + 3] = c[3];
+            }
+        }
+        // piece u of this thread: value row t / per_row + u * nthreads / per_row,
+        // chunk t mod per_row; the block table reads first, then the loads
+        uint32_t vrow[per_row];
+#pragma unroll
+        for (int u = 0; u < per_row; ++u) {
+            int bi, o;
+            split_pos(min(t / per_row + u * (nthreads / per_row), vis - 1), block_size, bi, o);
+            vrow[u] = (uint32_t)bids[min(bi, n_block_ids - 1)] * (uint32_t)block_size + (uint32_t)o;
+        }
+        const uint16_t *vbase = v_cache + (size_t)kh * D + 8 * (t % per_row);
+        u32x4 vp[per_row];
+#pragma unroll
+        for (int u = 0; u < per_row; ++u)
+            if (t / per_row + u * (nthreads / per_row) < vis)
+                vp[u] = *(const u32x4 *)(vbase + (size_t)vrow[u] * (uint32_t)(Hkv * D));
+        float *red = part;                // [kWaves] the waves' maxima, then 1 / sum
+        float e = -__builtin_inff();
+        if (t < vis) e = bfr(bfr(score_dot<D>(qs, ka, naive)) * scale);
+        const float m = wave_max_dpp(e);
+        if (lane == 0) red[wave] = m;
+        lds_only_barrier();               // every wave's maximum (and every key row read)
+        float mx = red[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, red[w]);
+        // the exps by sum chain (position j at cm[(j mod 8) c8 + j / 8]), then
+        // the weights by P.V chain (cm[(j mod 4) c4 + j / 4]) besides sc[j]
+        const int c8 = ((scs + 7) / 8 + 3) & ~3, c4 = (scs / 4 + 3) & ~3;
+        if (t < vis) {
+            e = sleef_expf(e - mx);
+            cm[(t & 7) * c8 + (t >> 3)] = e;
+        }
+        lds_only_barrier();
+        if (wave == 0) {
+            const float inv = __fdiv_rn(1.0f, exp_sum_chains(cm, c8, vis, cache_len, lane));
+            if (lane == 0) red[kWaves] = inv;
+        }
+        lds_only_barrier();
+        if (t < vis) {
+            const float w = bfr(e * red[kWaves]);
+            sc[t] = w;
+            cm[(t & 3) * c4 + (t >> 2)] = w;
+        }
+#pragma unroll
+        for (int u = 0; u < per_row; ++u) {
+            const int r = t / per_row + u * (nthreads / per_row);
+            if (r < vis) *(u32x4 *)(vs + (size_t)r * D + 8 * (t % per_row)) = vp[u];
+        }
+    } else if (early_v) {
         wait_vmcnt<0>();
         __syncthreads();                  // the key rows (and the roped q and k) are in
         if (is_k && pos >= 0 && pos < vis) {
@@ -917,8 +1077,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
         stage(v_cache, 0, false);             // value rows arrive during the softmax
     }
 
-    // softmax per head: wave r
-    for (int r = wave; r < hpw; r += nthreads / 64) {
+    // softmax per head: wave r (the split path has its weights)
+    for (int r = wave; r < (split_v ? 0 : hpw); r += nthreads / 64) {
         float *x = sc + (size_t)r * scs;
         float mx = -__builtin_inff();
         for (int j = lane; j < vis; j += 64) mx = fmaxf(mx, x[j]);
@@ -927,30 +1087,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float sum = 0.0f;
-        if (cache_len >= 8) {
-            float a = 0.0f;
-            if (lane < 8) {
-                a = lane < vis ? x[lane] : 0.0f;
-                int j = lane + 8;
-                for (; j + 56 < vis; j += 64) {
-                    float v[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) v[u] = x[j + 8 * u];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) a = a + v[u];
-                }
-                for (; j < vis; j += 8) a = a + x[j];
-            }
-            // ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)), lanes read with readlane
-            float l[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) l[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), q));
-            sum = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
-        } else {
-            for (int j = 0; j < vis; ++j) sum = sum + x[j];
-        }
-        const float inv = __fdiv_rn(1.0f, sum);
+        const float inv = __fdiv_rn(1.0f, exp_sum(x, vis, cache_len, lane));
         for (int j = lane; j < vis; j += 64) x[j] = bfr(x[j] * inv);
     }
 
@@ -959,7 +1096,54 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     // eight positions of a chain (their value and rep weights) loaded ahead
     const int main_len = naive ? 0 : (cache_len / 4) * 4;
     constexpr int nthr = 4 * D;
-    for (int base = 0; base < nthr; base += nthreads) {
+    if (split_v) {
+        // one pass, one head: thread (chain k, column pair cp), k = t / (D / 2),
+        // a wave reading whole value rows as 32-bit pairs; chain k's weights
+        // four at a time from cm[k c4 + i] (position k + 4 i)
+        wait_vmcnt<0>();
+        __syncthreads();                  // the value rows and the weights are in
+        if (is_k && pos >= 0 && pos < vis) {
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) vs[(size_t)pos * D + lane + 64 * u] = vr[u];
+        }
+        __syncthreads();                  // the new value row replaces the staged copy
+        if (t < 2 * D) {
+            const int k = t / (D / 2), cp = t % (D / 2);
+            const uint32_t *vw = (const uint32_t *)vs + cp;       // vw[j * D / 2]: the pair at position j
+            float a0 = 0.0f, a1 = 0.0f;
+            auto fma_pos = [&](float w, int j) {
+                const uint32_t v = vw[(size_t)j * (D / 2)];
+                a0 = __builtin_fmaf(w, bf16_lo(v), a0);
+                a1 = __builtin_fmaf(w, bf16_hi(v), a1);
+            };
+            if (naive) {
+                if (k == 0)
+                    for (int j = 0; j < vis; ++j) fma_pos(sc[j], j);
+            } else {
+                const float *wk = cm + k * ((scs / 4 + 3) & ~3);
+                const int im = max(0, (min(vis, main_len) - k + 3) / 4);   // positions k + 4 i
+                int i = 0;
+                for (; i + 8 <= im; i += 8) {
+                    const float4 wa = *(const float4 *)(wk + i), wb = *(const float4 *)(wk + i + 4);
+                    uint32_t v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = vw[(size_t)(k + 4 * (i + u)) * (D / 2)];
+                    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        a0 = __builtin_fmaf(wv[u], bf16_lo(v[u]), a0);
+                        a1 = __builtin_fmaf(wv[u], bf16_hi(v[u]), a1);
+                    }
+                }
+                for (; i < im; ++i) fma_pos(wk[i], k + 4 * i);
+                if (k == 0)
+                    for (int j = main_len; j < vis; ++j) fma_pos(sc[j], j);
+            }
+            part[k * D + 2 * cp] = a0;
+            part[k * D + 2 * cp + 1] = a1;
+        }
+    }
+    for (int base = 0; base < (split_v ? 0 : nthr); base += nthreads) {
         const int i = base + t;
         const bool active = i < nthr;
         const int k = (i / D) & 3, c = i % D;
@@ -1461,7 +1645,7 @@ int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint
     // 796 -> 848 tok/s), or all rep q heads of the kv head sharing the key
     // rows' widening (PILM_DECODE_ATTN_SHARED=1)
     const size_t hpw = env_int("PILM_DECODE_ATTN_SHARED", 0) == 1 ? rep : 1;
-    const size_t fixed = ((hpw + 1) * D + hpw * D + hpw * ((max_len + 3) & ~(size_t)3) + hpw * 4 * D +
+    const size_t fixed = ((hpw + 1) * D + hpw * D + (hpw + 1) * ((max_len + 3) & ~(size_t)3) + 32 + hpw * 4 * D +
                           ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
     const size_t budget = lds_limit();
     const size_t room = fixed < budget ? (budget - fixed) / (D * 2) : 0;
