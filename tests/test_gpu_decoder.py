@@ -364,7 +364,8 @@ def test_rope_attention_batch_rejects_bad_tables(lib, dev):
 @pytest.mark.parametrize("H,Hkv,D,pos0", [(16, 8, 128, 383), (16, 8, 128, 0), (16, 8, 128, 1), (16, 8, 128, 2),
                                           (16, 8, 128, 3), (16, 8, 128, 7), (16, 8, 128, 64), (32, 8, 128, 2043),
                                           (4, 2, 128, 0), (8, 8, 64, 17), (16, 4, 128, 100), (16, 8, 128, 4000),
-                                          (32, 8, 64, 515), (16, 8, 128, 511)])
+                                          (32, 8, 64, 515), (16, 8, 128, 511), (16, 8, 128, 512),
+                                          (16, 8, 64, 255), (8, 2, 64, 300)])
 @pytest.mark.parametrize("shared", [False, True])
 def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0, shared, monkeypatch):
     """ekernel_decode_attention_bf16 (one launch) against the oracle's two
@@ -373,7 +374,10 @@ def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0, shared, monkeypatch):
     (torch's small-matrix kernel below 4), 8 and 65 (tails of the four- and
     eight-way sums), 1, 2 and 4 q heads per kv head, value rows staged in one
     pass and in several (2044 and 4001 positions); one q head per workgroup
-    and (shared) all q heads of a kv head per workgroup."""
+    and (shared) all q heads of a kv head per workgroup.  With one q head per
+    workgroup, 512 positions are the last that take the value rows through
+    registers and the workgroup-wide softmax, 513 the first staged by copy
+    after the scores."""
     import ctypes
     from pilm_amd import bindings as abi
     monkeypatch.setenv("PILM_DECODE_ATTN_SHARED", "1" if shared else "0")
