@@ -40,7 +40,9 @@ Printed JSON line:
                w4row, w8a32, w8a16, gemm, gemm_fp16 (torch's fp16 GEMM at
                the same shapes, for reference), fused, attention, load
                (bundle -> HBM), verify (16-sequence MTP verify, M = 80),
-               verify_step (the whole batched verify step, Qwen3-1.7B), or all
+               verify_step (the whole batched verify step, Qwen3-1.7B W4A16
+               g128), verify_step_8b (the same on Qwen3-8B with int8
+               per-row weights, 256-token prompts), or all
 
 Profiling helpers (rocprofv3 runs the program, these read its output):
   --pmc-pass            eager steps plus a plain copy kernel of known size,
@@ -385,6 +387,9 @@ def sweep(torch, dev, sections) -> dict:
         res["verify_8b"] = sweep_verify(torch, dev)
     if "verify_step" in sections:
         res["verify_step_1p7b"] = sweep_verify_step(torch, dev)
+    if "verify_step_8b" in sections:
+        from pilm_amd import qwen3 as Q
+        res["verify_step_8b_w8"] = sweep_verify_step(torch, dev, cfg=Q.QWEN3_8B_W8, prompt_len=256)
     return res
 
 
@@ -417,9 +422,9 @@ def sweep_gemm_fp16(torch, dev, ms, reps: int = 20) -> dict:
 
 
 def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int = 8, prompt_len: int = 128,
-                      seed: int = 1) -> dict:
-    """One batched MTP verify step end to end on Qwen3-1.7B W4A16-g128
-    (Qwen3Batch.verify: n_seq sequences x (1 + drafts) rows through every
+                      seed: int = 1, cfg=None) -> dict:
+    """One batched MTP verify step end to end, on Qwen3-1.7B W4A16-g128 unless
+    cfg names another model (Qwen3Batch.verify: n_seq sequences x (1 + drafts) rows through every
     linear as one M, rope and attention for all sequences in one launch
     each, lm_head on every row, acceptance on the host): GPU time between
     HIP events and wall time per step after a prefill of every prompt.
@@ -427,12 +432,19 @@ def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int =
     same whatever is accepted, every row goes through the model."""
     from pilm_amd import qwen3 as Q
     from pilm_amd import synth_model as SM
-    cfg = Q.QWEN3_1P7B
+    cfg = cfg or Q.QWEN3_1P7B
+    t_w = time.perf_counter()
     w = Q.Qwen3Weights.synthetic(cfg, seed, 0.02, device=dev)
+    torch.cuda.synchronize()
+    t_w = time.perf_counter() - t_w
     b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=prompt_len + (steps + 2) * (1 + drafts) + 1,
                      max_rows=n_seq * (1 + drafts))
     prompts = [SM.token_ids(seed + i, prompt_len, cfg.vocab).tolist() for i in range(n_seq)]
+    torch.cuda.synchronize()
+    t_p = time.perf_counter()
     last = b.prefill_seqs(list(range(n_seq)), prompts)
+    torch.cuda.synchronize()
+    t_p = time.perf_counter() - t_p
     drafts_of = [[0] * drafts for _ in range(n_seq)]
     s = torch.cuda.current_stream(dev)
     gpu_ms, wall_ms, accepted = [], [], 0
@@ -451,9 +463,11 @@ def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int =
         last = [nxt for _, nxt in out]
     m = n_seq * (1 + drafts)
     g = sorted(gpu_ms)[len(gpu_ms) // 2]
-    return {"sequences": n_seq, "rows_per_step": m, "steps": steps, "gpu_ms_per_step": round(g, 3),
+    return {"model": f"Qwen3 {cfg.layers} layers, hidden {cfg.hidden}, {cfg.weights}", "sequences": n_seq,
+            "prompt_tokens": prompt_len, "rows_per_step": m, "steps": steps, "gpu_ms_per_step": round(g, 3),
             "wall_ms_per_step": round(sorted(wall_ms)[len(wall_ms) // 2], 3),
-            "rows_per_s": round(m / g * 1e3, 1), "accepted_drafts_per_step": round(accepted / steps, 1)}
+            "rows_per_s": round(m / g * 1e3, 1), "accepted_drafts_per_step": round(accepted / steps, 1),
+            "weights_build_s": round(t_w, 2), "prefill_s": round(t_p, 2)}
 
 
 def sweep_verify(torch, dev, n_seq: int = 16, drafts: int = 4) -> dict:
@@ -1097,7 +1111,7 @@ def main(argv=None) -> int:
         calls = xs = run = None
     if args.sweep:
         sections = ("g128", "w4row", "w8a32", "w8a16", "gemm", "gemm_fp16", "fused", "attention", "load", "verify",
-                    "verify_step") \
+                    "verify_step", "verify_step_8b") \
             if args.sweep == "all" \
             else tuple(args.sweep.split(","))
         print(f"[bench] sweeps: {', '.join(sections)}", flush=True)

@@ -166,13 +166,16 @@ def sha_u16(a: np.ndarray) -> str:
 
 
 class OracleDecoder:
-    """piLM's Qwen3Model (all layers full attention, every Linear W4A16 g128)
-    evaluated with the oracle, on the fixture's seeded weights."""
+    """piLM's Qwen3Model (all layers full attention, every Linear W4A16 g128,
+    or with cfg["weights"] == "w8" int8 per output row run as W8A16 on the
+    bf16 activations, linear.py:210-231) evaluated with the oracle, on the
+    fixture's seeded weights."""
 
     def __init__(self, cfg: dict):
         import torch
         from pilm_amd import synth_model as SM
         self.cfg = c = cfg
+        self.w8 = c.get("weights", "w4g128") == "w8"
         L, H, V = c["layers"], c["hidden"], c["vocab"]
         ids = SM.tensor_ids(L)
         seed, std = c["seed"], c["std"]
@@ -184,7 +187,10 @@ class OracleDecoder:
 
         def quant(name, out_f, in_f):
             w = SM.normal_f32(seed, ids[name], (out_f, in_f), std).numpy()
-            q, s = O.quantize_weight_i4_grouped(w, c["group_size"])
+            if self.w8:
+                q, s = O.quantize_weight_i8_per_row(w)
+            else:
+                q, s = O.quantize_weight_i4_grouped(w, c["group_size"])
             self.qsha[name] = [hashlib.sha256(q.tobytes()).hexdigest(), hashlib.sha256(s.tobytes()).hexdigest()]
             return q, s
 
@@ -219,6 +225,8 @@ class OracleDecoder:
 
     def _lin(self, x, qs):
         q, s = qs
+        if self.w8:
+            return O.linear_w8a16_bf16(x, q, s)
         return O.linear_w4a16g_bf16(x, q, s, self.cfg["group_size"])
 
     def forward(self, ids, pos0, all_rows=False):

@@ -49,6 +49,7 @@ class Qwen3Config:
     partial_rotary: float = 1.0
     block_size: int = 16
     group_size: int = 128
+    weights: str = "w4g128"     # every Linear: "w4g128" (W4A16, group 128) or "w8" (int8 per output row)
 
     @classmethod
     def from_dict(cls, d: dict) -> "Qwen3Config":
@@ -61,6 +62,7 @@ class Qwen3Config:
 
 QWEN3_1P7B = Qwen3Config()
 QWEN3_8B = Qwen3Config(layers=36, hidden=4096, heads=32, kv_heads=8, intermediate=12288)
+QWEN3_8B_W8 = Qwen3Config(layers=36, hidden=4096, heads=32, kv_heads=8, intermediate=12288, weights="w8")
 
 
 def rope_tables(theta: float, rot_dim: int, positions: int):
@@ -79,9 +81,11 @@ def _sha(t: torch.Tensor) -> str:
 
 @dataclass
 class Qwen3Weights:
-    """Device-resident weights: bf16 embedding and norms, W4A16 g128 linears
-    (qweight uint8 [N, K/2], scales fp32 [N, K/128]) with q/k/v and gate/up
-    concatenated row-wise."""
+    """Device-resident weights: bf16 embedding and norms, and the linears with
+    q/k/v and gate/up concatenated row-wise, either W4A16 g128 (qweight uint8
+    [N, K/2], scales fp32 [N, K/128]) or int8 per output row (qweight int8
+    [N, K], scales fp32 [N]; with bf16 activations the reference runs these
+    through ekernel_linear_w8a16_bf16, linear.py:210-231)."""
     cfg: Qwen3Config
     embed: torch.Tensor
     layers: list
@@ -93,7 +97,9 @@ class Qwen3Weights:
     def synthetic(cls, cfg: Qwen3Config, seed: int, std: float = 0.02, device="cuda", hashes: bool = False):
         """Random-init weights ~N(0, std) (pilm_amd.synth_model, bit-identical on
         any device), every Linear quantized on the device with the reference's
-        grouped int4 quantizer (ckernel.quantize_weight_i4_grouped_chunked)."""
+        grouped int4 quantizer (ckernel.quantize_weight_i4_grouped_chunked) or,
+        for cfg.weights "w8", its int8 per-row quantizer
+        (ckernel.quantize_weight_i8_per_row_chunked)."""
         ids = SM.tensor_ids(cfg.layers)
         qsha = {}
         D, H, Hq, Hkv, I = cfg.head_dim, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.intermediate
@@ -103,7 +109,12 @@ class Qwen3Weights:
 
         def quant(name, out_f, in_f):
             w = SM.normal_f32(seed, ids[name], (out_f, in_f), std, device=device)
-            q, s = ckernel.quantize_weight_i4_grouped_chunked(w, group_size=cfg.group_size, rows_per_chunk=8192)
+            if cfg.weights == "w8":
+                q, s = ckernel.quantize_weight_i8_per_row_chunked(w, rows_per_chunk=8192)
+            elif cfg.weights == "w4g128":
+                q, s = ckernel.quantize_weight_i4_grouped_chunked(w, group_size=cfg.group_size, rows_per_chunk=8192)
+            else:
+                raise ValueError(f"unknown weight format {cfg.weights!r} (w4g128 or w8)")
             del w
             if hashes:
                 qsha[name] = [_sha(q), _sha(s)]
@@ -191,7 +202,9 @@ class Qwen3Decoder:
         # the one-launch decode attention serves 64- and 128-wide heads, 1, 2 or 4 q heads per kv head
         self.fused_decode = c.head_dim in (64, 128) and c.heads // c.kv_heads in (1, 2, 4)
         # decode tokens: each GemmaRMSNorm inside the launch of the linear after it, SwiGLU inside gate_up
-        self.fused_norm = self.fused_decode and c.hidden % 256 == 0 and c.hidden <= 16384
+        # (the norm-fused GEMV is W4A16 g128)
+        self.fused_norm = (self.fused_decode and c.weights == "w4g128" and c.hidden % 256 == 0
+                           and c.hidden <= 16384)
 
     # ---------------------------------------------------------------- calls
     def _check(self, rc: int, name: str) -> None:
@@ -208,8 +221,12 @@ class Qwen3Decoder:
         q, s = wq
         d = self._desc(("lin", m, q.shape[0], x.shape[1]),
                        lambda: abi.EkernelLinearW8A32Desc(m, q.shape[0], x.shape[1]))
-        self._check(self.lib.ekernel_linear_w4a16g128_bf16(ctypes.byref(d), _vp(x), _vp(q), _vp(s), _vp(out), 6),
-                    "ekernel_linear_w4a16g128_bf16")
+        if q.dtype == torch.int8:
+            self._check(self.lib.ekernel_linear_w8a16_bf16(ctypes.byref(d), _vp(x), _vp(q), _vp(s), _vp(out), 6),
+                        "ekernel_linear_w8a16_bf16")
+        else:
+            self._check(self.lib.ekernel_linear_w4a16g128_bf16(ctypes.byref(d), _vp(x), _vp(q), _vp(s), _vp(out),
+                                                               6), "ekernel_linear_w4a16g128_bf16")
 
     def _norm(self, x, res, weight, out, res_out, m):
         d = self._desc(("norm", m), lambda: abi.EkernelRmsnormDesc(m, self.cfg.hidden, self.cfg.eps))

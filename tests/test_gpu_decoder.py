@@ -563,6 +563,34 @@ def test_decoder_tiny_matches_reference(dev):
     assert dec3.generate(fx["prompt"], len(fx["tokens"]), graph=True) == fx["tokens"]
 
 
+def test_decoder_tiny_w8_matches_oracle(dev):
+    """The two-layer model with every Linear int8 per output row (the
+    reference's W8A32 quantization in a bf16 model runs them as W8A16,
+    linear.py:210-231): quantized weights, every step's logits and the greedy
+    tokens equal to the oracle's (oracle/decoder.py), eager and replayed.
+    The norms run as their own launches (the norm-fused GEMV is W4A16 g128)."""
+    from pilm_amd import qwen3 as Q
+    c = dict(_fixture("tiny")["config"])
+    c["weights"], c["new_tokens"] = "w8", 16
+    prompt = _fixture("tiny")["prompt"]
+    _say("[gpu] decoder, two-layer W8 model: oracle (CPU)")
+    od = OD.OracleDecoder(c)
+    want_sha = []
+    want = od.generate(prompt, c["new_tokens"], on_logits=lambda i, lg: want_sha.append(OD.sha_u16(lg)))
+    _say("[gpu] decoder, two-layer W8 model: weights, eager steps")
+    w, dec = _decoder({"config": c}, dev, hashes=True)
+    assert w.quantized_sha == od.qsha
+    assert not dec.fused_norm and w.layers[0]["qkv"][0].dtype == torch.int8
+    shas = []
+    toks = dec.generate(prompt, c["new_tokens"], on_logits=lambda i, lg: shas.append(OD.sha_u16(_bits(lg))))
+    first = next((i for i, (a, b) in enumerate(zip(shas, want_sha)) if a != b), None)
+    assert first is None, f"logits differ first at step {first}"
+    assert toks == want
+    _say("[gpu] decoder, two-layer W8 model: graph replay")
+    dec2 = Q.Qwen3Decoder(w, max_positions=dec.max_pos, max_new_tokens=dec.max_new)
+    assert dec2.generate(prompt, c["new_tokens"], graph=True) == want
+
+
 def test_decoder_qwen3_1p7b_matches_reference(dev):
     """Config 4: Qwen3-1.7B W4A16 g128, 128-token prompt, 256 greedy tokens."""
     fx = _fixture("qwen3_1p7b")

@@ -9,8 +9,9 @@ device takes every running sequence's rows as one M: 16 sequences x
 own block table in a shared KV pool.
 
 Checked here:
-  * the two-layer model: every verify row's bf16 logits bit-identical to the
-    oracle's per-sequence model call (oracle/decoder.py), the accepted drafts
+  * the two-layer model, W4A16 g128 and int8 per-row weights: every verify
+    row's bf16 logits bit-identical to the oracle's per-sequence model call
+    (oracle/decoder.py), the accepted drafts
     and next token per sequence equal to the oracle's, and the emitted tokens
     equal to plain greedy decoding (what greedy speculation must give);
   * Qwen3-1.7B W4A16 g128: 16 sequences on the 128-token prompt of the
@@ -65,11 +66,16 @@ def _drafts(greedy, start, n, bad, vocab, salt):
     return d
 
 
-def test_batched_verify_two_layer_matches_oracle(dev):
+@pytest.mark.parametrize("weights", ["w4g128", "w8"])
+def test_batched_verify_two_layer_matches_oracle(dev, weights):
+    """W4A16 g128, and int8 per-row weights as the reference's W8A32
+    quantization runs them in a bf16 model (W8A16, the Qwen3-8B MTP
+    configuration's format), on the two-layer model."""
     from pilm_amd import qwen3 as Q
     from pilm_amd import synth_model as SM
     fx = _fixture("tiny")
     c = dict(fx["config"])
+    c["weights"] = weights
     n_seq, n_greedy = 16, 12
     prompts = [SM.token_ids(200 + i, 3 + 7 * i, c["vocab"]) for i in range(n_seq)]
     c["prompt"], c["new_tokens"] = max(len(p) for p in prompts), n_greedy + 4
@@ -83,7 +89,7 @@ def test_batched_verify_two_layer_matches_oracle(dev):
         n2, j2 = i % 5, (3 * i + 1) % 5
         plan.append((j1, n2, j2))
 
-    _say("[gpu] batched verify, two-layer model: oracle greedy and verify rows (CPU)")
+    _say(f"[gpu] batched verify, two-layer {weights} model: oracle greedy and verify rows (CPU)")
     od = OD.OracleDecoder(c)
     greedy, want = [], []
     for i in range(n_seq):
