@@ -467,6 +467,8 @@ def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int =
             "prompt_tokens": prompt_len, "rows_per_step": m, "steps": steps, "gpu_ms_per_step": round(g, 3),
             "wall_ms_per_step": round(sorted(wall_ms)[len(wall_ms) // 2], 3),
             "rows_per_s": round(m / g * 1e3, 1), "accepted_drafts_per_step": round(accepted / steps, 1),
+            # a step emits n_seq tokens plus the accepted drafts: the bounds of no and of every draft accepted
+            "tokens_per_s_bounds": [round(n_seq / g * 1e3, 1), round(m / g * 1e3, 1)],
             "weights_build_s": round(t_w, 2), "prefill_s": round(t_p, 2)}
 
 
