@@ -424,12 +424,15 @@ def sweep_gemm_fp16(torch, dev, ms, reps: int = 20) -> dict:
 def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int = 8, prompt_len: int = 128,
                       seed: int = 1, cfg=None) -> dict:
     """One batched MTP verify step end to end, on Qwen3-1.7B W4A16-g128 unless
-    cfg names another model (Qwen3Batch.verify: n_seq sequences x (1 + drafts) rows through every
-    linear as one M, rope and attention for all sequences in one launch
-    each, lm_head on every row, acceptance on the host): GPU time between
-    HIP events and wall time per step after a prefill of every prompt.
-    The drafts are fixed tokens (mostly rejected): the step's work is the
-    same whatever is accepted, every row goes through the model."""
+    cfg names another model (Qwen3Batch.verify: n_seq sequences x (1 +
+    drafts) rows through every linear as one M, rope and attention for all
+    sequences in one launch each, lm_head on every row, acceptance on the
+    host): GPU time between HIP events and wall time per step after a
+    prefill of every prompt, with the linears on the bit-exact kernels
+    ("exact") and with batches of 64 rows or more on the matrix cores
+    ("matrix_cores", within their tolerance).  The drafts are fixed tokens
+    (mostly rejected): the step's work is the same whatever is accepted,
+    every row goes through the model."""
     from pilm_amd import qwen3 as Q
     from pilm_amd import synth_model as SM
     cfg = cfg or Q.QWEN3_1P7B
@@ -437,39 +440,43 @@ def sweep_verify_step(torch, dev, n_seq: int = 16, drafts: int = 4, steps: int =
     w = Q.Qwen3Weights.synthetic(cfg, seed, 0.02, device=dev)
     torch.cuda.synchronize()
     t_w = time.perf_counter() - t_w
-    b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=prompt_len + (steps + 2) * (1 + drafts) + 1,
-                     max_rows=n_seq * (1 + drafts))
     prompts = [SM.token_ids(seed + i, prompt_len, cfg.vocab).tolist() for i in range(n_seq)]
-    torch.cuda.synchronize()
-    t_p = time.perf_counter()
-    last = b.prefill_seqs(list(range(n_seq)), prompts)
-    torch.cuda.synchronize()
-    t_p = time.perf_counter() - t_p
-    drafts_of = [[0] * drafts for _ in range(n_seq)]
-    s = torch.cuda.current_stream(dev)
-    gpu_ms, wall_ms, accepted = [], [], 0
-    for it in range(steps + 1):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(s)
-        out = b.verify(last, drafts_of)
-        e1.record(s)
-        torch.cuda.synchronize()
-        if it > 0:                                         # the first step warms the descriptors and scratch
-            wall_ms.append((time.perf_counter() - t0) * 1e3)
-            gpu_ms.append(e0.elapsed_time(e1))
-            accepted += sum(len(a) for a, _ in out)
-        last = [nxt for _, nxt in out]
     m = n_seq * (1 + drafts)
-    g = sorted(gpu_ms)[len(gpu_ms) // 2]
-    return {"model": f"Qwen3 {cfg.layers} layers, hidden {cfg.hidden}, {cfg.weights}", "sequences": n_seq,
-            "prompt_tokens": prompt_len, "rows_per_step": m, "steps": steps, "gpu_ms_per_step": round(g, 3),
-            "wall_ms_per_step": round(sorted(wall_ms)[len(wall_ms) // 2], 3),
-            "rows_per_s": round(m / g * 1e3, 1), "accepted_drafts_per_step": round(accepted / steps, 1),
-            # a step emits n_seq tokens plus the accepted drafts: the bounds of no and of every draft accepted
-            "tokens_per_s_bounds": [round(n_seq / g * 1e3, 1), round(m / g * 1e3, 1)],
-            "weights_build_s": round(t_w, 2), "prefill_s": round(t_p, 2)}
+    res = {"model": f"Qwen3 {cfg.layers} layers, hidden {cfg.hidden}, {cfg.weights}", "sequences": n_seq,
+           "prompt_tokens": prompt_len, "rows_per_step": m, "steps": steps, "weights_build_s": round(t_w, 2)}
+    for mode, exact in (("exact", True), ("matrix_cores", False)):
+        b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=prompt_len + (steps + 2) * (1 + drafts) + 1,
+                         max_rows=m, exact=exact)
+        torch.cuda.synchronize()
+        t_p = time.perf_counter()
+        last = b.prefill_seqs(list(range(n_seq)), prompts)
+        torch.cuda.synchronize()
+        t_p = time.perf_counter() - t_p
+        drafts_of = [[0] * drafts for _ in range(n_seq)]
+        s = torch.cuda.current_stream(dev)
+        gpu_ms, wall_ms, accepted = [], [], 0
+        for it in range(steps + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            e0.record(s)
+            out = b.verify(last, drafts_of)
+            e1.record(s)
+            torch.cuda.synchronize()
+            if it > 0:                                     # the first step warms the descriptors and scratch
+                wall_ms.append((time.perf_counter() - t0) * 1e3)
+                gpu_ms.append(e0.elapsed_time(e1))
+                accepted += sum(len(a) for a, _ in out)
+            last = [nxt for _, nxt in out]
+        g = sorted(gpu_ms)[len(gpu_ms) // 2]
+        res[mode] = {"gpu_ms_per_step": round(g, 3), "wall_ms_per_step": round(sorted(wall_ms)[len(wall_ms) // 2], 3),
+                     "rows_per_s": round(m / g * 1e3, 1), "accepted_drafts_per_step": round(accepted / steps, 1),
+                     # a step emits n_seq tokens plus the accepted drafts: no draft / every draft accepted
+                     "tokens_per_s_bounds": [round(n_seq / g * 1e3, 1), round(m / g * 1e3, 1)],
+                     "prefill_s": round(t_p, 2)}
+        del b
+        torch.cuda.empty_cache()
+    return res
 
 
 def sweep_verify(torch, dev, n_seq: int = 16, drafts: int = 4) -> dict:

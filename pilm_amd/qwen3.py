@@ -482,13 +482,17 @@ class Qwen3Batch(Qwen3Decoder):
     src/runtime/scheduler/scheduler.py:70-178): one paged KV pool per layer,
     one block table per sequence, and steps that pass every sequence's rows
     as one M to the linears -- an MTP verify step of 16 sequences x (1 + 4
-    drafts) is one M = 80 call per linear.  The linears run on the bit-exact
-    kernels at every M (the matrix-core threshold is raised above the batch
-    for the step), so each sequence's logits are bit-identical to its own
-    per-sequence run, as the reference verifies each sequence by itself
-    (src/engine.py:416-459)."""
+    drafts) is one M = 80 call per linear.  With exact (the default) the
+    linears run on the bit-exact kernels at every M (the matrix-core
+    threshold is lowered to none for the step), so each sequence's logits
+    are bit-identical to its own per-sequence run, as the reference verifies
+    each sequence by itself (src/engine.py:416-459).  exact=False leaves the
+    library's threshold: batches of 64 rows or more go to the matrix cores
+    (outputs within their 1e-2 tolerance, not bit-identical; an argmax at a
+    near tie can then differ from the reference's)."""
 
-    def __init__(self, weights: Qwen3Weights, n_seqs: int, max_positions: int, max_rows: int = 96):
+    def __init__(self, weights: Qwen3Weights, n_seqs: int, max_positions: int, max_rows: int = 96,
+                 exact: bool = True):
         bs = weights.cfg.block_size
         per_seq = (max_positions + bs - 1) // bs
         super().__init__(weights, max_positions, max_new_tokens=1, max_rows=max_rows,
@@ -496,6 +500,7 @@ class Qwen3Batch(Qwen3Decoder):
         self.tables_all = torch.arange(n_seqs * per_seq, dtype=torch.int32, device=self.dev)
         self.tables = [self.tables_all[i * per_seq:(i + 1) * per_seq] for i in range(n_seqs)]
         self.cache_len = [0] * n_seqs
+        self.exact = exact
 
     def _run(self, groups_tokens, with_logits: bool):
         rows = sum(len(t) for _, t in groups_tokens)
@@ -510,6 +515,10 @@ class Qwen3Batch(Qwen3Decoder):
                 raise ValueError(f"sequence {seq} would exceed {self.max_pos} positions")
             groups.append((r0, len(toks), pos0, self.tables[seq], seq))
             r0 += len(toks)
+        if not self.exact:
+            self._bind()
+            self._forward(rows, with_logits, groups=groups)
+            return rows
         prev = abi.matrix_core_min_rows()
         abi.set_matrix_core_min_rows(0)          # 0: exact kernels at every M
         try:

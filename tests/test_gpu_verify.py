@@ -171,3 +171,32 @@ def test_batched_speculation_qwen3_1p7b_matches_oracle(dev):
         last = [o[1] for o in out]
     for i, q in enumerate(sv["sequences"]):
         assert b.cache_len[i] == len(fx["prompt"]) + len(q["emitted"]) - 1
+
+
+def test_batched_verify_matrix_cores_close_to_exact(dev):
+    """Qwen3Batch(exact=False): batches of 64 rows or more on the matrix cores.
+    On the two-layer model, 16 sequences x 5 rows after their prompts: every
+    verify row's logits within 5e-2 of the row's largest magnitude of the
+    exact mode's (two layers of 1e-2 GEMM tolerance, prefill included), and
+    the rows' argmax equal wherever the exact row's top two are apart by
+    more than that."""
+    from pilm_amd import qwen3 as Q
+    from pilm_amd import synth_model as SM
+    c = dict(_fixture("tiny")["config"])
+    n_seq = 16
+    prompts = [SM.token_ids(300 + i, 20 + 3 * i, c["vocab"]).tolist() for i in range(n_seq)]
+    w = Q.Qwen3Weights.synthetic(Q.Qwen3Config.from_dict(c), c["seed"], c["std"], device=dev)
+    rows = {}
+    for exact in (True, False):
+        _say(f"[gpu] batched verify, two-layer model, exact={exact}: prefill and one step, M = 80")
+        b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=max(len(p) for p in prompts) + 8, max_rows=96, exact=exact)
+        b.prefill_seqs(list(range(n_seq)), prompts)
+        b.verify([1 + i for i in range(n_seq)], [[7, 8, 9, 10]] * n_seq)
+        rows[exact] = b.logits_rows[:80].to(torch.float32).cpu()
+    a, m = rows[True], rows[False]
+    scale = a.abs().amax(dim=1)
+    err = ((a - m).abs().amax(dim=1) / scale).max().item()
+    assert err <= 5e-2, f"matrix-core verify rows differ by {err:.3g} of the row's largest logit"
+    top2 = a.topk(2, dim=1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 5e-2 * scale
+    assert torch.equal(a.argmax(dim=1)[clear], m.argmax(dim=1)[clear])
