@@ -809,8 +809,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
     float *qs = xn + (hpw + 1) * D;                            // [hpw][D] roped q
     float *sc = qs + hpw * D;                                  // [hpw][scs]
     float *part = sc + (size_t)hpw * scs;                      // [hpw][4][D] chain sums
-    float *cm = part + hpw * 4 * D;                            // [scs + 32] one row, chain-major
-    int *bids = (int *)(cm + scs + 32);                        // [n_block_ids]
+    // one row's exps / weights by chain (the one-pass path: <= nthreads positions)
+    constexpr int kC8 = (nthreads / 8 + 3) & ~3, kC4 = (nthreads / 4 + 3) & ~3;   // chain strides
+    float *cm = part + hpw * 4 * D;                            // [nthreads + 32]
+    int *bids = (int *)(cm + nthreads + 32);                   // [n_block_ids]
     uint16_t *vs = (uint16_t *)(bids + ((n_block_ids + 3) & ~3));   // [vcap][D]
 
     const int pos = step ? step[0] : pos0_host;
@@ -986,7 +988,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
         for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, red[w]);
         // the exps by sum chain (position j at cm[(j mod 8) c8 + j / 8]), then
         // the weights by P.V chain (cm[(j mod 4) c4 + j / 4]) besides sc[j]
-        const int c8 = ((scs + 7) / 8 + 3) & ~3, c4 = (scs / 4 + 3) & ~3;
+        constexpr int c8 = kC8, c4 = kC4;
         if (t < vis) {
             e = sleef_expf(e - mx);
             cm[(t & 7) * c8 + (t >> 3)] = e;
@@ -1120,7 +1122,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(
                 if (k == 0)
                     for (int j = 0; j < vis; ++j) fma_pos(sc[j], j);
             } else {
-                const float *wk = cm + k * ((scs / 4 + 3) & ~3);
+                const float *wk = cm + k * kC4;
                 const int im = max(0, (min(vis, main_len) - k + 3) / 4);   // positions k + 4 i
                 int i = 0;
                 for (; i + 8 <= im; i += 8) {
@@ -1645,8 +1647,8 @@ int ekernel_decode_attention_bf16(const ekernel_qk_rope_desc_t *desc, const uint
     // 796 -> 848 tok/s), or all rep q heads of the kv head sharing the key
     // rows' widening (PILM_DECODE_ATTN_SHARED=1)
     const size_t hpw = env_int("PILM_DECODE_ATTN_SHARED", 0) == 1 ? rep : 1;
-    const size_t fixed = ((hpw + 1) * D + hpw * D + (hpw + 1) * ((max_len + 3) & ~(size_t)3) + 32 + hpw * 4 * D +
-                          ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
+    const size_t fixed = ((hpw + 1) * D + hpw * D + hpw * ((max_len + 3) & ~(size_t)3) + kDecodeThreads + 32 +
+                          hpw * 4 * D + ((d.n_block_ids + 3) & ~(size_t)3)) * 4;
     const size_t budget = lds_limit();
     const size_t room = fixed < budget ? (budget - fixed) / (D * 2) : 0;
     const size_t vcap = std::min<size_t>(room / 64 * 64, (max_len + 63) / 64 * 64);

@@ -418,6 +418,43 @@ def test_decode_attention_fused(lib, dev, H, Hkv, D, pos0, shared, monkeypatch):
         assert len(bad) == 0, f"{len(bad)} outputs differ, first {bad[:4].tolist()} (step={use_step})"
 
 
+@pytest.mark.parametrize("pos0", [100, 511])
+def test_decode_attention_fused_long_table(lib, dev, pos0):
+    """A short row in block tables and rope tables sized for 32768 positions
+    (the decoder sized for long sequences): accepted, with the oracle's
+    output and cache rows, as in a table sized to fit."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(pos0 + 77)
+    H, Hkv, D, bs, cap = 16, 8, 128, 16, 32768
+    L, block_ids, kc, vc, qkv, qw, kw = _attn_case(rng, 1, H, Hkv, D, pos0, bs)
+    ids_long = np.concatenate([block_ids, np.zeros(cap // bs - len(block_ids), np.int32)])
+    cos, sin = OD.rope_tables(1e6, D, cap)
+    stride = qkv.shape[1]
+    qg, k, v = qkv[:, :2 * H * D], qkv[:, 2 * H * D:2 * H * D + Hkv * D], qkv[:, 2 * H * D + Hkv * D:]
+    kc_o, vc_o = kc.copy(), vc.copy()
+    q_want = OD.qk_norm_rope_bf16(qg, k, v, qw, kw, cos, sin, pos0, kc_o, vc_o, block_ids, n_heads=H, n_kv_heads=Hkv,
+                                  head_dim=D, rot_dim=D, eps=1e-6, block_size=bs)
+    want = OD.attention_exact_bf16(q_want, kc_o, vc_o, block_ids, L, qkv.reshape(-1)[D:], stride, 2 * D,
+                                   block_size=bs)
+    qkv_d, kc_d, vc_d = _dev16(qkv, dev), _dev16(kc, dev), _dev16(vc, dev)
+    bid_d = torch.from_numpy(ids_long).to(dev)
+    cos_d, sin_d = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    qw_d, kw_d = _dev16(qw, dev), _dev16(kw, dev)
+    out_d = torch.zeros((1, H * D), dtype=torch.bfloat16, device=dev)
+    _say(f"[gpu] fused decode attention, {cap}-position tables, pos0={pos0}")
+    _bind()
+    p = qkv_d.data_ptr()
+    rd = abi.EkernelQkRopeDesc(1, H, Hkv, D, D, stride, stride, pos0, cap, bs, kc.shape[0], len(ids_long), 1e-6)
+    rc = lib.ekernel_decode_attention_bf16(ctypes.byref(rd), ctypes.c_void_p(p), ctypes.c_void_p(p + 2 * H * D * 2),
+                                           ctypes.c_void_p(p + (2 * H * D + Hkv * D) * 2), _vp(qw_d), _vp(kw_d),
+                                           _vp(cos_d), _vp(sin_d), None, _vp(kc_d), _vp(vc_d), _vp(bid_d),
+                                           _vp(out_d))
+    assert rc == 0, abi.last_error()
+    assert np.array_equal(_bits(kc_d), kc_o) and np.array_equal(_bits(vc_d), vc_o)
+    assert np.array_equal(_bits(out_d), want)
+
+
 def test_decode_attention_fused_refuses_unsupported(lib, dev):
     """Other than 1, 2 or 4 q heads per kv head, 256-wide heads and S > 1 are
     refused (the two-call path serves them)."""
