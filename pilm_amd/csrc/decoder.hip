@@ -1485,6 +1485,8 @@ int ekernel_qk_norm_rope_batch_bf16(const ekernel_qk_rope_desc_t *desc, const ek
     return check_launch(fn);
 }
 
+static size_t lds_limit();
+
 int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *desc, const ekernel_batch_seq_t *seqs,
                                        size_t n_seqs, size_t n_tables, const uint16_t *q, const uint16_t *k_cache,
                                        const uint16_t *v_cache, const int32_t *block_ids, const uint16_t *gate,
@@ -1515,7 +1517,7 @@ int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *des
     if ((D == 64 || D == 128) && rep <= (size_t)kTileVecs && env_int("PILM_HIP_ATTN_TILE", 1) != 0) {
         // tiles of at most rt rows per sequence: the most rows per tile that
         // still give 256 workgroups (else one row per tile), fewer if the
-        // scores do not fit the LDS budget
+        // scores do not fit the workgroup's LDS
         int longest = 1, most = 1;
         for (size_t i = 0; i < n_seqs; ++i) {
             longest = std::max(longest, seqs[i].pos0 + seqs[i].rows);
@@ -1534,7 +1536,7 @@ int ekernel_attention_exact_batch_bf16(const ekernel_attention_exact_desc_t *des
                 }
             }
         }
-        const size_t scs = ((size_t)longest + 3) & ~(size_t)3, budget = 64 * 1024;
+        const size_t scs = ((size_t)longest + 3) & ~(size_t)3, budget = lds_limit();
         for (rt = std::min(rt, rt_max); rt >= 1; --rt) {
             BatchTiles bt;
             int n_tiles = 0, widest = 0;

@@ -333,6 +333,44 @@ def test_rope_attention_batch_matches_per_sequence(lib, dev, monkeypatch, H, Hkv
         assert len(bad) == 0, f"{len(bad)} outputs differ (tile {tile}/{tile_rows}), first {bad[:4].tolist()}"
 
 
+def test_attention_batch_long_sequence(lib, dev):
+    """A sequence of 8002 positions beside a short one in one batched
+    attention call (the scores of a row no longer fit 64 KB: the tile kernel
+    takes the workgroup's whole LDS); outputs equal to the oracle's."""
+    import ctypes
+    from pilm_amd import bindings as abi
+    rng = np.random.default_rng(8000)
+    H, Hkv, D, bs = 16, 8, 128, 16
+    plan = [(2, 8000), (5, 100)]
+    per = max((p + n + bs - 1) // bs for n, p in plan)
+    nseq = len(plan)
+    nphys = nseq * per
+    tables = rng.permutation(nphys).astype(np.int32).reshape(nseq, per)
+    kc, vc = _rand16(rng, (nphys, bs, Hkv, D)), _rand16(rng, (nphys, bs, Hkv, D))
+    rows = sum(n for n, _ in plan)
+    width = (2 * H + 2 * Hkv) * D
+    qkv = _rand16(rng, (rows, width))
+    q = _rand16(rng, (rows, H, D))
+    want = np.zeros((rows, H * D), np.uint16)
+    r0 = 0
+    for i, (n, p0) in enumerate(plan):
+        want[r0:r0 + n] = OD.attention_exact_bf16(q[r0:r0 + n], kc, vc, tables[i], p0 + n,
+                                                  qkv[r0:r0 + n].reshape(-1)[D:], width, 2 * D,
+                                                  block_size=bs).reshape(n, H * D)
+        r0 += n
+    q_d, kc_d, vc_d, qkv_d = _dev16(q, dev), _dev16(kc, dev), _dev16(vc, dev), _dev16(qkv, dev)
+    tab_d = torch.from_numpy(tables.reshape(-1).copy()).to(dev)
+    out_d = torch.zeros((rows, H * D), dtype=torch.bfloat16, device=dev)
+    seqs = (abi.EkernelBatchSeq * nseq)(abi.EkernelBatchSeq(0, 2, 8000, 0), abi.EkernelBatchSeq(2, 5, 100, 1))
+    _say("[gpu] batched attention, 8002 and 105 positions")
+    _bind()
+    ad = abi.EkernelAttentionExactDesc(rows, H, Hkv, D, 0, bs, nphys, per, width, 2 * D)
+    rc = lib.ekernel_attention_exact_batch_bf16(ctypes.byref(ad), seqs, nseq, nseq, _vp(q_d), _vp(kc_d), _vp(vc_d),
+                                                _vp(tab_d), ctypes.c_void_p(qkv_d.data_ptr() + D * 2), _vp(out_d))
+    assert rc == 0, abi.last_error()
+    assert np.array_equal(_bits(out_d), want)
+
+
 def test_rope_attention_batch_rejects_bad_tables(lib, dev):
     """Rows in two sequences or in none, a table index beyond n_tables,
     positions beyond the tables and more than 128 rows are refused before
