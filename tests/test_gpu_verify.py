@@ -200,3 +200,49 @@ def test_batched_verify_matrix_cores_close_to_exact(dev):
     top2 = a.topk(2, dim=1).values
     clear = (top2[:, 0] - top2[:, 1]) > 5e-2 * scale
     assert torch.equal(a.argmax(dim=1)[clear], m.argmax(dim=1)[clear])
+
+
+def test_w8_8b_shapes_decode_and_verify_match_oracle(dev):
+    """Two layers with Qwen3-8B's shapes (hidden 4096, 32 q / 8 kv heads,
+    intermediate 12288; a 4096-token vocabulary keeps the oracle fast) and
+    int8 per-row weights, the MTP configuration's format: the greedy tokens
+    and every step's logits of one sequence, then one batched verify step of
+    4 sequences x 5 rows, bit for bit against the oracle run per sequence."""
+    from pilm_amd import qwen3 as Q
+    from pilm_amd import synth_model as SM
+    c = {"layers": 2, "hidden": 4096, "heads": 32, "kv_heads": 8, "head_dim": 128, "intermediate": 12288,
+         "vocab": 4096, "eps": 1e-6, "rope_theta": 1e6, "partial_rotary": 1.0, "block_size": 16, "group_size": 128,
+         "std": 0.02, "seed": 23, "weights": "w8", "prompt": 20, "new_tokens": 6}
+    prompt = SM.token_ids(51, c["prompt"], c["vocab"]).tolist()
+    _say("[gpu] 8B-shaped W8 model: oracle weights and greedy decode (CPU)")
+    od = OD.OracleDecoder(c)
+    want_sha = []
+    want = od.generate(prompt, c["new_tokens"], on_logits=lambda i, lg: want_sha.append(OD.sha_u16(lg)))
+    _say("[gpu] 8B-shaped W8 model: device weights and decode")
+    w = Q.Qwen3Weights.synthetic(Q.Qwen3Config.from_dict(c), c["seed"], c["std"], device=dev, hashes=True)
+    assert w.quantized_sha == od.qsha
+    dec = Q.Qwen3Decoder(w, max_positions=c["prompt"] + c["new_tokens"] + 1, max_new_tokens=c["new_tokens"])
+    shas = []
+    toks = dec.generate(prompt, c["new_tokens"], on_logits=lambda i, lg: shas.append(OD.sha_u16(_bits(lg))))
+    first = next((i for i, (a, b) in enumerate(zip(shas, want_sha)) if a != b), None)
+    assert first is None, f"logits differ first at step {first}"
+    assert toks == want
+
+    n_seq = 4
+    prompts = [SM.token_ids(60 + i, 5 + 3 * i, c["vocab"]).tolist() for i in range(n_seq)]
+    drafts = [[(7 * i + j) % c["vocab"] for j in range(4)] for i in range(n_seq)]
+    _say("[gpu] 8B-shaped W8 model: oracle verify rows per sequence (CPU)")
+    want_rows, last = [], []
+    for i in range(n_seq):          # the oracle's cache is rewritten from position 0 for each sequence
+        g = od.generate(prompts[i], 1)
+        last.append(g[0])
+        want_rows.append(od.forward([g[0]] + drafts[i], len(prompts[i]), all_rows=True))
+    _say("[gpu] 8B-shaped W8 model: batched prefill and one verify step, M = 20")
+    b = Q.Qwen3Batch(w, n_seqs=n_seq, max_positions=max(len(p) for p in prompts) + 9, max_rows=32)
+    assert b.prefill_seqs(list(range(n_seq)), prompts) == last
+    b.verify(last, drafts)
+    r0 = 0
+    for i in range(n_seq):
+        got = _bits(b.logits_rows[r0:r0 + 5])
+        assert np.array_equal(got, want_rows[i]), f"sequence {i}: verify rows differ from the oracle"
+        r0 += 5
