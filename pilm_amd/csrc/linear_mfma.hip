@@ -29,6 +29,11 @@
 //
 // A small pre-pass converts the activations once into that fp16 layout (two
 // planes, hi and lo, for fp32 activations) in a per-device scratch buffer.
+// W8A16 skips it (BF): v_mfma_f32_32x32x16_bf16 takes the bf16 activations
+// as they are, in natural k order, and each int8 weight becomes the bf16 of
+// its value (exact: |w| <= 128 has at most 8 significant bits) by one
+// sign-extending byte conversion to fp32, two of which one v_perm packs;
+// products stay exact and the per-row scale is applied in fp32 at the end.
 // Tiling: a workgroup of four waves computes BM x BN outputs (waves WM x WN,
 // each (BM/WM) x (BN/WN) in 32 x 32 MFMA tiles) over K in steps of 64, with a
 // double-buffered LDS stage filled by global -> LDS DMA (activation blocks
@@ -51,6 +56,7 @@ namespace pilm {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 64;           // K per stage
@@ -90,6 +96,14 @@ __device__ __forceinline__ u32x4 act_block(const float (&v)[8]) {
         o[3] = f16x2_of_f32(v[3], v[7]);
     }
     return o;
+}
+
+// Bytes lo and lo + 1 of u (int8) as a bf16 pair, byte lo in the low half:
+// the fp32 of a small integer is exact and its upper 16 bits are its bf16.
+__device__ __forceinline__ uint32_t bf16x2_of_i8(uint32_t u, int lo) {
+    const float f0 = (float)((int)(u << (24 - 8 * lo)) >> 24);
+    const float f1 = (float)((int)(u << (16 - 8 * lo)) >> 24);
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
 }
 
 // fp32 activations: v = hi + lo with hi = fp16(v) (round to nearest) and
@@ -212,7 +226,8 @@ __global__ __launch_bounds__(256) void act_prep_kernel(const void *__restrict__ 
 // (scale x weight then stays within fp16 and off its subnormals); a
 // workgroup finds it from the scales of its own K range, which changes
 // nothing but that exact power of two, taken out again in the epilogue.
-// X: the activations prepared by act_prep_kernel (fp16, planes x M x K).
+// X: the activations prepared by act_prep_kernel (fp16, planes x M x K), or
+// with BF (W8A16 only) the caller's bf16 activations [M, K] and E unused.
 template <int FMT, int BM, int BN, int WM>
 constexpr int mfma_stage_bytes() {
     using F = MF<FMT>;
@@ -226,13 +241,14 @@ constexpr int mfma_min_blocks() {
     return 4 * mfma_stage_bytes<FMT, BM, BN, WM>() <= 160 * 1024 ? 2 : 1;
 }
 
-template <int FMT, int BM, int BN, int WM>
+template <int FMT, int BM, int BN, int WM, bool BF>
 __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>())) void gemm_mfma_kernel(const _Float16 *__restrict__ X,
                                                                 const uint8_t *__restrict__ W,
                                                                 const float *__restrict__ S, void *__restrict__ C,
                                                                 float *__restrict__ P, const int *__restrict__ E,
                                                                 int M, int N, int K, int steps_per_split) {
     using F = MF<FMT>;
+    static_assert(!BF || FMT == F_W8A16, "bf16 operands: int8 weights with bf16 activations");
     constexpr int WN = 4 / WM;
     constexpr int TM = BM / WM / 32;     // 32x32 tiles per wave along M
     constexpr int TN = BN / WN / 32;     // ... along N
@@ -401,7 +417,13 @@ __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>()))
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 u32x4 q;
-                if constexpr (F::w8) {
+                if constexpr (BF) {   // natural order: (0,1) (2,3) (4,5) (6,7)
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        q[2 * d] = bf16x2_of_i8(wraw[slot][j][d], 0);
+                        q[2 * d + 1] = bf16x2_of_i8(wraw[slot][j][d], 2);
+                    }
+                } else if constexpr (F::w8) {
                     const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
                     for (int d = 0; d < 2; ++d) {
@@ -429,8 +451,15 @@ __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>()))
 #pragma unroll
                 for (int pl = 0; pl < F::planes; ++pl)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[slot][i][pl], bfr[j], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < TN; ++j) {
+                        if constexpr (BF)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(bf16x8, afr[slot][i][pl]), __builtin_bit_cast(bf16x8, bfr[j]),
+                                acc[i][j], 0, 0, 0);
+                        else
+                            acc[i][j] =
+                                __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[slot][i][pl], bfr[j], acc[i][j], 0, 0, 0);
+                    }
         }
         wait_vmcnt<0>();               // stage t + 1 has landed
         __syncthreads();               // ... and stage t's buffer is free for stage t + 2
@@ -454,7 +483,7 @@ __global__ __launch_bounds__(kMfmaThreads, (mfma_min_blocks<FMT, BM, BN, WM>()))
                     pz[(size_t)m * N + n] = ldexpf(acc[i][j][e], -wexp[j]);
                     continue;
                 }
-                const float y = ldexpf(acc[i][j][e], -(E[m] + wexp[j])) * sc;
+                const float y = ldexpf(acc[i][j][e], -((BF ? 0 : E[m]) + wexp[j])) * sc;
                 if constexpr (F::a32)
                     ((float *)C)[(size_t)m * N + n] = y;
                 else
@@ -476,7 +505,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
     float y = 0.0f;
     for (int z = 0; z < splits; ++z) y += P[(size_t)z * total + idx];
     const int m = (int)(idx / N), n = (int)(idx % N);
-    y = ldexpf(y, -E[m]);
+    if (E) y = ldexpf(y, -E[m]);   // null: activations taken unscaled (BF)
     if constexpr (F::group == 0) y *= S[n];
     if constexpr (F::a32)
         ((float *)C)[idx] = y;
@@ -484,12 +513,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
         ((uint16_t *)C)[idx] = f32_to_bf16(y);
 }
 
-template <int FMT, int BM, int BN, int WM>
+template <int FMT, int BM, int BN, int WM, bool BF = false>
 void launch_mfma(hipStream_t st, const _Float16 *X, const uint8_t *W, const float *S, void *C, float *P,
                  const int *E, int splits, int sps, int M, int N, int K) {
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
-    gemm_mfma_kernel<FMT, BM, BN, WM><<<grid, kMfmaThreads, 0, st>>>(X, W, S, C, splits > 1 ? P : nullptr, E, M, N,
-                                                                     K, sps);
+    gemm_mfma_kernel<FMT, BM, BN, WM, BF><<<grid, kMfmaThreads, 0, st>>>(X, W, S, C, splits > 1 ? P : nullptr, E, M,
+                                                                         N, K, sps);
     if (splits > 1) {
         const size_t total = (size_t)M * N;
         split_reduce_kernel<FMT><<<(unsigned)((total + 255) / 256), 256, 0, st>>>(P, S, C, E, M, N, splits);
@@ -520,6 +549,24 @@ void launch_mfma_fmt(int bm, hipStream_t st, const void *A, const _Float16 *X, i
     else
         wm == 1 ? launch_mfma<FMT, 64, 128, 1>(st, X, W, S, C, P, E, splits, sps, M, N, K)
                 : launch_mfma<FMT, 64, 128, 2>(st, X, W, S, C, P, E, splits, sps, M, N, K);
+}
+
+// W8A16 on bf16 MFMAs: no activation pass, the kernel reads A directly.
+void launch_mfma_bf16(int bm, hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, float *P,
+                      int splits, int sps, int M, int N, int K) {
+    const _Float16 *X = (const _Float16 *)A;   // bf16 [M, K]; only copied by byte
+    int wm = 2;
+    const int env_wm = env_int("PILM_HIP_MFMA_WM", 0);
+    if (env_wm == 1 || env_wm == 2) wm = env_wm;
+    if (bm == 256)
+        wm == 1 ? launch_mfma<F_W8A16, 256, 128, 1, true>(st, X, W, S, C, P, nullptr, splits, sps, M, N, K)
+                : launch_mfma<F_W8A16, 256, 128, 2, true>(st, X, W, S, C, P, nullptr, splits, sps, M, N, K);
+    else if (bm == 128)
+        wm == 1 ? launch_mfma<F_W8A16, 128, 128, 1, true>(st, X, W, S, C, P, nullptr, splits, sps, M, N, K)
+                : launch_mfma<F_W8A16, 128, 128, 2, true>(st, X, W, S, C, P, nullptr, splits, sps, M, N, K);
+    else
+        wm == 1 ? launch_mfma<F_W8A16, 64, 128, 1, true>(st, X, W, S, C, P, nullptr, splits, sps, M, N, K)
+                : launch_mfma<F_W8A16, 64, 128, 2, true>(st, X, W, S, C, P, nullptr, splits, sps, M, N, K);
 }
 
 }  // namespace
@@ -574,6 +621,12 @@ int run_mfma(int fmt, size_t M, size_t N, size_t K, const void *A, const uint8_t
         int *T = nullptr;
         const int rc = split_scratch(st, (size_t)splits * M * N, 1, &P, &T, fn);
         if (rc != ECPU_OK) return rc;
+    }
+    // W8A16 runs on bf16 MFMAs straight from the caller's activations
+    // (PILM_HIP_MFMA_BF16=0: the fp16 path with its activation pass)
+    if (fmt == F_W8A16 && env_int("PILM_HIP_MFMA_BF16", 1) != 0) {
+        launch_mfma_bf16(bm, st, A, W, S, C, P, splits, sps, (int)M, (int)N, (int)K);
+        return ECPU_OK;
     }
     // activation planes, then the activation-row exponents
     void *X = nullptr;

@@ -82,6 +82,30 @@ def test_mfma_config3_shape(fmt, dev):
     check_close(fmt, y, ref, f"{fmt} config3")
 
 
+@pytest.mark.parametrize("shape", SHAPES + [(256, 2048, 4096)], ids=lambda s: "x".join(map(str, s)))
+def test_mfma_w8a16_both_operand_types(shape, dev, monkeypatch):
+    """W8A16 runs on bf16 MFMAs by default (the bf16 activations as they are,
+    each int8 weight converted exactly) and on fp16 MFMAs after the
+    activation pass with PILM_HIP_MFMA_BF16=0.  Either way every product is
+    exact and only the fp32 order of the sums differs from the reference, so
+    each output lies within one bf16 rounding step of the oracle's
+    (2^-7 |ref| covers a step on either side) except where the row's sums
+    cancel (1e-3 of the row's largest output)."""
+    m, n, k = shape
+    gen = GV._gen()
+    x, w, s = gen.make_inputs("w8a16", m, n, k, 515 + m + n + k)
+    ref = gen.run("w8a16", x, w, s, "oracle")
+    rf = as_f32("w8a16", ref)
+    for bf16 in ("1", "0"):
+        monkeypatch.setenv("PILM_HIP_MFMA_BF16", bf16)
+        _say(f"[gpu] mfma w8a16 bf16={bf16} M={m} N={n} K={k}")
+        y = run_gpu("w8a16", x, w, s, dev)
+        check_close("w8a16", y, ref, f"w8a16 bf16={bf16} {shape}")
+        err = np.abs(as_f32("w8a16", y) - rf)
+        bound = 2.0 ** -7 * np.abs(rf) + 1e-3 * np.abs(rf).max(axis=1, keepdims=True)
+        assert (err <= bound).all(), f"bf16={bf16}: {(err > bound).sum()} outputs beyond one bf16 step"
+
+
 @pytest.mark.parametrize("fmt", ["w8a16", "w4g128"])
 def test_below_threshold_stays_exact(fmt, dev, monkeypatch):
     """M below the threshold, or the threshold disabled, keeps the exact kernels."""
