@@ -346,7 +346,7 @@ def sweep(torch, dev, sections) -> dict:
       w4row  per-row W4A16 (bundle v2) at the 1.7B shapes, M = 1, 4, 16
       w8a32  W8A32: 4096x4096 (the single-GEMV configuration) and the 8B shapes, M = 1
       w8a16  W8A16 at the 8B shapes, M = 1 and 5 (MTP verify of one sequence)
-      gemm   prefill / verify at the 8B shapes, W8A32 and W4A16 g128,
+      gemm   prefill / verify at the 8B shapes, W8A32, W8A16 and W4A16 g128,
              M = 64, 256, 1024, 2048 (matrix cores; TFLOP/s)
       fused  W4 SwiGLU MLP and W8A16 lm_head argmax vs their unfused calls
       attention  paged attention of one sequence (decode and MTP verify) at
@@ -374,7 +374,7 @@ def sweep(torch, dev, sections) -> dict:
         gm = (64, 256, 1024, 2048)
         res["gemm_8b"] = {f"{fmt}_{name}": {"N": n, "K": k, **time_linear(torch, dev, fmt, n, k, gm, reps=5,
                                                                          min_bytes=256 << 20)}
-                          for fmt in ("w8a32", "w4g128") for name, n, k in SHAPES_8B if name != "lm_head"}
+                          for fmt in ("w8a32", "w8a16", "w4g128") for name, n, k in SHAPES_8B if name != "lm_head"}
     if "gemm_fp16" in sections:
         res["gemm_fp16_8b"] = sweep_gemm_fp16(torch, dev, (64, 256, 1024, 2048))
     if "fused" in sections:
