@@ -1358,8 +1358,11 @@ int launch_w8b_one(hipStream_t st, const void *A, const uint8_t *W, const float 
 template <int FMT>
 int launch_w8b(hipStream_t st, const void *A, const uint8_t *W, const float *S, void *C, int N, int K) {
     // 8-row tiles up to 1024 rows (k/v: 1024x4096 W8A16 9.6 -> 8.9 us; the
-    // repeated lanes cost more than the extra CUs gain beyond), 16 below 8192.
-    int rows = N <= 1024 ? 8 : (N < 8192 ? 16 : 32);
+    // repeated lanes cost more than the extra CUs gain beyond), 16 below 8192
+    // -- for W8A16 below 4096 only (interleaved same-process A/B, 16 vs 32
+    // rows: W8A16 4096x12288 26.9 vs 25.0 us, 4096x4096 10.1 vs 9.8 us;
+    // W8A32 23.9 vs 25.5 us, 9.6 vs 10.0 us).
+    int rows = N <= 1024 ? 8 : (N < (FMT == F_W8A16 ? 4096 : 8192) ? 16 : 32);
     const int env_rows = env_int("PILM_HIP_W8B_ROWS", 0);
     if (env_rows == 8 || env_rows == 16 || env_rows == 32) rows = env_rows;
     // (a 32-slot ring measured slower at every shape: 4096x4096 11.2 vs 9.8 us)
